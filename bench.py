@@ -1,0 +1,229 @@
+"""Benchmark of the ragged paged-attention hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--kv bf16|f32]
+                    [--workload config2|target|config3] [--no-cpu-baseline]
+
+A step is one decode pass of the hot path over one ragged batch, for every
+layer of the model: the packed step metadata is uploaded once (one async
+copy), then per layer the new K/V rows are scattered into that layer's paged
+cache and ragged paged attention runs over the batch. Each layer has its own
+KV pool, so a step touches 24 distinct caches (>> the 256 MB Infinity Cache).
+
+Workloads (Qwen2.5-0.5B GQA: 14 q heads, 2 kv heads, head_dim 64, block 16):
+  config2  64 seqs, context log-uniform in [64, 4096], tables from a
+           32768-block pool -- the default
+  target   64 seqs x 4096 context (the >= 60 % of HBM peak target point)
+  config3  32 decode rows + 2 prefill chunks of 512 (MFMA chunk rows)
+
+Prints ONE JSON line. `value` is algorithmic HBM bytes per step / step time:
+K/V of each kv head once (the GQA-shared minimum), q, out, block tables and
+per-row metadata, plus the K/V rows written by the scatter.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+for p in (ROOT / "llm-engine_amd", ROOT / "tests", ROOT / "oracle"):
+    sys.path.insert(0, str(p))
+
+METRIC = "ragged paged-attn HBM GB/s (% of peak); decode tok/s at 64 seqs, 1 GPU"
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+Q_HEADS, KV_HEADS, HEAD_DIM, BS = 14, 2, 64, 16
+LAYERS = 24
+
+
+def workload_shape(name: str):
+    rng = np.random.default_rng(2)
+    if name == "config2":
+        from cases import loguniform_ctx
+        ctx = loguniform_ctx(rng, 64, 64, 4096)
+        return ctx, np.ones(64, dtype=np.int64), 32768
+    if name == "target":
+        return np.full(64, 4096, dtype=np.int64), np.ones(64, dtype=np.int64), 32768
+    if name == "config3":
+        dec = np.random.default_rng(3).integers(256, 2049, size=32)
+        ctx = np.array([512, 1536] + list(dec), dtype=np.int64)
+        return ctx, np.array([512, 512] + [1] * 32, dtype=np.int64), 16384
+    raise SystemExit(f"unknown workload {name}")
+
+
+def algorithmic_bytes(ctx, q_len, kv_size, act_size):
+    """HBM bytes one layer of the step must move at minimum."""
+    n = int(q_len.sum())
+    kv = int(ctx.sum()) * KV_HEADS * HEAD_DIM * 2 * kv_size          # K and V, once per kv head
+    qo = n * Q_HEADS * HEAD_DIM * act_size * 2                         # q in, out
+    tables = int(((ctx + BS - 1) // BS).sum()) * 4
+    meta = n * 4 * 2 + len(ctx) * 4                                    # token pos/seq, table offsets
+    attn = kv + qo + tables + meta
+    write = n * KV_HEADS * HEAD_DIM * 2 * (act_size + kv_size) + n * 4  # scatter: read rows, write cache
+    return attn, write
+
+
+def chunk_flops(ctx, q_len):
+    f = 0
+    for c, ql in zip(ctx, q_len):
+        if ql > 1:
+            keys = np.arange(c - ql, c) + 1
+            f += int(keys.sum())
+    return 4 * Q_HEADS * HEAD_DIM * f
+
+
+def cpu_baseline(ctx, q_len, kv_bf16: bool, budget_s: float):
+    """The oracle's (token, head) loop (cpu_model.cpp:160-185) on the host
+    cores, on one layer of the same batch, repeated until budget_s elapses."""
+    import oracle
+    from cases import make_case
+    case = make_case(ctx, q_len=q_len, num_blocks=int(((ctx + BS - 1) // BS).sum()) + 64,
+                     seed=21, kv_bf16=kv_bf16)
+    threads = oracle.threads_default()
+    attn_bytes, _ = algorithmic_bytes(ctx, q_len, 2 if kv_bf16 else 4, 4)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.paged_attention(case.q, case.k_cache, case.v_cache, case.tables, case.table_offset,
+                               case.token_seq, case.token_pos, Q_HEADS, KV_HEADS, HEAD_DIM, BS,
+                               case.scale, threads=threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    return {"value": round(attn_bytes * reps / el / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{reps} layer(s) of the same batch (one layer's attention, "
+                      f"{'bf16' if kv_bf16 else 'fp32'} K/V), {el:.1f} s, oracle.c "
+                      f"(token, head) loop on {threads} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--kv", choices=["bf16", "f32"], default="bf16")
+    ap.add_argument("--workload", choices=["config2", "target", "config3"], default="config2")
+    ap.add_argument("--layers", type=int, default=LAYERS)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--partition", type=int, default=0, help="decode partition tokens (0 = planner's choice)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build runs on one GPU only (the decode path shards by "
+              "sequence with no exchange; multi-GPU runs are not part of it).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from llm_engine_amd import kernels
+    from gpu_util import slices_of
+    from cases import make_case
+
+    dev = torch.device("cuda:0")
+    kv_dt = torch.bfloat16 if args.kv == "bf16" else torch.float32
+    act_dt = torch.float32
+    ctx, q_len, pool = workload_shape(args.workload)
+    case = make_case(ctx, q_len=q_len, num_blocks=pool, seed=2, fill="none")  # tables and rows only
+    kv_dim = KV_HEADS * HEAD_DIM
+    n = int(q_len.sum())
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    L = args.layers
+    kc = [torch.randn(pool * BS, kv_dim, device=dev, generator=g).to(kv_dt) for _ in range(L)]
+    vc = [torch.randn(pool * BS, kv_dim, device=dev, generator=g).to(kv_dt) for _ in range(L)]
+    qs = [torch.randn(n, Q_HEADS * HEAD_DIM, device=dev, generator=g).to(act_dt) for _ in range(L)]
+    knew = [torch.randn(n, kv_dim, device=dev, generator=g).to(act_dt) for _ in range(L)]
+    vnew = [torch.randn(n, kv_dim, device=dev, generator=g).to(act_dt) for _ in range(L)]
+    outs = [torch.empty_like(qs[0]) for _ in range(L)]
+
+    t0 = time.perf_counter()
+    plan = kernels.Plan(slices_of(case), Q_HEADS, KV_HEADS, HEAD_DIM, BS, kv_dt,
+                        partition_tokens=args.partition)
+    pack_us = (time.perf_counter() - t0) * 1e6
+    plan.upload()
+    torch.cuda.synchronize()
+    slots = plan.dev_array("slots")
+    ws = kernels.new_workspace(plan.workspace_size(), dev)
+    stream = torch.cuda.current_stream()
+
+    def attn(l):
+        kernels.ragged_paged_attention(qs[l], kc[l], vc[l], plan, case.scale, out=outs[l],
+                                       workspace=ws, stream=stream)
+
+    def step():
+        plan.upload(stream)
+        for l in range(L):
+            kernels.store_kv(knew[l], vnew[l], slots, kc[l], vc[l], stream=stream)
+            attn(l)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(args.steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+
+    kv_size = 2 if kv_dt == torch.bfloat16 else 4
+    attn_b, write_b = algorithmic_bytes(ctx, q_len, kv_size, 4)
+    step_bytes = L * (attn_b + write_b)
+    value = step_bytes / (ms * 1e-3) / 1e9
+
+    # Dominant kernel alone: the attention call per layer, back to back, timed
+    # with events on the stream it is launched on.
+    reps = max(4, args.steps // 2)
+    a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a0.record(stream)
+    for _ in range(reps):
+        for l in range(L):
+            attn(l)
+    a1.record(stream)
+    torch.cuda.synchronize()
+    attn_us = a0.elapsed_time(a1) * 1e3 / (reps * L)
+    achieved = attn_b / (attn_us * 1e-6) / 1e9
+    P = plan.plan
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "le_ragged_paged_attention (decode_kernel"
+                          + (" + chunk_kernel" if P.n_chunk_items else "")
+                          + (" + combine_kernel" if P.n_combine_items else "") + ")",
+                "bytes_per_launch": attn_b, "us_per_launch": round(attn_us, 3)}
+    if args.workload == "config3":
+        fl = chunk_flops(ctx, q_len)
+        roofline["chunk_flops_per_launch"] = fl
+
+    res = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": args.kv, "data": "synthetic",
+        "config": {"workload": f"{args.workload}: {len(ctx)} seqs, {n} rows, ctx "
+                               f"{'log-uniform [64,4096]' if args.workload == 'config2' else 'see bench.py'}"
+                               f", Qwen2.5-0.5B GQA 14/2 x 64, block 16, pool {pool} blocks,"
+                               f" {L} layers per step (own KV pool each)",
+                   "kv_dtype": args.kv, "act_dtype": "f32", "layers": L,
+                   "parallelism": "none (1 GPU)"},
+        "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "decode_rows_per_s": round(n / (ms * 1e-3), 1),
+        "plan": {"rows": P.n_tokens, "decode_items": P.n_decode_items, "chunk_items": P.n_chunk_items,
+                 "combine_items": P.n_combine_items, "bytes": int(P.bytes), "pack_us": round(pack_us, 1)},
+        "roofline": roofline,
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = cpu_baseline(ctx, q_len, kv_dt == torch.bfloat16, args.cpu_budget)
+    else:
+        res["cpu_baseline"] = None
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,169 @@
+/*
+ * llm-engine on MI355X: C ABI of the ragged continuous-batching hot path.
+ *
+ * This header replaces the CUDA launcher boundary of the reference engine,
+ * include/engine/cuda_kernels.h:17-64 (namespace engine, guarded by
+ * ENGINE_CUDA). Every entry point here is plain C: raw device pointers, sizes,
+ * a dtype tag and a hipStream_t. Nothing allocates device memory; scratch comes
+ * in through an explicit workspace argument whose size a *_workspace_size call
+ * reports. Exceptions never cross this boundary.
+ *
+ * Return value of every int-returning call:
+ *     0            LE_OK
+ *     < 0          a LE_E* code: bad shape or argument, nothing was launched
+ *     > 0          a hipError_t from the launch (hipGetLastError)
+ * The reference launchers return void and throw std::runtime_error on bad
+ * shapes (attention_decode_gqa.cu:211-224); the C++ engine in this repository
+ * turns a non-zero status back into that exception.
+ *
+ * Layouts (identical to the reference, cuda_model.cu:276-285 and
+ * kv_cache.h:21-32):
+ *   K and V cache, per layer:  [num_blocks * block_size][kv_heads][head_dim]
+ *   slot(pos)               =  block_table[pos / block_size] * block_size
+ *                              + pos % block_size
+ *   q, out                  :  [n_tokens][q_heads][head_dim], row-contiguous
+ *   new k, v rows           :  [n_tokens][kv_heads * head_dim]
+ * Element types: LE_F32 (float) or LE_BF16 (raw bf16 bits, uint16).
+ */
+#ifndef LLM_ENGINE_AMD_H
+#define LLM_ENGINE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LE_OK 0
+#define LE_EINVAL (-1)       /* a pointer, size or shape is invalid */
+#define LE_EUNSUPPORTED (-2) /* valid, but outside what the kernels are built for */
+#define LE_ENOSPACE (-3)     /* a caller buffer (host plan buffer, workspace) is too small */
+
+typedef enum le_dtype { LE_F32 = 0, LE_BF16 = 1 } le_dtype;
+
+/* Library version and build identification (for logs). */
+const char* le_version(void);
+/* Human-readable name of a status code. */
+const char* le_status_string(int status);
+
+/* ------------------------------------------------------------------------
+ * (2) K/V cache-write scatter.
+ * Replaces launch_store_kv (cuda_kernels.h:43-45, store_kv.cu:20-36):
+ *     k_cache[slot_mapping[t]][j] = k[t][j],  v likewise,  j < kv_dim.
+ * src and cache dtypes may differ (fp32 rows into a bf16 cache round to
+ * nearest even). A negative slot skips the token (padding). Slots at or
+ * beyond num_slots are rejected on the device (the row is not written).
+ * kv_dim must be a multiple of 8.
+ * ------------------------------------------------------------------------ */
+int le_kv_cache_write(const void* k, const void* v, le_dtype src_dtype,
+                      const int32_t* slot_mapping, void* k_cache, void* v_cache,
+                      le_dtype cache_dtype, int n_tokens, int kv_dim, int64_t num_slots,
+                      hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * (3)(4) Paged attention, reference-shaped.
+ * Replaces launch_attention_decode and launch_attention_decode_gqa
+ * (cuda_kernels.h:50-64, attention_decode.cu:45-161,
+ * attention_decode_gqa.cu:87-232). Same arguments and the same result:
+ * token t attends over positions 0..token_pos[t] of sequence token_seq[t],
+ * whose block table starts at block_tables + table_offset[token_seq[t]];
+ * kv_head = head / (q_heads / kv_heads). One K/V read serves the whole GQA
+ * group. The context of each token is split across workgroups (split-K), the
+ * partial results merged by a second kernel, so `workspace` must hold
+ * le_attention_decode_workspace_size(n_tokens, q_heads, head_dim) bytes.
+ * q/out dtype `act_dtype`, caches `kv_dtype`. head_dim 64 or 128;
+ * q_heads / kv_heads <= 8; block_size a multiple of 8 (16 in every config).
+ * num_cache_blocks bounds the block ids read from the tables.
+ * ------------------------------------------------------------------------ */
+size_t le_attention_decode_workspace_size(int n_tokens, int q_heads, int kv_heads, int head_dim);
+
+int le_attention_decode(const void* q, le_dtype act_dtype, const void* k_cache,
+                        const void* v_cache, le_dtype kv_dtype, const int32_t* block_tables,
+                        const int32_t* table_offset, const int32_t* token_seq,
+                        const int32_t* token_pos, void* out, int n_tokens, int q_heads,
+                        int kv_heads, int head_dim, int block_size, float scale,
+                        int64_t num_cache_blocks, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * (1) Ragged step packing.
+ * Replaces CudaModel::flatten + upload_step_indices (cuda_model.cu:434-491):
+ * the scheduler's slices (prefill chunks first, then decode tokens,
+ * scheduler.cpp:164-211) become ONE buffer holding token ids, positions,
+ * slot mapping, token->sequence, concatenated block tables + offsets,
+ * cu_seqlens_q, seq_lens_k, logit rows and the attention work lists, uploaded
+ * with one hipMemcpyAsync per step and shared by every layer.
+ * ------------------------------------------------------------------------ */
+typedef struct le_step_slice {
+  int64_t seq_key;       /* sequence identity; slices with one key share one table */
+  int32_t start;         /* first position computed by this slice */
+  int32_t len;           /* number of tokens (1 for decode) */
+  int32_t needs_logits;  /* last token produces a logits row */
+  int32_t num_blocks;    /* entries of `blocks` */
+  const int32_t* blocks; /* the sequence's block table */
+  const int32_t* tokens; /* the sequence's token ids, at least start+len of them */
+} le_step_slice;
+
+typedef struct le_plan_config {
+  int32_t q_heads, kv_heads, head_dim, block_size;
+  int32_t kv_dtype;            /* le_dtype of the cache the plan will be run against */
+  int32_t partition_tokens;    /* split-K partition of decode rows; 0 = default */
+  int32_t chunk_q_tile;        /* query rows per chunk tile (16); 0 = default */
+  int32_t chunk_partition_tokens; /* key partition of chunk tiles; 0 = default */
+} le_plan_config;
+
+typedef struct le_step_plan {
+  le_plan_config cfg;
+  int32_t n_tokens;      /* packed query rows */
+  int32_t n_seqs;        /* distinct sequences (tables), first-seen order */
+  int32_t n_table;       /* entries of the concatenated block tables */
+  int32_t n_logits;      /* logit rows */
+  int32_t n_decode_items, n_chunk_items, n_combine_items, n_parts;
+  int32_t max_pos;
+  int32_t n_slices;      /* entries of cu_seqlens_q minus one, and of seq_lens_k */
+  /* byte offsets of each array inside the packed buffer */
+  int64_t off_token_ids, off_positions, off_slots, off_token_seq, off_tables,
+      off_table_offset, off_cu_seqlens_q, off_seq_lens_k, off_logit_rows, off_decode_items,
+      off_chunk_items, off_combine_items;
+  int64_t bytes;         /* total size of the packed buffer */
+  const void* dev;       /* device copy, set by le_plan_upload */
+} le_step_plan;
+
+/* Packs a step into host_buf (pinned memory recommended). If host_cap is too
+ * small, returns LE_ENOSPACE with plan->bytes set to the size needed. */
+int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config* cfg,
+                 void* host_buf, int64_t host_cap, le_step_plan* plan);
+
+/* One async copy of the packed buffer to dev_buf (>= plan->bytes), then
+ * plan->dev = dev_buf. The host buffer must stay alive until the copy ends. */
+int le_plan_upload(le_step_plan* plan, const void* host_buf, void* dev_buf,
+                   hipStream_t stream);
+
+/* Device address of one packed array (e.g. plan->off_slots). */
+static inline const int32_t* le_plan_dev_array(const le_step_plan* plan, int64_t off) {
+  return (const int32_t*)((const char*)plan->dev + off);
+}
+
+/* ------------------------------------------------------------------------
+ * (3)(4) Ragged paged attention over a packed step.
+ * Decode rows (slices of length 1) run the bandwidth kernel: one workgroup per
+ * (row, kv head, context partition), each K/V row read once for the whole
+ * GQA group. Prefill-chunk rows run the MFMA kernel with a bf16 cache
+ * (causal mask by absolute position against the cached prefix), and the
+ * bandwidth kernel row by row with an fp32 cache. Split rows are merged by
+ * the combine kernel. The result equals le_attention_decode on the same step.
+ * ------------------------------------------------------------------------ */
+size_t le_ragged_workspace_size(const le_step_plan* plan);
+
+int le_ragged_paged_attention(const void* q, le_dtype act_dtype, const void* k_cache,
+                              const void* v_cache, le_dtype kv_dtype, int64_t num_cache_blocks,
+                              const le_step_plan* plan, float scale, void* out, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LLM_ENGINE_AMD_H */

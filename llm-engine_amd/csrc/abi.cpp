@@ -1,0 +1,206 @@
+// extern "C" entry points of include/llm_engine_amd.h: argument validation,
+// then the launchers in le_internal.h. No exception and no allocation crosses
+// this file.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+
+#include "le_internal.h"
+#include "llm_engine_amd.h"
+
+#ifndef LE_VERSION_STRING
+#define LE_VERSION_STRING "llm-engine-amd 0.1 (gfx950)"
+#endif
+
+namespace {
+
+int hip_status(hipError_t e) { return e == hipSuccess ? LE_OK : static_cast<int>(e); }
+
+bool valid_dtype(int d) { return d == LE_F32 || d == LE_BF16; }
+
+bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
+
+// Shapes every attention kernel supports.
+int check_attention_shape(int q_heads, int kv_heads, int head_dim, int block_size) {
+  if (q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || block_size <= 0) return LE_EINVAL;
+  if (q_heads % kv_heads != 0) return LE_EINVAL;
+  if (q_heads / kv_heads > 8) return LE_EUNSUPPORTED;
+  if (head_dim != 64 && head_dim != 128) return LE_EUNSUPPORTED;
+  // The score buffer holds 512 positions, a whole number of blocks; a wave
+  // load covers up to 8 rows of a block.
+  if (!pow2(block_size) || block_size < 8 || block_size > 512) return LE_EUNSUPPORTED;
+  return LE_OK;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+// Workspace: arrival counters first (so their offset does not depend on the
+// partial count), then the partial accumulators and (max, sum) pairs.
+size_t counter_bytes(int64_t n_rows, int kv_heads) {
+  return align256(static_cast<size_t>(n_rows) * kv_heads * sizeof(int32_t));
+}
+
+size_t partial_bytes(int64_t n_parts, int64_t n_rows, int q_heads, int kv_heads, int head_dim) {
+  return counter_bytes(n_rows, kv_heads) +
+         align256(static_cast<size_t>(n_parts) * q_heads * head_dim * sizeof(float)) +
+         align256(static_cast<size_t>(n_parts) * q_heads * sizeof(float2));
+}
+
+le::PartialLayout carve_partials(void* ws, int64_t n_parts, int64_t n_rows, int q_heads,
+                                 int kv_heads, int head_dim) {
+  le::PartialLayout L;
+  char* b = static_cast<char*>(ws);
+  L.counters = reinterpret_cast<int32_t*>(b);
+  b += counter_bytes(n_rows, kv_heads);
+  L.acc = reinterpret_cast<float*>(b);
+  b += align256(static_cast<size_t>(n_parts) * q_heads * head_dim * sizeof(float));
+  L.ml = reinterpret_cast<float2*>(b);
+  return L;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* le_version(void) { return LE_VERSION_STRING; }
+
+const char* le_status_string(int status) {
+  switch (status) {
+    case LE_OK: return "ok";
+    case LE_EINVAL: return "invalid argument";
+    case LE_EUNSUPPORTED: return "unsupported shape";
+    case LE_ENOSPACE: return "buffer too small";
+    default: return status > 0 ? hipGetErrorString(static_cast<hipError_t>(status)) : "unknown";
+  }
+}
+
+int le_kv_cache_write(const void* k, const void* v, le_dtype src_dtype,
+                      const int32_t* slot_mapping, void* k_cache, void* v_cache,
+                      le_dtype cache_dtype, int n_tokens, int kv_dim, int64_t num_slots,
+                      hipStream_t stream) {
+  if (n_tokens < 0 || kv_dim <= 0 || num_slots < 0) return LE_EINVAL;
+  if (!valid_dtype(src_dtype) || !valid_dtype(cache_dtype)) return LE_EINVAL;
+  if (kv_dim % 8 != 0) return LE_EUNSUPPORTED;
+  if (n_tokens == 0) return LE_OK;  // the reference returns early on an empty grid
+  if (!k || !v || !slot_mapping || !k_cache || !v_cache) return LE_EINVAL;
+  return hip_status(le::kv_cache_write(k, v, src_dtype == LE_BF16, slot_mapping, k_cache, v_cache,
+                                       cache_dtype == LE_BF16, n_tokens, kv_dim, num_slots,
+                                       stream));
+}
+
+size_t le_attention_decode_workspace_size(int n_tokens, int q_heads, int kv_heads, int head_dim) {
+  if (n_tokens <= 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0) return 0;
+  const int ns = le::decode_nsplit(n_tokens, kv_heads);
+  return partial_bytes(static_cast<int64_t>(n_tokens) * ns, n_tokens, q_heads, kv_heads, head_dim);
+}
+
+int le_attention_decode(const void* q, le_dtype act_dtype, const void* k_cache,
+                        const void* v_cache, le_dtype kv_dtype, const int32_t* block_tables,
+                        const int32_t* table_offset, const int32_t* token_seq,
+                        const int32_t* token_pos, void* out, int n_tokens, int q_heads,
+                        int kv_heads, int head_dim, int block_size, float scale,
+                        int64_t num_cache_blocks, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream) {
+  if (n_tokens < 0 || !valid_dtype(act_dtype) || !valid_dtype(kv_dtype)) return LE_EINVAL;
+  if (n_tokens == 0) return LE_OK;
+  const int shape = check_attention_shape(q_heads, kv_heads, head_dim, block_size);
+  if (shape != LE_OK) return shape;
+  if (!q || !k_cache || !v_cache || !block_tables || !table_offset || !token_seq || !token_pos ||
+      !out || !std::isfinite(scale) || num_cache_blocks <= 0)
+    return LE_EINVAL;
+  const size_t need = le_attention_decode_workspace_size(n_tokens, q_heads, kv_heads, head_dim);
+  if (!workspace || workspace_bytes < need) return LE_ENOSPACE;
+
+  le::DecodeParams p{};
+  p.q = q; p.k_cache = k_cache; p.v_cache = v_cache;
+  p.tables = block_tables; p.table_offset = table_offset;
+  p.token_seq = token_seq; p.token_pos = token_pos; p.out = out;
+  p.nsplit = le::decode_nsplit(n_tokens, kv_heads);
+  p.parts = carve_partials(workspace, static_cast<int64_t>(n_tokens) * p.nsplit, n_tokens, q_heads,
+                           kv_heads, head_dim);
+  p.items = nullptr;
+  p.n_rows = n_tokens;
+  p.q_heads = q_heads; p.kv_heads = kv_heads; p.head_dim = head_dim; p.block_size = block_size;
+  p.scale_log2 = scale * 1.4426950408889634f;
+  p.num_cache_blocks = num_cache_blocks;
+  // Split rows are merged inside the launch (last-arriving partition).
+  const hipError_t e = le::attention_decode(p, act_dtype == LE_BF16, kv_dtype == LE_BF16, stream);
+  return hip_status(e);
+}
+
+}  // extern "C"
+
+extern "C" {
+
+size_t le_ragged_workspace_size(const le_step_plan* plan) {
+  if (!plan || plan->n_parts <= 0) return 0;
+  return partial_bytes(plan->n_parts, plan->n_tokens, plan->cfg.q_heads, plan->cfg.kv_heads,
+                       plan->cfg.head_dim);
+}
+
+int le_ragged_paged_attention(const void* q, le_dtype act_dtype, const void* k_cache,
+                              const void* v_cache, le_dtype kv_dtype, int64_t num_cache_blocks,
+                              const le_step_plan* plan, float scale, void* out, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream) {
+  if (!plan || !valid_dtype(act_dtype) || !valid_dtype(kv_dtype)) return LE_EINVAL;
+  if (plan->n_tokens == 0) return LE_OK;
+  const le_plan_config& cfg = plan->cfg;
+  const int shape = check_attention_shape(cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.block_size);
+  if (shape != LE_OK) return shape;
+  // A plan routes chunk rows by the cache dtype it was built for.
+  if (cfg.kv_dtype != kv_dtype) return LE_EINVAL;
+  if (!plan->dev || !q || !k_cache || !v_cache || !out || !std::isfinite(scale) ||
+      num_cache_blocks <= 0)
+    return LE_EINVAL;
+  const size_t need = le_ragged_workspace_size(plan);
+  if (need > 0 && (!workspace || workspace_bytes < need)) return LE_ENOSPACE;
+
+  const char* dev = static_cast<const char*>(plan->dev);
+  auto arr = [&](int64_t off) { return reinterpret_cast<const int32_t*>(dev + off); };
+  le::PartialLayout parts{};
+  if (need > 0)
+    parts = carve_partials(workspace, plan->n_parts, plan->n_tokens, cfg.q_heads, cfg.kv_heads,
+                           cfg.head_dim);
+  const float scale_log2 = scale * 1.4426950408889634f;
+
+  le::DecodeParams d{};
+  d.q = q; d.k_cache = k_cache; d.v_cache = v_cache;
+  d.tables = arr(plan->off_tables); d.table_offset = arr(plan->off_table_offset);
+  d.token_seq = arr(plan->off_token_seq); d.token_pos = arr(plan->off_positions);
+  d.out = out; d.parts = parts;
+  d.items = reinterpret_cast<const le::DecodeItem*>(dev + plan->off_decode_items);
+  d.n_rows = plan->n_decode_items; d.nsplit = 1;
+  d.q_heads = cfg.q_heads; d.kv_heads = cfg.kv_heads; d.head_dim = cfg.head_dim;
+  d.block_size = cfg.block_size; d.scale_log2 = scale_log2; d.num_cache_blocks = num_cache_blocks;
+  hipError_t e = le::attention_decode(d, act_dtype == LE_BF16, kv_dtype == LE_BF16, stream);
+  if (e != hipSuccess) return hip_status(e);
+
+  if (plan->n_chunk_items > 0) {
+    if (kv_dtype != LE_BF16) return LE_EINVAL;
+    le::ChunkParams c{};
+    c.q = q; c.k_cache = k_cache; c.v_cache = v_cache;
+    c.tables = d.tables; c.table_offset = d.table_offset; c.token_pos = d.token_pos;
+    c.out = out; c.parts = parts;
+    c.items = reinterpret_cast<const le::ChunkItem*>(dev + plan->off_chunk_items);
+    c.n_items = plan->n_chunk_items;
+    c.q_heads = cfg.q_heads; c.kv_heads = cfg.kv_heads; c.head_dim = cfg.head_dim;
+    c.block_size = cfg.block_size; c.scale_log2 = scale_log2;
+    c.num_cache_blocks = num_cache_blocks;
+    e = le::attention_chunk(c, act_dtype == LE_BF16, stream);
+    if (e != hipSuccess) return hip_status(e);
+  }
+
+  if (plan->n_combine_items > 0) {
+    le::CombineParams m{};
+    m.parts = parts;
+    m.items = reinterpret_cast<const le::CombineItem*>(dev + plan->off_combine_items);
+    m.token_pos = d.token_pos;
+    m.n_rows = plan->n_combine_items; m.nsplit = 1; m.block_size = cfg.block_size;
+    m.q_heads = cfg.q_heads; m.head_dim = cfg.head_dim; m.out = out;
+    e = le::attention_combine(m, act_dtype == LE_BF16, stream);
+  }
+  return hip_status(e);
+}
+
+}  // extern "C"

@@ -1,0 +1,100 @@
+// Internal launch functions behind the C ABI in include/llm_engine_amd.h.
+// Argument validation happens in abi.cpp; these assume valid shapes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace le {
+
+// Split-K partial result of one (row, q head, context partition): the
+// unnormalised accumulator, and the running max (log2 domain) and sum.
+struct PartialLayout {
+  float* acc;         // [n_parts][q_heads][head_dim]
+  float2* ml;         // [n_parts][q_heads]  (m, l)
+  int32_t* counters;  // [n_rows][kv_heads] arrivals; zero between launches
+};
+
+// Decode work item: query row `token` (position `pos`, block table starting
+// at tables + table_off) over blocks [blk_begin, blk_end) of its table. The
+// row's position and table offset travel in the item so a workgroup reaches
+// its first K/V load after one dependent read. part < 0: the row has a single
+// partition and the kernel writes the normalised output itself. Otherwise the
+// item writes partial `part`, and the last of the row's n_parts items to
+// arrive (per kv head) merges partials [part_begin, part_begin + n_parts).
+struct DecodeItem {
+  int32_t token, pos, table_off, blk_begin, blk_end, part, part_begin, n_parts;
+};
+
+// Chunk work item: query rows [tok_begin, tok_begin + n_q) (consecutive
+// positions of one sequence) over key blocks [blk_begin, blk_end). Row
+// tok_begin + i writes partial part0 + i * part_stride, or, when part0 < 0,
+// its normalised output directly.
+struct ChunkItem {
+  int32_t tok_begin, n_q, blk_begin, blk_end, part0, part_stride, seq, pad_;
+};
+
+// Rows whose context was split: partials [part_begin, part_begin + n_parts).
+struct CombineItem {
+  int32_t token, part_begin, n_parts, pad_;
+};
+
+hipError_t kv_cache_write(const void* k, const void* v, int src_bf16, const int32_t* slots,
+                          void* kc, void* vc, int cache_bf16, int n_tokens, int kv_dim,
+                          int64_t num_slots, hipStream_t stream);
+
+struct DecodeParams {
+  const void* q;
+  const void* k_cache;
+  const void* v_cache;
+  const int32_t* tables;
+  const int32_t* table_offset;
+  const int32_t* token_seq;
+  const int32_t* token_pos;
+  void* out;
+  PartialLayout parts;
+  const DecodeItem* items;  // null: one item per (token, split) with `nsplit` splits
+  int n_rows;               // items, or tokens when items is null
+  int nsplit;
+  int q_heads, kv_heads, head_dim, block_size;
+  float scale_log2;         // softmax scale * log2(e)
+  int64_t num_cache_blocks;
+};
+
+hipError_t attention_decode(const DecodeParams& p, int act_bf16, int kv_bf16, hipStream_t stream);
+
+struct CombineParams {
+  PartialLayout parts;
+  const CombineItem* items;  // null: token = blockIdx.x with `nsplit` splits derived from pos
+  const int32_t* token_pos;
+  int n_rows, nsplit, block_size;
+  int q_heads, head_dim;
+  void* out;
+};
+
+hipError_t attention_combine(const CombineParams& p, int act_bf16, hipStream_t stream);
+
+struct ChunkParams {
+  const void* q;
+  const void* k_cache;
+  const void* v_cache;
+  const int32_t* tables;
+  const int32_t* table_offset;
+  const int32_t* token_pos;
+  void* out;
+  PartialLayout parts;
+  const ChunkItem* items;
+  int n_items;
+  int q_heads, kv_heads, head_dim, block_size;
+  float scale_log2;
+  int64_t num_cache_blocks;
+};
+
+hipError_t attention_chunk(const ChunkParams& p, int act_bf16, hipStream_t stream);
+
+// Split count for the reference-shaped entry point, where the host does not
+// know the context lengths: enough workgroups to cover the chip several times.
+int decode_nsplit(int n_tokens, int kv_heads);
+
+}  // namespace le

@@ -1,0 +1,275 @@
+// Ragged step packing (hot-path part 1): le_plan_step / le_plan_upload.
+//
+// Reference: CudaModel::flatten and upload_step_indices,
+// src/model/cuda/cuda_model.cu:434-491, and the CPU twin cpu_model.cpp:107-118.
+// The reference builds five int arrays and sends them with six synchronous
+// pageable cudaMemcpy calls per step, deduplicating sequences with an O(N*S)
+// scan. Here the same arrays (identical values: token ids, positions, int32
+// slots, token->sequence index in first-seen order, concatenated tables and
+// their offsets) are written into one caller-owned buffer together with
+// cu_seqlens_q / seq_lens_k and the attention work lists, then sent with one
+// hipMemcpyAsync that every layer of the step shares.
+//
+// Work lists. A row whose slice has length 1 is a decode row: its context
+// 0..pos is cut into partitions of ~partition_tokens (whole blocks, equal
+// shares) and each partition becomes one DecodeItem. With a bf16 cache, the
+// rows of a longer slice (a prefill chunk) are cut into tiles of chunk_q_tile
+// consecutive positions; each tile's keys 0..last position are cut into
+// partitions of ~chunk_partition_tokens, one ChunkItem each, run on MFMA.
+// With an fp32 cache, chunk rows are decode rows (exact fp32 arithmetic on the
+// vector ALUs). A chunk row with more than one partition gets a CombineItem;
+// a split decode row is merged inside the decode launch.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <unordered_map>
+#include <vector>
+
+#include "le_internal.h"
+#include "llm_engine_amd.h"
+
+namespace {
+
+constexpr int kDefaultPartition = 256;       // decode rows: smallest automatic partition
+constexpr int kMaxAutoPartition = 4096;      // decode rows: largest automatic partition
+constexpr int kPartitionQuantum = 256;       // 4 waves x 64-key tiles
+constexpr int64_t kTargetItems = 1024;       // workgroups per step the sizing aims for
+constexpr int kMaxMergeEntries = 1024;       // partitions x group the decode merge can stage
+constexpr int kDefaultChunkTile = 16;        // MFMA row tile
+constexpr int kDefaultChunkPartition = 256;  // chunk tiles
+
+int64_t align256(int64_t x) { return (x + 255) & ~static_cast<int64_t>(255); }
+
+int round_to_blocks(int tokens, int bs) {
+  const int b = (tokens + bs - 1) / bs;
+  return b < 1 ? 1 : b;
+}
+
+}  // namespace
+
+extern "C" {
+
+int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config* cfg_in,
+                 void* host_buf, int64_t host_cap, le_step_plan* plan) {
+  if (!plan || !cfg_in || n_slices < 0 || (n_slices > 0 && !slices)) return LE_EINVAL;
+  le_plan_config cfg = *cfg_in;
+  if (cfg.block_size <= 0 || cfg.q_heads <= 0 || cfg.kv_heads <= 0 || cfg.head_dim <= 0)
+    return LE_EINVAL;
+  if (cfg.kv_dtype != LE_F32 && cfg.kv_dtype != LE_BF16) return LE_EINVAL;
+  const int bs = cfg.block_size;
+  if (cfg.partition_tokens <= 0) {
+    // Size decode partitions so the step has about kTargetItems workgroups:
+    // enough to cover every CU several times, few enough that each one
+    // streams a long stretch of K/V and its fixed costs (item fetch, wave
+    // merge, partial write) stay small next to it.
+    int64_t ctx = 0;
+    for (int i = 0; i < n_slices; i++)
+      if (slices[i].len == 1 || cfg.kv_dtype != LE_BF16)
+        for (int r = 0; r < slices[i].len; r++) ctx += slices[i].start + r + 1;
+    const int64_t per_kvh = std::max<int64_t>(1, kTargetItems / cfg.kv_heads);
+    int64_t part = (ctx + per_kvh - 1) / per_kvh;
+    part = (part + kPartitionQuantum - 1) / kPartitionQuantum * kPartitionQuantum;
+    cfg.partition_tokens = static_cast<int32_t>(std::min<int64_t>(
+        std::max<int64_t>(part, kDefaultPartition), kMaxAutoPartition));
+  }
+  if (cfg.chunk_q_tile <= 0) cfg.chunk_q_tile = kDefaultChunkTile;
+  if (cfg.chunk_partition_tokens <= 0) cfg.chunk_partition_tokens = kDefaultChunkPartition;
+  if (cfg.chunk_q_tile != 16) return LE_EUNSUPPORTED;  // the MFMA tile height
+  const int dec_pb = round_to_blocks(cfg.partition_tokens, bs);
+  const int chk_pb = round_to_blocks(cfg.chunk_partition_tokens, bs);
+  const bool mfma_chunks = cfg.kv_dtype == LE_BF16;
+  const int max_decode_parts = std::max(1, kMaxMergeEntries / (cfg.q_heads / cfg.kv_heads));
+
+  // ---- sizes, and validation of every slice against its table ----
+  int64_t n_tok = 0, n_table = 0;
+  int n_logits = 0, n_seqs = 0, max_pos = 0;
+  std::unordered_map<int64_t, int> seq_index;
+  std::vector<int> slice_seq(static_cast<size_t>(n_slices));
+  std::vector<int> seq_first_slice;
+  for (int i = 0; i < n_slices; i++) {
+    const le_step_slice& s = slices[i];
+    if (s.len <= 0 || s.start < 0 || s.num_blocks < 0 || !s.tokens) return LE_EINVAL;
+    if (s.num_blocks > 0 && !s.blocks) return LE_EINVAL;
+    const int last = s.start + s.len - 1;
+    if (last / bs >= s.num_blocks) return LE_EINVAL;  // a position without a block
+    auto it = seq_index.find(s.seq_key);
+    if (it == seq_index.end()) {
+      seq_index.emplace(s.seq_key, n_seqs);
+      slice_seq[i] = n_seqs++;
+      seq_first_slice.push_back(i);
+      n_table += s.num_blocks;
+    } else {
+      slice_seq[i] = it->second;
+    }
+    n_tok += s.len;
+    if (s.needs_logits) n_logits++;
+    max_pos = std::max(max_pos, last);
+  }
+  if (n_tok > INT32_MAX / 2) return LE_EUNSUPPORTED;
+
+  // Table offset of each distinct sequence in the concatenated tables.
+  std::vector<int32_t> seq_table_off(static_cast<size_t>(n_seqs));
+  {
+    int32_t o = 0;
+    for (int s = 0; s < n_seqs; s++) {
+      seq_table_off[s] = o;
+      o += slices[seq_first_slice[s]].num_blocks;
+    }
+  }
+
+  // ---- work lists ----
+  std::vector<le::DecodeItem> dec;
+  std::vector<le::ChunkItem> chk;
+  std::vector<le::CombineItem> cmb;
+  int32_t parts = 0;
+  {
+    int32_t t = 0;
+    for (int i = 0; i < n_slices; i++) {
+      const le_step_slice& s = slices[i];
+      if (s.len > 1 && mfma_chunks) {
+        for (int q0 = 0; q0 < s.len; q0 += cfg.chunk_q_tile) {
+          const int nq = std::min(cfg.chunk_q_tile, s.len - q0);
+          const int last = s.start + q0 + nq - 1;
+          const int nb = last / bs + 1;
+          const int J = (nb + chk_pb - 1) / chk_pb;
+          const int base = J > 1 ? parts : -1;
+          for (int j = 0; j < J; j++) {
+            le::ChunkItem c{};
+            c.tok_begin = t + q0;
+            c.n_q = nq;
+            c.blk_begin = static_cast<int32_t>(static_cast<int64_t>(j) * nb / J);
+            c.blk_end = static_cast<int32_t>(static_cast<int64_t>(j + 1) * nb / J);
+            c.part0 = J > 1 ? base + j : -1;
+            c.part_stride = J;
+            c.seq = slice_seq[i];
+            chk.push_back(c);
+          }
+          if (J > 1) {
+            for (int r = 0; r < nq; r++) cmb.push_back({t + q0 + r, base + r * J, J, 0});
+            parts += nq * J;
+          }
+        }
+      } else {
+        for (int r = 0; r < s.len; r++) {
+          const int pos = s.start + r;
+          const int nb = pos / bs + 1;
+          // The in-kernel merge stages n_parts * group (m, l) pairs in LDS.
+          const int J = std::min((nb + dec_pb - 1) / dec_pb, max_decode_parts);
+          // Split rows are merged inside the decode launch by the last
+          // partition to finish, so they need no combine item.
+          for (int j = 0; j < J; j++) {
+            le::DecodeItem d{};
+            d.token = t + r;
+            d.pos = pos;
+            d.table_off = seq_table_off[slice_seq[i]];
+            d.blk_begin = static_cast<int32_t>(static_cast<int64_t>(j) * nb / J);
+            d.blk_end = static_cast<int32_t>(static_cast<int64_t>(j + 1) * nb / J);
+            d.part = J > 1 ? parts + j : -1;
+            d.part_begin = parts;
+            d.n_parts = J;
+            dec.push_back(d);
+          }
+          if (J > 1) parts += J;
+        }
+      }
+      t += s.len;
+    }
+  }
+
+  // ---- layout: every array 256-byte aligned in one buffer ----
+  le_step_plan P{};
+  P.cfg = cfg;
+  P.n_tokens = static_cast<int32_t>(n_tok);
+  P.n_seqs = n_seqs;
+  P.n_table = static_cast<int32_t>(n_table);
+  P.n_logits = n_logits;
+  P.n_decode_items = static_cast<int32_t>(dec.size());
+  P.n_chunk_items = static_cast<int32_t>(chk.size());
+  P.n_combine_items = static_cast<int32_t>(cmb.size());
+  P.n_parts = parts;
+  P.max_pos = max_pos;
+  P.n_slices = n_slices;
+  int64_t off = 0;
+  auto take = [&](int64_t bytes) {
+    const int64_t o = off;
+    off = align256(off + std::max<int64_t>(bytes, 4));
+    return o;
+  };
+  P.off_token_ids = take(n_tok * 4);
+  P.off_positions = take(n_tok * 4);
+  P.off_slots = take(n_tok * 4);
+  P.off_token_seq = take(n_tok * 4);
+  P.off_tables = take(n_table * 4);
+  P.off_table_offset = take(static_cast<int64_t>(n_seqs) * 4);
+  P.off_cu_seqlens_q = take(static_cast<int64_t>(n_slices + 1) * 4);
+  P.off_seq_lens_k = take(static_cast<int64_t>(n_slices) * 4);
+  P.off_logit_rows = take(static_cast<int64_t>(n_logits) * 4);
+  P.off_decode_items = take(static_cast<int64_t>(dec.size()) * sizeof(le::DecodeItem));
+  P.off_chunk_items = take(static_cast<int64_t>(chk.size()) * sizeof(le::ChunkItem));
+  P.off_combine_items = take(static_cast<int64_t>(cmb.size()) * sizeof(le::CombineItem));
+  P.bytes = off;
+  P.dev = nullptr;
+  if (!host_buf || host_cap < P.bytes) {
+    *plan = P;
+    return LE_ENOSPACE;
+  }
+
+  char* base = static_cast<char*>(host_buf);
+  auto arr = [&](int64_t o) { return reinterpret_cast<int32_t*>(base + o); };
+  int32_t* token_ids = arr(P.off_token_ids);
+  int32_t* positions = arr(P.off_positions);
+  int32_t* slots = arr(P.off_slots);
+  int32_t* token_seq = arr(P.off_token_seq);
+  int32_t* tables = arr(P.off_tables);
+  int32_t* table_offset = arr(P.off_table_offset);
+  int32_t* cu_q = arr(P.off_cu_seqlens_q);
+  int32_t* lens_k = arr(P.off_seq_lens_k);
+  int32_t* logit_rows = arr(P.off_logit_rows);
+
+  int32_t nt = 0;
+  for (int s = 0; s < n_seqs; s++) {
+    const le_step_slice& f = slices[seq_first_slice[s]];
+    table_offset[s] = nt;
+    if (f.num_blocks) std::memcpy(tables + nt, f.blocks, sizeof(int32_t) * f.num_blocks);
+    nt += f.num_blocks;
+  }
+  int32_t t = 0, r = 0;
+  cu_q[0] = 0;
+  for (int i = 0; i < n_slices; i++) {
+    const le_step_slice& s = slices[i];
+    // Slots come from the table of the sequence (its first slice), as the
+    // reference reads them from the Sequence object.
+    const le_step_slice& f = slices[seq_first_slice[slice_seq[i]]];
+    for (int k = 0; k < s.len; k++) {
+      const int pos = s.start + k;
+      token_ids[t] = s.tokens[pos];
+      positions[t] = pos;
+      token_seq[t] = slice_seq[i];
+      slots[t] = static_cast<int32_t>(static_cast<int64_t>(f.blocks[pos / bs]) * bs + pos % bs);
+      t++;
+    }
+    if (s.needs_logits) logit_rows[r++] = t - 1;
+    cu_q[i + 1] = t;
+    lens_k[i] = s.start + s.len;
+  }
+  if (!dec.empty())
+    std::memcpy(base + P.off_decode_items, dec.data(), dec.size() * sizeof(le::DecodeItem));
+  if (!chk.empty())
+    std::memcpy(base + P.off_chunk_items, chk.data(), chk.size() * sizeof(le::ChunkItem));
+  if (!cmb.empty())
+    std::memcpy(base + P.off_combine_items, cmb.data(), cmb.size() * sizeof(le::CombineItem));
+  *plan = P;
+  return LE_OK;
+}
+
+int le_plan_upload(le_step_plan* plan, const void* host_buf, void* dev_buf, hipStream_t stream) {
+  if (!plan || !host_buf || !dev_buf || plan->bytes <= 0) return LE_EINVAL;
+  const hipError_t e = hipMemcpyAsync(dev_buf, host_buf, static_cast<size_t>(plan->bytes),
+                                      hipMemcpyHostToDevice, stream);
+  if (e != hipSuccess) return static_cast<int>(e);
+  plan->dev = dev_buf;
+  return LE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,137 @@
+"""Loads libllm_engine_amd.so (the gfx950 C ABI) with ctypes and declares its
+entry points. There is no fallback: if the library is missing, importing the
+kernels raises, so nothing silently runs on the CPU instead."""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import os
+
+# LE_LIB_PATH selects another build of the same library (e.g. a variant under
+# test); by default the in-tree build is loaded.
+LIB_PATH = Path(os.environ.get("LE_LIB_PATH") or
+                Path(__file__).resolve().parent.parent / "lib" / "libllm_engine_amd.so")
+
+LE_OK = 0
+LE_EINVAL = -1
+LE_EUNSUPPORTED = -2
+LE_ENOSPACE = -3
+LE_F32 = 0
+LE_BF16 = 1
+
+c_i32p = ctypes.POINTER(ctypes.c_int32)
+
+
+class StepSlice(ctypes.Structure):
+    _fields_ = [
+        ("seq_key", ctypes.c_int64),
+        ("start", ctypes.c_int32),
+        ("len", ctypes.c_int32),
+        ("needs_logits", ctypes.c_int32),
+        ("num_blocks", ctypes.c_int32),
+        ("blocks", ctypes.c_void_p),
+        ("tokens", ctypes.c_void_p),
+    ]
+
+
+class PlanConfig(ctypes.Structure):
+    _fields_ = [
+        ("q_heads", ctypes.c_int32),
+        ("kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("block_size", ctypes.c_int32),
+        ("kv_dtype", ctypes.c_int32),
+        ("partition_tokens", ctypes.c_int32),
+        ("chunk_q_tile", ctypes.c_int32),
+        ("chunk_partition_tokens", ctypes.c_int32),
+    ]
+
+
+class StepPlan(ctypes.Structure):
+    _fields_ = [
+        ("cfg", PlanConfig),
+        ("n_tokens", ctypes.c_int32),
+        ("n_seqs", ctypes.c_int32),
+        ("n_table", ctypes.c_int32),
+        ("n_logits", ctypes.c_int32),
+        ("n_decode_items", ctypes.c_int32),
+        ("n_chunk_items", ctypes.c_int32),
+        ("n_combine_items", ctypes.c_int32),
+        ("n_parts", ctypes.c_int32),
+        ("max_pos", ctypes.c_int32),
+        ("n_slices", ctypes.c_int32),
+        ("off_token_ids", ctypes.c_int64),
+        ("off_positions", ctypes.c_int64),
+        ("off_slots", ctypes.c_int64),
+        ("off_token_seq", ctypes.c_int64),
+        ("off_tables", ctypes.c_int64),
+        ("off_table_offset", ctypes.c_int64),
+        ("off_cu_seqlens_q", ctypes.c_int64),
+        ("off_seq_lens_k", ctypes.c_int64),
+        ("off_logit_rows", ctypes.c_int64),
+        ("off_decode_items", ctypes.c_int64),
+        ("off_chunk_items", ctypes.c_int64),
+        ("off_combine_items", ctypes.c_int64),
+        ("bytes", ctypes.c_int64),
+        ("dev", ctypes.c_void_p),
+    ]
+
+
+# name -> (restype, argtypes). Exactly the symbols include/llm_engine_amd.h declares.
+SIGNATURES = {
+    "le_version": (ctypes.c_char_p, []),
+    "le_status_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "le_kv_cache_write": (ctypes.c_int, [
+        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+        ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64,
+        ctypes.c_void_p]),
+    "le_attention_decode_workspace_size": (ctypes.c_size_t, [
+        ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "le_attention_decode": (ctypes.c_int, [
+        ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+        ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float,
+        ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "le_plan_step": (ctypes.c_int, [
+        ctypes.POINTER(StepSlice), ctypes.c_int, ctypes.POINTER(PlanConfig), ctypes.c_void_p,
+        ctypes.c_int64, ctypes.POINTER(StepPlan)]),
+    "le_plan_upload": (ctypes.c_int, [
+        ctypes.POINTER(StepPlan), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
+    "le_ragged_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(StepPlan)]),
+    "le_ragged_paged_attention": (ctypes.c_int, [
+        ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+        ctypes.c_int64, ctypes.POINTER(StepPlan), ctypes.c_float, ctypes.c_void_p,
+        ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+}
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """The loaded library; raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python llm-engine_amd/build.py` "
+                "(there is no CPU fallback for these kernels)")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+class LeError(RuntimeError):
+    def __init__(self, fn: str, status: int):
+        msg = load().le_status_string(status).decode()
+        super().__init__(f"{fn} failed: status {status} ({msg})")
+        self.status = status
+
+
+def check(fn: str, status: int) -> None:
+    if status != LE_OK:
+        raise LeError(fn, status)

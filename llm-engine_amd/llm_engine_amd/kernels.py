@@ -1,0 +1,198 @@
+"""Python face of the C ABI for torch device tensors.
+
+The names mirror the reference launchers (include/engine/cuda_kernels.h:43-64:
+launch_store_kv, launch_attention_decode[_gqa]) plus the ragged step API.
+Every call goes through libllm_engine_amd.so; there is no CPU path. Shapes
+are checked on the host before anything is launched, and a non-zero status
+raises LeError, as the reference launchers throw std::runtime_error.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import LE_BF16, LE_F32, PlanConfig, StepPlan, StepSlice, check
+
+
+def _dt(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return LE_F32
+    if t.dtype == torch.bfloat16:
+        return LE_BF16
+    raise TypeError(f"unsupported dtype {t.dtype}: expected float32 or bfloat16")
+
+
+def _stream(stream) -> ctypes.c_void_p:
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _p(t: torch.Tensor | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _req(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _dev_i32(t: torch.Tensor, name: str, n: int | None = None) -> None:
+    _req(t.is_cuda and t.dtype == torch.int32 and t.is_contiguous(), f"{name}: contiguous int32 cuda tensor")
+    if n is not None:
+        _req(t.numel() >= n, f"{name}: needs {n} entries, has {t.numel()}")
+
+
+def store_kv(k: torch.Tensor, v: torch.Tensor, slots: torch.Tensor, k_cache: torch.Tensor,
+             v_cache: torch.Tensor, stream=None) -> None:
+    """k_cache[slots[t]] = k[t], v likewise (store_kv.cu:20-36). k, v: [N, kv_dim];
+    caches: [num_slots, kv_dim] or [num_slots, kv_heads, head_dim]."""
+    _req(k.shape == v.shape and k.dim() == 2, "k, v: [N, kv_dim]")
+    n, kv_dim = k.shape
+    _req(k_cache.shape == v_cache.shape and k_cache.dtype == v_cache.dtype, "k/v caches must match")
+    num_slots = k_cache.shape[0]
+    _req(k_cache.numel() == num_slots * kv_dim, "cache row size must equal kv_dim")
+    _req(k.is_contiguous() and v.is_contiguous() and k_cache.is_contiguous() and v_cache.is_contiguous(),
+         "contiguous tensors")
+    _dev_i32(slots, "slots", n)
+    check("le_kv_cache_write", _lib.load().le_kv_cache_write(
+        _p(k), _p(v), _dt(k), _p(slots), _p(k_cache), _p(v_cache), _dt(k_cache), n, kv_dim,
+        num_slots, _stream(stream)))
+
+
+def new_workspace(nbytes: int, device="cuda") -> torch.Tensor:
+    """A workspace for the attention calls: zero-filled once, as the ABI requires
+    (the kernels leave its arrival counters at zero after every launch)."""
+    return torch.zeros(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def attention_decode_workspace_size(n_tokens: int, q_heads: int, kv_heads: int, head_dim: int) -> int:
+    return int(_lib.load().le_attention_decode_workspace_size(n_tokens, q_heads, kv_heads, head_dim))
+
+
+def attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                     block_tables: torch.Tensor, table_offset: torch.Tensor,
+                     token_seq: torch.Tensor, token_pos: torch.Tensor, q_heads: int, kv_heads: int,
+                     head_dim: int, block_size: int, scale: float, out: torch.Tensor | None = None,
+                     workspace: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    """Paged attention with the reference launcher's arguments
+    (launch_attention_decode_gqa, cuda_kernels.h:60-64). q: [N, q_heads*head_dim]."""
+    n = q.shape[0]
+    _req(q.is_contiguous() and q.numel() == n * q_heads * head_dim, "q: [N, q_heads*head_dim]")
+    _req(k_cache.shape == v_cache.shape and k_cache.dtype == v_cache.dtype, "k/v caches must match")
+    kv_dim = kv_heads * head_dim
+    _req(k_cache.numel() % (block_size * kv_dim) == 0, "cache must hold whole blocks")
+    num_blocks = k_cache.numel() // (block_size * kv_dim)
+    for name, t in (("block_tables", block_tables), ("table_offset", table_offset),
+                    ("token_seq", token_seq), ("token_pos", token_pos)):
+        _dev_i32(t, name)
+    _req(token_seq.numel() >= n and token_pos.numel() >= n, "token_seq/token_pos: N entries")
+    if out is None:
+        out = torch.empty_like(q)
+    _req(out.dtype == q.dtype and out.shape == q.shape and out.is_contiguous(), "out like q")
+    need = attention_decode_workspace_size(n, q_heads, kv_heads, head_dim)
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.zeros(max(need, 1), dtype=torch.uint8, device=q.device)
+    check("le_attention_decode", _lib.load().le_attention_decode(
+        _p(q), _dt(q), _p(k_cache), _p(v_cache), _dt(k_cache), _p(block_tables), _p(table_offset),
+        _p(token_seq), _p(token_pos), _p(out), n, q_heads, kv_heads, head_dim, block_size,
+        float(scale), num_blocks, _p(workspace), workspace.numel() * workspace.element_size(),
+        _stream(stream)))
+    return out
+
+
+@dataclass
+class Slice:
+    """One scheduler slice (sequence.h:74-80): tokens [start, start+len) of a sequence."""
+    seq_key: int
+    start: int
+    len: int
+    needs_logits: bool
+    blocks: np.ndarray   # int32 block table of the sequence
+    tokens: np.ndarray   # int32 token ids of the sequence
+
+
+class Plan:
+    """A packed step (le_plan_step), its pinned host buffer and its device copy."""
+
+    FIELDS = ("token_ids", "positions", "slots", "token_seq", "tables", "table_offset",
+              "cu_seqlens_q", "seq_lens_k", "logit_rows")
+
+    def __init__(self, slices: list[Slice], q_heads: int, kv_heads: int, head_dim: int,
+                 block_size: int, kv_dtype: torch.dtype, partition_tokens: int = 0,
+                 chunk_partition_tokens: int = 0, device="cuda", pin: bool = True):
+        self.cfg = PlanConfig(q_heads, kv_heads, head_dim, block_size,
+                              LE_BF16 if kv_dtype == torch.bfloat16 else LE_F32,
+                              partition_tokens, 0, chunk_partition_tokens)
+        keep = []
+        arr = (StepSlice * max(1, len(slices)))()
+        for i, s in enumerate(slices):
+            b = np.ascontiguousarray(s.blocks, dtype=np.int32)
+            t = np.ascontiguousarray(s.tokens, dtype=np.int32)
+            keep += [b, t]
+            arr[i] = StepSlice(s.seq_key, s.start, s.len, int(s.needs_logits), b.size,
+                               b.ctypes.data, t.ctypes.data)
+        self.plan = StepPlan()
+        L = _lib.load()
+        st = L.le_plan_step(arr, len(slices), ctypes.byref(self.cfg), None, 0, ctypes.byref(self.plan))
+        _req(st == _lib.LE_ENOSPACE, f"le_plan_step sizing returned {st}")
+        nbytes = int(self.plan.bytes)
+        self.host = torch.empty(nbytes, dtype=torch.uint8, pin_memory=pin and torch.cuda.is_available())
+        check("le_plan_step", L.le_plan_step(arr, len(slices), ctypes.byref(self.cfg),
+                                             ctypes.c_void_p(self.host.data_ptr()), nbytes,
+                                             ctypes.byref(self.plan)))
+        self.device_buf = None
+        self.device = device
+
+    # host views of the packed arrays (numpy int32)
+    def host_array(self, name: str) -> np.ndarray:
+        n = {"token_ids": self.plan.n_tokens, "positions": self.plan.n_tokens,
+             "slots": self.plan.n_tokens, "token_seq": self.plan.n_tokens,
+             "tables": self.plan.n_table, "table_offset": self.plan.n_seqs,
+             "cu_seqlens_q": self.plan.n_slices + 1, "seq_lens_k": self.plan.n_slices,
+             "logit_rows": self.plan.n_logits}[name]
+        off = getattr(self.plan, "off_" + name)
+        return self.host.numpy()[off:off + 4 * n].view(np.int32).copy()
+
+    def upload(self, stream=None) -> "Plan":
+        nbytes = int(self.plan.bytes)
+        if self.device_buf is None or self.device_buf.numel() < nbytes:
+            self.device_buf = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        check("le_plan_upload", _lib.load().le_plan_upload(
+            ctypes.byref(self.plan), ctypes.c_void_p(self.host.data_ptr()),
+            ctypes.c_void_p(self.device_buf.data_ptr()), _stream(stream)))
+        return self
+
+    def dev_array(self, name: str) -> torch.Tensor:
+        n = len(self.host_array(name))
+        off = getattr(self.plan, "off_" + name)
+        return self.device_buf[off:off + 4 * n].view(torch.int32)
+
+    def workspace_size(self) -> int:
+        return int(_lib.load().le_ragged_workspace_size(ctypes.byref(self.plan)))
+
+
+def ragged_paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                           plan: Plan, scale: float, out: torch.Tensor | None = None,
+                           workspace: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+    P = plan.plan
+    cfg = P.cfg
+    n = P.n_tokens
+    _req(plan.device_buf is not None, "plan not uploaded")
+    _req(q.is_contiguous() and q.numel() == n * cfg.q_heads * cfg.head_dim, "q: [N, q_heads*head_dim]")
+    kv_dim = cfg.kv_heads * cfg.head_dim
+    _req(k_cache.shape == v_cache.shape and k_cache.dtype == v_cache.dtype, "k/v caches must match")
+    num_blocks = k_cache.numel() // (cfg.block_size * kv_dim)
+    if out is None:
+        out = torch.empty_like(q)
+    need = plan.workspace_size()
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.zeros(max(need, 1), dtype=torch.uint8, device=q.device)
+    check("le_ragged_paged_attention", _lib.load().le_ragged_paged_attention(
+        _p(q), _dt(q), _p(k_cache), _p(v_cache), _dt(k_cache), num_blocks, ctypes.byref(P),
+        float(scale), _p(out), _p(workspace), workspace.numel() * workspace.element_size(),
+        _stream(stream)))
+    return out

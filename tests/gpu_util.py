@@ -1,0 +1,50 @@
+"""Helpers for GPU parity tests: move a seeded case to the device, run the
+oracle on exactly the inputs the device sees."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+import oracle
+from cases import AttnCase
+
+
+def to_dev_cache(c: np.ndarray, dev) -> torch.Tensor:
+    if c.dtype == np.uint16:
+        return torch.from_numpy(c.view(np.int16)).to(dev).view(torch.bfloat16)
+    return torch.from_numpy(c).to(dev)
+
+
+def i32(a, dev) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).to(dev)
+
+
+def device_q(case: AttnCase, act: torch.dtype, dev) -> tuple[torch.Tensor, np.ndarray]:
+    """The device q in `act`, and the fp32 values the device actually holds."""
+    if act == torch.bfloat16:
+        qh = oracle.bf16_to_f32(oracle.f32_to_bf16(case.q))
+        return torch.from_numpy(qh).to(dev).to(torch.bfloat16), qh
+    return torch.from_numpy(case.q).to(dev), case.q
+
+
+def oracle_out(case: AttnCase, q_f32: np.ndarray) -> np.ndarray:
+    return oracle.paged_attention(q_f32, case.k_cache, case.v_cache, case.tables,
+                                  case.table_offset, case.token_seq, case.token_pos, case.q_heads,
+                                  case.kv_heads, case.head_dim, case.block_size, case.scale)
+
+
+def max_abs(a, b) -> float:
+    return float(np.max(np.abs(np.asarray(a, dtype=np.float64) - np.asarray(b, dtype=np.float64))))
+
+
+def slices_of(case: AttnCase):
+    """Scheduler-style slices for a case (one per sequence, prefill chunks and
+    decode rows in case order); token ids are irrelevant to attention."""
+    from llm_engine_amd.kernels import Slice
+    out = []
+    for s in range(len(case.table_len)):
+        start = int(case.seq_start[s])
+        ln = int(case.seq_qlen[s])
+        out.append(Slice(s, start, ln, True, case.blocks_of(s),
+                         np.zeros(start + ln, dtype=np.int32)))
+    return out

@@ -1,0 +1,165 @@
+"""Host-side checks of the C ABI (no GPU needed): the library loads and
+exports exactly what include/llm_engine_amd.h declares, argument validation
+returns the documented codes without launching anything, and the step packer
+(le_plan_step) reproduces the reference's packing bit for bit on steps the
+reference's own scheduler produced (tests/golden/schedule_ref.npz)."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from cases import parse_trace
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def declared_symbols():
+    syms = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        for m in re.finditer(r"^\s*(?!static)[A-Za-z_][\w\s\*]*?\b(le_\w+)\s*\(", text, flags=re.M):
+            syms.add(m.group(1))
+    return syms
+
+
+def test_library_exports_every_declared_symbol():
+    from llm_engine_amd import _lib
+    lib = _lib.load()
+    syms = declared_symbols()
+    assert {"le_kv_cache_write", "le_attention_decode", "le_plan_step",
+            "le_ragged_paged_attention"} <= syms
+    for s in sorted(syms):
+        assert hasattr(lib, s), s
+    assert set(_lib.SIGNATURES) == syms
+    assert b"gfx950" in lib.le_version()
+
+
+def test_validation_codes_without_launch():
+    from llm_engine_amd import _lib
+    L = _lib.load()
+    nul = ctypes.c_void_p(0)
+    assert L.le_kv_cache_write(nul, nul, 0, nul, nul, nul, 0, 0, 128, 10, nul) == _lib.LE_OK
+    assert L.le_kv_cache_write(nul, nul, 0, nul, nul, nul, 0, 4, 100, 10, nul) == _lib.LE_EUNSUPPORTED
+    assert L.le_kv_cache_write(nul, nul, 0, nul, nul, nul, 0, 4, 128, 10, nul) == _lib.LE_EINVAL
+    assert L.le_kv_cache_write(nul, nul, 7, nul, nul, nul, 0, 4, 128, 10, nul) == _lib.LE_EINVAL
+    args = lambda qh, kvh, hd, bs: (nul, 0, nul, nul, 0, nul, nul, nul, nul, nul, 3, qh, kvh, hd, bs,
+                                    0.125, 100, nul, 0, nul)
+    assert L.le_attention_decode(*args(14, 2, 64, 16)) == _lib.LE_EINVAL          # null pointers
+    assert L.le_attention_decode(*args(14, 3, 64, 16)) == _lib.LE_EINVAL          # heads not divisible
+    assert L.le_attention_decode(*args(18, 2, 64, 16)) == _lib.LE_EUNSUPPORTED    # group 9
+    assert L.le_attention_decode(*args(14, 2, 96, 16)) == _lib.LE_EUNSUPPORTED    # head_dim 96
+    assert L.le_attention_decode(*args(14, 2, 64, 12)) == _lib.LE_EUNSUPPORTED    # block 12
+    assert L.le_status_string(_lib.LE_ENOSPACE) == b"buffer too small"
+
+
+def _plan(slices, kv=torch.bfloat16, **kw):
+    from llm_engine_amd import kernels
+    return kernels.Plan(slices, 14, 2, 64, 16, kv, device="cpu", pin=False, **kw)
+
+
+def _items(plan, kind):
+    P = plan.plan
+    n, w, off = {"decode": (P.n_decode_items, 8, P.off_decode_items),
+                 "chunk": (P.n_chunk_items, 8, P.off_chunk_items),
+                 "combine": (P.n_combine_items, 4, P.off_combine_items)}[kind]
+    return plan.host.numpy()[off:off + 4 * n * w].view(np.int32).reshape(n, w)
+
+
+def check_work_lists(plan, slices, bs=16):
+    P = plan.plan
+    dec, chk, cmb = _items(plan, "decode"), _items(plan, "chunk"), _items(plan, "combine")
+    pos = plan.host_array("positions")
+    toff = plan.host_array("table_offset")
+    tseq = plan.host_array("token_seq")
+    # decode items: per row, [blk_begin, blk_end) ranges tile [0, pos/bs] exactly once
+    rows = {}
+    for it in dec:
+        token, p, to, b0, b1, part, pb, npart = (int(x) for x in it)
+        assert p == pos[token] and to == toff[tseq[token]]
+        rows.setdefault(token, []).append((b0, b1, part, pb, npart))
+    for token, items in rows.items():
+        items.sort()
+        assert items[0][0] == 0 and items[-1][1] == pos[token] // bs + 1
+        for a, b in zip(items, items[1:]):
+            assert a[1] == b[0]
+        npart = items[0][4]
+        assert len(items) == npart
+        if npart == 1:
+            assert items[0][2] == -1
+        else:
+            assert sorted(i[2] for i in items) == list(range(items[0][3], items[0][3] + npart))
+    # chunk items: each tile's partitions tile the keys up to its last row
+    tiles = {}
+    for it in chk:
+        tb, nq, b0, b1, p0, stride, seq, _ = (int(x) for x in it)
+        tiles.setdefault(tb, []).append((b0, b1, p0, stride, nq))
+    for tb, items in tiles.items():
+        items.sort()
+        nq = items[0][4]
+        assert items[0][0] == 0 and items[-1][1] == pos[tb + nq - 1] // bs + 1
+        for a, b in zip(items, items[1:]):
+            assert a[1] == b[0]
+    # every partial index is owned exactly once
+    owned = []
+    for it in dec:
+        if it[5] >= 0:
+            owned.append(int(it[5]))
+    for it in chk:
+        if it[4] >= 0:
+            owned += [int(it[4]) + r * int(it[5]) for r in range(int(it[1]))]
+    assert sorted(owned) == list(range(P.n_parts))
+    for it in cmb:
+        assert int(it[2]) > 1
+
+
+TRACES = np.load(ROOT / "tests" / "golden" / "schedule_ref.npz")
+TRACE_NAMES = sorted({k.split(".")[0] for k in TRACES.files})
+
+
+@pytest.mark.parametrize("name", TRACE_NAMES)
+@pytest.mark.parametrize("kv", [torch.bfloat16, torch.float32])
+def test_packer_matches_reference_on_scheduler_steps(name, kv):
+    """Every step the reference Scheduler built (fragmented pool, chunked
+    prefill, preemption, token budget, prefix caching): token ids, positions,
+    int32 slots, token->sequence, concatenated tables + offsets and logit rows
+    equal the reference packing (restated in the oracle, cuda_model.cu:434-491);
+    cu_seqlens/seq_lens and the work lists are consistent."""
+    from llm_engine_amd.kernels import Slice
+    steps, toks = parse_trace(TRACES[f"{name}.trace"])
+    assert len(steps) > 3
+    for st in steps:
+        slices = [Slice(sid, start, ln, bool(nl), blocks, toks[sid]) for sid, start, ln, nl, pf, blocks in st]
+        plan = _plan(slices, kv=kv)
+        want = oracle.pack_step([(s.seq_key, s.start, s.len, s.needs_logits, s.blocks, s.tokens)
+                                 for s in slices], 16)
+        for f in ("token_ids", "positions", "slots", "token_seq", "tables", "table_offset", "logit_rows"):
+            assert np.array_equal(plan.host_array(f), getattr(want, f)), (name, f)
+        cu = plan.host_array("cu_seqlens_q")
+        assert np.array_equal(np.diff(cu), [s.len for s in slices])
+        assert np.array_equal(plan.host_array("seq_lens_k"), [s.start + s.len for s in slices])
+        check_work_lists(plan, slices)
+
+
+def test_slot_closed_form_and_fragmentation():
+    """kv_cache.h:29-31 on a fragmented table (test_block_allocator.cpp:39)."""
+    from llm_engine_amd.kernels import Slice
+    rng = np.random.default_rng(3)
+    blocks = rng.permutation(4096)[:40].astype(np.int32)
+    toks = np.arange(640, dtype=np.int32)
+    plan = _plan([Slice(1, 0, 640, True, blocks, toks)], kv=torch.float32)
+    p = np.arange(640)
+    assert np.array_equal(plan.host_array("slots"), blocks[p // 16] * 16 + p % 16)
+
+
+def test_plan_errors():
+    from llm_engine_amd import _lib
+    from llm_engine_amd.kernels import Slice
+    with pytest.raises(ValueError):  # position 32 has no block
+        _plan([Slice(1, 0, 33, True, np.array([3, 4], np.int32), np.zeros(33, np.int32))])
+    # an empty step packs to an empty plan
+    plan = _plan([])
+    assert plan.plan.n_tokens == 0 and plan.plan.n_decode_items == 0

@@ -1,0 +1,154 @@
+"""GPU parity of paged attention (reference-shaped entry and ragged plan)
+against the CPU oracle (oracle.c, restating ops.h:87-111) on identical inputs.
+
+Tolerances (max-abs against the fp32 oracle): 1e-3 with fp32 K/V, 2e-2 with
+bf16 K/V. With bf16 activations the oracle is fed the same bf16-rounded q, and
+the output's own bf16 rounding (<= 2^-9 relative, |out| < 4 here) is added."""
+import numpy as np
+import pytest
+import torch
+
+from cases import loguniform_ctx, make_case
+from gpu_util import device_q, i32, max_abs, oracle_out, slices_of, to_dev_cache
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-3
+TOL_BF16 = 2e-2
+TOL_BF16_OUT = 2e-2 + 4 * 2.0 ** -9
+
+
+def run_decode(case, act, dev):
+    from llm_engine_amd import kernels
+    q, qh = device_q(case, act, dev)
+    kc, vc = to_dev_cache(case.k_cache, dev), to_dev_cache(case.v_cache, dev)
+    out = kernels.attention_decode(q, kc, vc, i32(case.tables, dev), i32(case.table_offset, dev),
+                                   i32(case.token_seq, dev), i32(case.token_pos, dev),
+                                   case.q_heads, case.kv_heads, case.head_dim, case.block_size,
+                                   case.scale)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy(), qh
+
+
+def run_ragged(case, act, dev, **plan_kw):
+    from llm_engine_amd import kernels
+    q, qh = device_q(case, act, dev)
+    kc, vc = to_dev_cache(case.k_cache, dev), to_dev_cache(case.v_cache, dev)
+    plan = kernels.Plan(slices_of(case), case.q_heads, case.kv_heads, case.head_dim,
+                        case.block_size, kc.dtype, **plan_kw).upload()
+    out = kernels.ragged_paged_attention(q, kc, vc, plan, case.scale)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy(), qh, plan
+
+
+def tol_for(kv_bf16, act):
+    if act == torch.bfloat16:
+        return TOL_BF16_OUT
+    return TOL_BF16 if kv_bf16 else TOL_F32
+
+
+@pytest.mark.parametrize("kv_bf16", [False, True])
+@pytest.mark.parametrize("act", [torch.float32, torch.bfloat16])
+def test_decode_config2_shape(gpu, kv_bf16, act):
+    """Config 2 at full size: 64 seqs, ctx log-uniform in [64, 4096], tables
+    from a 32768-block pool, Qwen2.5-0.5B GQA shape."""
+    rng = np.random.default_rng(2)
+    ctx = loguniform_ctx(rng, 64, 64, 4096)
+    case = make_case(ctx, num_blocks=32768, seed=2, kv_bf16=kv_bf16)
+    got, qh = run_decode(case, act, gpu)
+    want = oracle_out(case, qh)
+    err = max_abs(got, want)
+    print(f"config2 kv_bf16={kv_bf16} act={act}: max|err|={err:.3e}")
+    assert err < tol_for(kv_bf16, act)
+
+
+@pytest.mark.parametrize("kv_bf16", [False, True])
+def test_ragged_equals_reference_shaped(gpu, kv_bf16):
+    rng = np.random.default_rng(5)
+    ctx = loguniform_ctx(rng, 40, 1, 3000)
+    case = make_case(ctx, num_blocks=8192, seed=5, kv_bf16=kv_bf16)
+    a, qh = run_decode(case, torch.float32, gpu)
+    b, _, plan = run_ragged(case, torch.float32, gpu)
+    want = oracle_out(case, qh)
+    tol = tol_for(kv_bf16, torch.float32)
+    assert max_abs(a, want) < tol
+    assert max_abs(b, want) < tol
+    assert plan.plan.n_chunk_items == 0
+
+
+@pytest.mark.parametrize("q_heads,kv_heads,head_dim", [(32, 4, 64), (8, 8, 64), (16, 2, 128), (4, 1, 128)])
+@pytest.mark.parametrize("kv_bf16", [False, True])
+def test_decode_other_shapes(gpu, q_heads, kv_heads, head_dim, kv_bf16):
+    """GQA group 8 (TinyLlama), no grouping, head_dim 128."""
+    rng = np.random.default_rng(q_heads * 100 + head_dim)
+    ctx = loguniform_ctx(rng, 12, 1, 2500)
+    case = make_case(ctx, q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim,
+                     num_blocks=4096, seed=7, kv_bf16=kv_bf16)
+    got, qh = run_decode(case, torch.float32, gpu)
+    assert max_abs(got, oracle_out(case, qh)) < tol_for(kv_bf16, torch.float32)
+    got2, _, _ = run_ragged(case, torch.float32, gpu)
+    assert max_abs(got2, oracle_out(case, qh)) < tol_for(kv_bf16, torch.float32)
+
+
+@pytest.mark.parametrize("block_size", [8, 32, 64])
+def test_decode_block_sizes(gpu, block_size):
+    rng = np.random.default_rng(block_size)
+    ctx = loguniform_ctx(rng, 10, 1, 2000)
+    case = make_case(ctx, block_size=block_size, num_blocks=2048, seed=block_size)
+    got, qh = run_decode(case, torch.float32, gpu)
+    assert max_abs(got, oracle_out(case, qh)) < TOL_F32
+    got2, _, _ = run_ragged(case, torch.float32, gpu)
+    assert max_abs(got2, oracle_out(case, qh)) < TOL_F32
+
+
+def test_decode_edges(gpu):
+    """pos 0 (one key), exact block multiples, one row past a boundary, and a
+    long 8192 context (several 512-position LDS chunks in one workgroup)."""
+    ctx = [1, 2, 15, 16, 17, 32, 33, 511, 512, 513, 8192]
+    case = make_case(ctx, num_blocks=1024, seed=11)
+    got, qh = run_decode(case, torch.float32, gpu)
+    want = oracle_out(case, qh)
+    assert max_abs(got, want) < TOL_F32
+    # one partition covering the whole context: exercises the chunked online rescale
+    got2, _, plan = run_ragged(case, torch.float32, gpu, partition_tokens=16384)
+    assert plan.plan.n_combine_items == 0
+    assert max_abs(got2, want) < TOL_F32
+    # pos 0 attends to exactly one key: output equals that V row
+    v0 = case.v_cache[case.blocks_of(0)[0] * 16, :64]
+    assert max_abs(got[0, :64], v0) < 1e-6
+
+
+@pytest.mark.parametrize("kv_bf16", [False, True])
+def test_chunk_rows_small(gpu, kv_bf16):
+    """Prefill chunks (causal inside the chunk, over a cached prefix) beside
+    decode rows. bf16 K/V runs the MFMA chunk kernel, fp32 the decode kernel."""
+    ctx = [40, 97, 160, 300, 64, 500]
+    q_len = [1, 1, 64, 37, 64, 17]   # chunk at offsets 0, 263, 96, 483
+    case = make_case(ctx, q_len=q_len, num_blocks=1024, seed=13, kv_bf16=kv_bf16)
+    got, qh, plan = run_ragged(case, torch.float32, gpu)
+    want = oracle_out(case, qh)
+    err = max_abs(got, want)
+    print(f"chunk rows kv_bf16={kv_bf16}: items dec={plan.plan.n_decode_items} "
+          f"chunk={plan.plan.n_chunk_items} max|err|={err:.3e}")
+    assert (plan.plan.n_chunk_items > 0) == kv_bf16
+    assert err < tol_for(kv_bf16, torch.float32)
+    ref_shaped, _ = run_decode(case, torch.float32, gpu)
+    assert max_abs(ref_shaped, want) < tol_for(kv_bf16, torch.float32)
+
+
+@pytest.mark.parametrize("act", [torch.float32, torch.bfloat16])
+def test_mixed_step_config3(gpu, act):
+    """Config 3: 32 decode rows (ctx U[256, 2048]) + 2 prefill chunks of 512
+    at cached offsets 0 and 1024, bf16 K/V: 32 + 2 * 512 = 1056 ragged rows."""
+    rng = np.random.default_rng(3)
+    dec_ctx = rng.integers(256, 2049, size=32)
+    ctx = [512, 1536] + list(dec_ctx)
+    q_len = [512, 512] + [1] * 32
+    case = make_case(ctx, q_len=q_len, num_blocks=16384, seed=3, kv_bf16=True)
+    got, qh, plan = run_ragged(case, act, gpu)
+    assert plan.plan.n_tokens == 1056
+    assert plan.plan.n_chunk_items > 0
+    want = oracle_out(case, qh)
+    err = max_abs(got, want)
+    print(f"config3 act={act}: max|err|={err:.3e}")
+    assert err < tol_for(True, act)
