@@ -128,6 +128,9 @@ typedef struct le_step_plan {
   int64_t off_token_ids, off_positions, off_slots, off_token_seq, off_tables,
       off_table_offset, off_cu_seqlens_q, off_seq_lens_k, off_logit_rows, off_decode_items,
       off_chunk_items, off_combine_items;
+  int64_t off_decode_ids;     /* block ids of each decode item, decode_ids_stride apart */
+  int32_t decode_ids_stride;  /* entries per decode item in that array (padded with -1) */
+  int32_t reserved1_;
   int64_t bytes;         /* total size of the packed buffer */
   const void* dev;       /* device copy, set by le_plan_upload */
 } le_step_plan;

@@ -170,6 +170,8 @@ int le_ragged_paged_attention(const void* q, le_dtype act_dtype, const void* k_c
   d.token_seq = arr(plan->off_token_seq); d.token_pos = arr(plan->off_positions);
   d.out = out; d.parts = parts;
   d.items = reinterpret_cast<const le::DecodeItem*>(dev + plan->off_decode_items);
+  d.item_ids = arr(plan->off_decode_ids);
+  d.ids_stride = plan->decode_ids_stride;
   d.n_rows = plan->n_decode_items; d.nsplit = 1;
   d.q_heads = cfg.q_heads; d.kv_heads = cfg.kv_heads; d.head_dim = cfg.head_dim;
   d.block_size = cfg.block_size; d.scale_log2 = scale_log2; d.num_cache_blocks = num_cache_blocks;

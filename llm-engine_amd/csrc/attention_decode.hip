@@ -54,6 +54,15 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+#ifdef LE_PROBE_TIMING
+// Diagnostic build only: per-workgroup phase timestamps (100 MHz counter).
+__device__ uint64_t g_probe_ts[16384][8];
+#define PROBE_TS(k) do { if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 16384) \
+    g_probe_ts[blockIdx.x][k] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define PROBE_TS(k) do {} while (0)
+#endif
+
 struct Work {
   int token, pos, table_off, b_begin, b_end, part, part_begin, n_parts;
   bool valid;
@@ -119,11 +128,13 @@ __device__ __forceinline__ void finish(const DecodeParams& p, const Work& w, int
   }
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are performed
   __syncthreads();                // ... and every other thread's
+  PROBE_TS(4);
   int32_t* counter = p.parts.counters + static_cast<int64_t>(w.token) * p.kv_heads + kvh;
   if (tid == 0)
     *flag = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
             w.n_parts - 1;
   __syncthreads();
+  PROBE_TS(5);
   if (!*flag) return;
   // Every other partition incremented the counter after its partial was
   // performed, so the coherent loads below see all of them. The loads are
@@ -132,10 +143,26 @@ __device__ __forceinline__ void finish(const DecodeParams& p, const Work& w, int
   // latencies, not one per partition.
   const int np = w.n_parts;
   const int64_t rbase = static_cast<int64_t>(w.part_begin) * p.q_heads + kvh * G;
+  // Every (m, l) pair and every accumulator value is requested before any is
+  // used: one memory round trip for the whole merge (np <= kMergeBatch per
+  // batch of accumulators; more partitions take more batches).
   for (int i = tid; i < np * G; i += kThreads) {
     const int j = i / G, g = i - j * G;
     const float* r = ml + (rbase + static_cast<int64_t>(j) * p.q_heads + g) * 2;
     merge_w[i] = make_float2(ld_dev(r), ld_dev(r + 1));  // (m, l) of partition j, head g
+  }
+  constexpr int kOutPerThread = (kMaxG * HD + kThreads - 1) / kThreads;
+  float o[kOutPerThread];
+  float v0[kOutPerThread][kMergeBatch];
+#pragma unroll
+  for (int u = 0; u < kOutPerThread; u++) {
+    o[u] = 0.f;
+    const int i = min(tid + u * kThreads, G * HD - 1);
+#pragma unroll
+    for (int b = 0; b < kMergeBatch; b++) {
+      const int j = min(b, np - 1);
+      v0[u][b] = ld_dev(p.parts.acc + (rbase + static_cast<int64_t>(j) * p.q_heads) * HD + i);
+    }
   }
   __syncthreads();
   if (tid < G) {
@@ -151,22 +178,26 @@ __device__ __forceinline__ void finish(const DecodeParams& p, const Work& w, int
     merge_w[i].x = exp2f(merge_w[i].x - merge_ml[g].x) * merge_ml[g].y;
   }
   __syncthreads();
-  for (int i = tid; i < G * HD; i += kThreads) {
+#pragma unroll
+  for (int u = 0; u < kOutPerThread; u++) {
+    const int i = tid + u * kThreads;
+    if (i >= G * HD) continue;
     const int g = i / HD;
-    float o = 0.f;
-    for (int j0 = 0; j0 < np; j0 += kMergeBatch) {
+#pragma unroll
+    for (int b = 0; b < kMergeBatch; b++)
+      if (b < np) o[u] += v0[u][b] * merge_w[b * G + g].x;
+    for (int j0 = kMergeBatch; j0 < np; j0 += kMergeBatch) {
       float v[kMergeBatch];
 #pragma unroll
-      for (int u = 0; u < kMergeBatch; u++) {
-        const int j = min(j0 + u, np - 1);
-        v[u] = ld_dev(p.parts.acc + (rbase + static_cast<int64_t>(j) * p.q_heads) * HD + i);
-      }
+      for (int b = 0; b < kMergeBatch; b++)
+        v[b] = ld_dev(p.parts.acc + (rbase + static_cast<int64_t>(min(j0 + b, np - 1)) * p.q_heads) * HD + i);
 #pragma unroll
-      for (int u = 0; u < kMergeBatch; u++)
-        if (j0 + u < np) o += v[u] * merge_w[(j0 + u) * G + g].x;
+      for (int b = 0; b < kMergeBatch; b++)
+        if (j0 + b < np) o[u] += v[b] * merge_w[(j0 + b) * G + g].x;
     }
-    elem<ACT>::store1(static_cast<ACT*>(p.out) + head0 * HD + i, o);
+    elem<ACT>::store1(static_cast<ACT*>(p.out) + head0 * HD + i, o[u]);
   }
+  PROBE_TS(6);
   if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -174,8 +205,8 @@ __device__ __forceinline__ void finish(const DecodeParams& p, const Work& w, int
 // bf16 cache: MFMA kernel
 // ---------------------------------------------------------------------------
 template <int HD> struct MfmaLds {
-  static constexpr int VT_STRIDE = kTile * 2 + 8;        // bytes per dim row of V^T
-  static constexpr int VT_BYTES = HD * VT_STRIDE;        // per wave
+  static constexpr int V_STRIDE = HD * 2 + 16;           // bytes per key row of the V tile
+  static constexpr int VT_BYTES = kTile * V_STRIDE;      // per wave
   static constexpr int RED_STRIDE = HD + 4;              // floats per head in the merge area
   static constexpr int RED_BYTES = kWaves * kMaxG * RED_STRIDE * 4;
   static constexpr int BYTES = (kWaves * VT_BYTES > RED_BYTES ? kWaves * VT_BYTES : RED_BYTES);
@@ -185,6 +216,16 @@ constexpr int kTabCap = 1024;  // block ids of a partition staged in LDS
 
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+// ds_read_b64_tr_b16: in each group of 16 lanes, lane i receives 16-bit
+// element (i % 4) of the 8-byte chunks addressed by lanes 4j + i/4, j = 0..3.
+__device__ __forceinline__ bf16x4 lds_read_tr(const char* p) {
+  // C-style cast: the generic LDS pointer becomes an address-space-3 pointer.
+  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) i16x4*)(p));
+  return __builtin_bit_cast(bf16x4, v);
 }
 
 // One wave's K/V registers for a 64-key tile: this lane's key of each of the
@@ -238,6 +279,17 @@ __device__ __forceinline__ void compute_tile(WaveAcc<HD>& st, const TileRegs<HD 
   using L = MfmaLds<HD>;
   constexpr int KS = HD / 32;
   constexpr int DT = HD / 16;
+#ifdef LE_PROBE_NOCOMPUTE
+  // Measurement variant: consume the loads, skip the attention arithmetic.
+  uint32_t x = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) x ^= r.k[i][ks].x ^ r.k[i][ks].w ^ r.v[i][ks].y ^ r.v[i][ks].z;
+  st.acc[0][0] += __uint_as_float(x & 0x3fffffff) * 1e-30f;
+  st.l += 1.f;
+  return;
+#endif
   // S^T = K . Q^T: lane holds head `col`, keys key0 + 16i + 4grp + j
   f32x4 s[4];
 #pragma unroll
@@ -275,25 +327,26 @@ __device__ __forceinline__ void compute_tile(WaveAcc<HD>& st, const TileRegs<HD 
 #pragma unroll
   for (int d = 0; d < DT; d++) st.acc[d] *= alpha;
 
-  // V^T into this wave's LDS tile: row = dim, column = key. A dead key's V
-  // row is replaced by zeros (its p is 0, but the row read may hold NaNs).
+  // V rows into this wave's LDS tile, row-major (key rows), with 16-byte
+  // stores. A dead key's row is replaced by zeros (its p is 0, but the row
+  // read may hold NaNs).
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
     for (int ks = 0; ks < KS; ks++) {
       const bool vlive = key0 + i * 16 + col < key_end && r.ok[i];
-      const uint32_t wv[4] = {vlive ? r.v[i][ks].x : 0u, vlive ? r.v[i][ks].y : 0u,
-                              vlive ? r.v[i][ks].z : 0u, vlive ? r.v[i][ks].w : 0u};
-#pragma unroll
-      for (int e = 0; e < 8; e++)
-        *reinterpret_cast<uint16_t*>(vt + (ks * 32 + grp * 8 + e) * L::VT_STRIDE + (i * 16 + col) * 2) =
-            static_cast<uint16_t>(wv[e >> 1] >> ((e & 1) * 16));
+      *reinterpret_cast<uint4*>(vt + (i * 16 + col) * L::V_STRIDE + (ks * 32 + grp * 8) * 2) =
+          vlive ? r.v[i][ks] : make_uint4(0, 0, 0, 0);
     }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  // O^T += V^T . P^T over the tile (2 k-steps of 32 keys)
+  // O^T += V^T . P^T over the tile (2 k-steps of 32 keys). The A operand
+  // (16 dims x 8 keys per lane group) comes from the row-major tile through
+  // the transposing LDS read: lane (col, grp) addresses key row
+  // kk*32 + 4*grp + col/4 (then +16) at dims 16*d + 4*(col%4) and receives
+  // dim 16*d + col of four keys, the same keys P^T holds for that group.
 #pragma unroll
   for (int kk = 0; kk < 2; kk++) {
     bf16x8 pb;
@@ -302,11 +355,12 @@ __device__ __forceinline__ void compute_tile(WaveAcc<HD>& st, const TileRegs<HD 
       pb[j] = static_cast<__bf16>(s[2 * kk][j]);
       pb[4 + j] = static_cast<__bf16>(s[2 * kk + 1][j]);
     }
+    const char* r_lo = vt + (kk * 32 + grp * 4 + (col >> 2)) * L::V_STRIDE + (col & 3) * 8;
+    const char* r_hi = r_lo + 16 * L::V_STRIDE;
 #pragma unroll
     for (int d = 0; d < DT; d++) {
-      const char* row = vt + (d * 16 + col) * L::VT_STRIDE;
-      const bf16x4 lo = *reinterpret_cast<const bf16x4*>(row + (kk * 32 + grp * 4) * 2);
-      const bf16x4 hi = *reinterpret_cast<const bf16x4*>(row + (kk * 32 + 16 + grp * 4) * 2);
+      const bf16x4 lo = lds_read_tr(r_lo + d * 32);
+      const bf16x4 hi = lds_read_tr(r_hi + d * 32);
       const bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       st.acc[d] = mfma16(a, pb, st.acc[d]);
     }
@@ -331,8 +385,27 @@ __global__ __launch_bounds__(kThreads) void mfma_kernel(DecodeParams p) {
   __shared__ int tab[kTabCap];
   __shared__ int flag;
 
+  PROBE_TS(0);
+  // With a plan, the item's block ids sit at a fixed stride: fetch them now,
+  // in the same memory round trip as the item itself.
+  const bool item_ids = p.items != nullptr && p.item_ids != nullptr && p.ids_stride <= kTabCap;
+  constexpr int kIdsPerThread = kTabCap / kThreads;
+  int pre_ids[kIdsPerThread];
+  if (item_ids) {
+    const int32_t* ids = p.item_ids + static_cast<int64_t>(blockIdx.x) * p.ids_stride;
+#pragma unroll
+    for (int u = 0; u < kIdsPerThread; u++) {
+      const int i = threadIdx.x + u * kThreads;
+      pre_ids[u] = i < p.ids_stride ? ids[i] : -1;
+    }
+  }
   const Work w = resolve(p);
   if (!w.valid) return;
+#ifdef LE_PROBE_TIMING
+  if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 16384) {
+    g_probe_ts[blockIdx.x][4] = __builtin_amdgcn_s_memrealtime() + (w.token & 0) ;
+  }
+#endif
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
@@ -365,6 +438,17 @@ __global__ __launch_bounds__(kThreads) void mfma_kernel(DecodeParams p) {
   for (int d = 0; d < DT; d++) st.acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
   st.m = -FLT_MAX;
   st.l = 0.f;
+#ifdef LE_PROBE_TIMING
+  {
+    float qs = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) qs += static_cast<float>(qb[ks][0]);
+    if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 16384)
+      g_probe_ts[blockIdx.x][5] = __builtin_amdgcn_s_memrealtime() + (qs == 12345.f);
+    if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 16384)
+      g_probe_ts[blockIdx.x][6] = __builtin_amdgcn_s_memrealtime() + (pre_ids[0] == 12345);
+  }
+#endif
 
   const int bs_shift = __builtin_ctz(bs);  // block sizes are powers of two
   const int stride = kWaves * kTile;
@@ -373,11 +457,20 @@ __global__ __launch_bounds__(kThreads) void mfma_kernel(DecodeParams p) {
   for (int sb0 = w.b_begin; sb0 < w.b_end; sb0 += kTabCap) {
     const int sb1 = min(w.b_end, sb0 + kTabCap);
     __syncthreads();  // the previous segment's table is no longer read
-    for (int i = tid; i < sb1 - sb0; i += kThreads) {
-      const int bid = gtab[sb0 + i];
-      tab[i] = (bid >= 0 && bid < p.num_cache_blocks) ? bid : -1;
+    if (item_ids) {  // one segment: the whole item (ids_stride <= kTabCap)
+#pragma unroll
+      for (int u = 0; u < kIdsPerThread; u++) {
+        const int bid = pre_ids[u];
+        tab[tid + u * kThreads] = (bid >= 0 && bid < p.num_cache_blocks) ? bid : -1;
+      }
+    } else {
+      for (int i = tid; i < sb1 - sb0; i += kThreads) {
+        const int bid = gtab[sb0 + i];
+        tab[i] = (bid >= 0 && bid < p.num_cache_blocks) ? bid : -1;
+      }
     }
     __syncthreads();
+    PROBE_TS(1);
     const int key_end = min(sb1 << bs_shift, w.pos + 1);
     int key0 = (sb0 << bs_shift) + wave * kTile;
     if (key0 >= key_end) continue;
@@ -408,6 +501,7 @@ __global__ __launch_bounds__(kThreads) void mfma_kernel(DecodeParams p) {
     }
   }
 
+  PROBE_TS(2);
   // ---- merge the four waves ----
   float l_tot = st.l + __shfl_xor(st.l, 16, kWave);
   l_tot += __shfl_xor(l_tot, 32, kWave);
@@ -447,7 +541,9 @@ __global__ __launch_bounds__(kThreads) void mfma_kernel(DecodeParams p) {
     fin_acc[i] = o;
   }
   __syncthreads();
+  PROBE_TS(3);
   finish<ACT, HD>(p, w, G, kvh, fin_acc, fin_ml, merge_ml, merge_w, &flag);
+  PROBE_TS(7);
 }
 
 // ---------------------------------------------------------------------------
@@ -711,6 +807,16 @@ hipError_t dispatch(const DecodeParams& p, int kv_bf16, hipStream_t s) {
 }
 
 }  // namespace
+
+#ifdef LE_PROBE_TIMING
+extern "C" int le_probe_timing(void* host, size_t bytes) {
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_probe_ts), bytes < sizeof(g_probe_ts) ? bytes : sizeof(g_probe_ts)) == hipSuccess ? 0 : 1;
+}
+extern "C" int le_probe_timing_clear(void) {
+  static uint64_t zeros[16384][8];
+  return hipMemcpyToSymbol(HIP_SYMBOL(g_probe_ts), zeros, sizeof(zeros)) == hipSuccess ? 0 : 1;
+}
+#endif
 
 int decode_nsplit(int n_tokens, int kv_heads) {
   const int rows = n_tokens * kv_heads;

@@ -55,6 +55,8 @@ struct DecodeParams {
   void* out;
   PartialLayout parts;
   const DecodeItem* items;  // null: one item per (token, split) with `nsplit` splits
+  const int32_t* item_ids;  // with items: block ids of item i at item_ids[i * ids_stride + j]
+  int ids_stride;
   int n_rows;               // items, or tokens when items is null
   int nsplit;
   int q_heads, kv_heads, head_dim, block_size;

@@ -73,6 +73,9 @@ class StepPlan(ctypes.Structure):
         ("off_decode_items", ctypes.c_int64),
         ("off_chunk_items", ctypes.c_int64),
         ("off_combine_items", ctypes.c_int64),
+        ("off_decode_ids", ctypes.c_int64),
+        ("decode_ids_stride", ctypes.c_int32),
+        ("reserved1_", ctypes.c_int32),
         ("bytes", ctypes.c_int64),
         ("dev", ctypes.c_void_p),
     ]
