@@ -77,6 +77,17 @@ def chunk_flops(ctx, q_len):
     return 4 * Q_HEADS * HEAD_DIM * f
 
 
+def measured_traffic(workload: str, kv: str):
+    """HBM bytes per attention launch from the committed rocprofv3 PMC summary
+    (profiles/traffic.json: FETCH_SIZE and WRITE_SIZE of the decode kernel,
+    scaled by the factors a plain copy of known size gives), or None."""
+    f = ROOT / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    d = json.loads(f.read_text()).get(f"{workload}/{kv}")
+    return None if d is None else int(d["traffic_bytes"])
+
+
 def cpu_baseline(ctx, q_len, kv_bf16: bool, budget_s: float):
     """The oracle's (token, head) loop (cpu_model.cpp:160-185) on the host
     cores, on one layer of the same batch, repeated until budget_s elapses."""
@@ -113,7 +124,20 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--partition", type=int, default=0, help="decode partition tokens (0 = planner's choice)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 256 MiB device copy (the reference kernel for scaling "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        import torch
+        x = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        x.fill_(1)
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "copy", "bytes_read": x.numel(), "bytes_written": y.numel()}))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (the decode path shards by "
               "sequence with no exchange; multi-GPU runs are not part of it).", file=sys.stderr)
@@ -192,7 +216,8 @@ def main():
     achieved = attn_b / (attn_us * 1e-6) / 1e9
     P = plan.plan
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic(args.workload, args.kv) if args.partition == 0 else None,
                 "kernel": "le_ragged_paged_attention (decode_kernel"
                           + (" + chunk_kernel" if P.n_chunk_items else "")
                           + (" + combine_kernel" if P.n_combine_items else "") + ")",
