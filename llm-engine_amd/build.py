@@ -33,11 +33,12 @@ COMMON = [
 
 
 def sources() -> list[Path]:
-    return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
+    return sorted(list(CSRC.rglob("*.hip")) + list(CSRC.rglob("*.cpp")))
 
 
 def _compile(src: Path, defines=(), build_dir: Path = BUILD) -> Path:
-    obj = build_dir / (src.stem + src.suffix.replace(".", "_") + ".o")
+    rel = src.relative_to(CSRC)
+    obj = build_dir / ("_".join(rel.parts[:-1] + (src.stem,)) + src.suffix.replace(".", "_") + ".o")
     cmd = [HIPCC, *COMMON, *[f"-D{d}" for d in defines], "-c", str(src), "-o", str(obj)]
     if src.suffix == ".cpp":
         cmd[1:1] = ["-x", "hip"]
@@ -59,7 +60,7 @@ def build(jobs: int | None = None, verbose: bool = False, out: Path = LIB, defin
         objs = list(ex.map(lambda s: _compile(s, defines, build_dir), srcs))
     tmp = out.with_suffix(".so.tmp")
     cmd = [HIPCC, "-shared", "--offload-arch=gfx950", "-fPIC", "-o", str(tmp), *map(str, objs),
-           "-Wl,--no-undefined"]
+           "-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib", "-Wl,--no-undefined"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr[-6000:]}")

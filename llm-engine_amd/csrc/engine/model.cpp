@@ -1,0 +1,463 @@
+// Device model and serving loop over the hot path (le_engine.h).
+//
+// The forward pass follows the reference's CudaModel::forward
+// (src/model/cuda/cuda_model.cu:324-429) and its CPU twin cpu_model.cpp:98-214:
+// embedding gather, then per layer RMSNorm, Q/K/V projections (+bias),
+// RoPE, the K/V scatter into the paged cache, ragged paged attention over the
+// packed step, output projection and residual, RMSNorm, SiLU-gated MLP and
+// residual; finally RMSNorm and the LM head on the logit rows only. Where the
+// reference uploads six index arrays with synchronous copies every step, here
+// the step is packed once (le_plan_step) and sent with one async copy, and
+// greedy selection runs on the device so only the chosen ids come back.
+#include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "le_engine.h"
+#include "llm_engine_amd.h"
+#include "model_kernels.h"
+#include "scheduler.h"
+
+namespace le::engine {
+namespace {
+
+void hip_ok(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+void blas_ok(rocblas_status s, const char* what) {
+  if (s != rocblas_status_success)
+    throw std::runtime_error(std::string(what) + ": rocBLAS status " + std::to_string(static_cast<int>(s)));
+}
+void le_ok(int st, const char* what) {
+  if (st != LE_OK) throw std::runtime_error(std::string(what) + ": " + le_status_string(st));
+}
+
+uint16_t to_bf16(float f) {  // round to nearest even, inf/nan unrounded (tensor.h:23-28)
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7f800000u) == 0x7f800000u) return static_cast<uint16_t>(u >> 16);
+  return static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+// Device buffer that grows on demand and is then reused across steps.
+struct DevBuf {
+  void* p = nullptr;
+  size_t cap = 0;
+  DevBuf() = default;
+  DevBuf(const DevBuf&) = delete;
+  DevBuf& operator=(const DevBuf&) = delete;
+  ~DevBuf() { if (p) (void)hipFree(p); }
+  void* get(size_t bytes, bool zero = false, hipStream_t s = nullptr) {
+    if (bytes > cap) {
+      if (p) hip_ok(hipFree(p), "hipFree");
+      p = nullptr;
+      hip_ok(hipMalloc(&p, bytes), "hipMalloc");
+      cap = bytes;
+      if (zero) hip_ok(hipMemsetAsync(p, 0, bytes, s), "hipMemsetAsync");
+    }
+    return p;
+  }
+};
+
+struct HostBuf {
+  void* p = nullptr;
+  size_t cap = 0;
+  HostBuf() = default;
+  HostBuf(const HostBuf&) = delete;
+  HostBuf& operator=(const HostBuf&) = delete;
+  ~HostBuf() { if (p) (void)hipHostFree(p); }
+  void* get(size_t bytes) {
+    if (bytes > cap) {
+      if (p) hip_ok(hipHostFree(p), "hipHostFree");
+      p = nullptr;
+      hip_ok(hipHostMalloc(&p, bytes, hipHostMallocDefault), "hipHostMalloc");
+      cap = bytes;
+    }
+    return p;
+  }
+};
+
+struct Layer {
+  void *wq = nullptr, *wk = nullptr, *wv = nullptr, *wo = nullptr;
+  void *wgate = nullptr, *wup = nullptr, *wdown = nullptr;
+  float *in_norm = nullptr, *post_norm = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr;
+};
+
+}  // namespace
+
+class Model {
+ public:
+  Model(const le_model_desc& d, int num_blocks, int block_size);
+  ~Model();
+  void forward(const le_step_slice* slices, int n_slices, int32_t* tokens_out, float* logits_out);
+  int num_blocks() const { return num_blocks_; }
+  int block_size() const { return bs_; }
+
+ private:
+  void* upload(const float* host, size_t n, bool as_bf16);
+  float* upload_f32(const float* host, size_t n) { return static_cast<float*>(upload(host, n, false)); }
+  void gemm(const void* A, const void* B, void* C, int m, int n, int k, bool c_f32 = false);
+
+  le_model_desc d_;
+  bool bf16_, kv_bf16_;
+  int H_, QD_, KVD_, I_, V_, hd_, nh_, nkv_, bs_, num_blocks_;
+  size_t act_;
+  hipStream_t stream_ = nullptr;
+  rocblas_handle blas_ = nullptr;
+  std::vector<void*> owned_;
+  void* embed_ = nullptr;
+  void* lm_head_ = nullptr;
+  float* final_norm_ = nullptr;
+  float *cos_ = nullptr, *sin_ = nullptr;
+  std::vector<Layer> layers_;
+  std::vector<void*> kc_, vc_;
+  DevBuf x_, h_, q_, k_, v_, attn_, o_, gate_, up_, rows_, logits_, tokens_, plan_dev_, ws_;
+  HostBuf plan_host_, tokens_host_;
+};
+
+Model::Model(const le_model_desc& d, int num_blocks, int block_size) : d_(d) {
+  bf16_ = d.dtype == LE_BF16;
+  kv_bf16_ = d.kv_dtype == LE_BF16;
+  H_ = d.hidden;
+  hd_ = d.head_dim;
+  nh_ = d.q_heads;
+  nkv_ = d.kv_heads;
+  QD_ = nh_ * hd_;
+  KVD_ = nkv_ * hd_;
+  I_ = d.inter;
+  V_ = d.vocab;
+  bs_ = block_size;
+  num_blocks_ = num_blocks;
+  act_ = bf16_ ? 2 : 4;
+  if (nh_ % nkv_ != 0 || hd_ % 2 != 0) throw std::invalid_argument("head layout");
+  hip_ok(hipStreamCreate(&stream_), "hipStreamCreate");
+  blas_ok(rocblas_create_handle(&blas_), "rocblas_create_handle");
+  blas_ok(rocblas_set_stream(blas_, stream_), "rocblas_set_stream");
+
+  embed_ = upload(d.embed, static_cast<size_t>(V_) * H_, bf16_);
+  lm_head_ = d.tie_word_embeddings ? embed_ : upload(d.lm_head, static_cast<size_t>(V_) * H_, bf16_);
+  final_norm_ = upload_f32(d.final_norm, H_);
+  layers_.resize(d.layers);
+  for (int l = 0; l < d.layers; l++) {
+    Layer& L = layers_[l];
+    L.in_norm = upload_f32(d.in_norm[l], H_);
+    L.post_norm = upload_f32(d.post_norm[l], H_);
+    L.wq = upload(d.wq[l], static_cast<size_t>(QD_) * H_, bf16_);
+    L.wk = upload(d.wk[l], static_cast<size_t>(KVD_) * H_, bf16_);
+    L.wv = upload(d.wv[l], static_cast<size_t>(KVD_) * H_, bf16_);
+    L.wo = upload(d.wo[l], static_cast<size_t>(H_) * QD_, bf16_);
+    if (d.bq && d.bq[l]) {
+      L.bq = upload_f32(d.bq[l], QD_);
+      L.bk = upload_f32(d.bk[l], KVD_);
+      L.bv = upload_f32(d.bv[l], KVD_);
+    }
+    L.wgate = upload(d.wgate[l], static_cast<size_t>(I_) * H_, bf16_);
+    L.wup = upload(d.wup[l], static_cast<size_t>(I_) * H_, bf16_);
+    L.wdown = upload(d.wdown[l], static_cast<size_t>(H_) * I_, bf16_);
+  }
+  // RoPE tables as the reference builds them: angles in double, stored as
+  // float (ops.h:37-50).
+  const int half = hd_ / 2;
+  std::vector<float> c(static_cast<size_t>(d.max_pos) * half), s(c.size());
+  for (int i = 0; i < half; i++) {
+    const double inv_freq = 1.0 / std::pow(static_cast<double>(d.theta), (2.0 * i) / hd_);
+    for (int p = 0; p < d.max_pos; p++) {
+      c[static_cast<size_t>(p) * half + i] = static_cast<float>(std::cos(p * inv_freq));
+      s[static_cast<size_t>(p) * half + i] = static_cast<float>(std::sin(p * inv_freq));
+    }
+  }
+  cos_ = upload_f32(c.data(), c.size());
+  sin_ = upload_f32(s.data(), s.size());
+  const size_t cache_bytes = static_cast<size_t>(num_blocks) * bs_ * KVD_ * (kv_bf16_ ? 2 : 4);
+  for (int l = 0; l < d.layers; l++) {
+    void *k = nullptr, *v = nullptr;
+    hip_ok(hipMalloc(&k, cache_bytes), "hipMalloc kv");
+    owned_.push_back(k);
+    hip_ok(hipMalloc(&v, cache_bytes), "hipMalloc kv");
+    owned_.push_back(v);
+    hip_ok(hipMemsetAsync(k, 0, cache_bytes, stream_), "memset kv");
+    hip_ok(hipMemsetAsync(v, 0, cache_bytes, stream_), "memset kv");
+    kc_.push_back(k);
+    vc_.push_back(v);
+  }
+  hip_ok(hipStreamSynchronize(stream_), "sync");
+}
+
+Model::~Model() {
+  (void)hipStreamSynchronize(stream_);
+  for (void* p : owned_) (void)hipFree(p);
+  if (blas_) rocblas_destroy_handle(blas_);
+  if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+void* Model::upload(const float* host, size_t n, bool as_bf16) {
+  if (!host) throw std::invalid_argument("missing weight");
+  void* p = nullptr;
+  const size_t bytes = n * (as_bf16 ? 2 : 4);
+  hip_ok(hipMalloc(&p, bytes), "hipMalloc weight");
+  owned_.push_back(p);
+  if (as_bf16) {
+    std::vector<uint16_t> b(n);
+    for (size_t i = 0; i < n; i++) b[i] = to_bf16(host[i]);
+    hip_ok(hipMemcpy(p, b.data(), bytes, hipMemcpyHostToDevice), "upload");
+  } else {
+    hip_ok(hipMemcpy(p, host, bytes, hipMemcpyHostToDevice), "upload");
+  }
+  return p;
+}
+
+// C[m][n] = A[m][k] * B[n][k]^T in row-major terms. rocBLAS is column-major,
+// so it computes C^T = B * A^T: B with op T first, A with op N second.
+void Model::gemm(const void* A, const void* B, void* C, int m, int n, int k, bool c_f32) {
+  const float one = 1.f, zero = 0.f;
+  if (!bf16_) {
+    blas_ok(rocblas_sgemm(blas_, rocblas_operation_transpose, rocblas_operation_none, n, m, k, &one,
+                          static_cast<const float*>(B), k, static_cast<const float*>(A), k, &zero,
+                          static_cast<float*>(C), n),
+            "rocblas_sgemm");
+    return;
+  }
+  const rocblas_datatype ct = c_f32 ? rocblas_datatype_f32_r : rocblas_datatype_bf16_r;
+  blas_ok(rocblas_gemm_ex(blas_, rocblas_operation_transpose, rocblas_operation_none, n, m, k, &one,
+                          B, rocblas_datatype_bf16_r, k, A, rocblas_datatype_bf16_r, k, &zero, C, ct, n,
+                          C, ct, n, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0),
+          "rocblas_gemm_ex");
+}
+
+void Model::forward(const le_step_slice* slices, int n_slices, int32_t* tokens_out, float* logits_out) {
+  le_plan_config cfg{nh_, nkv_, hd_, bs_, kv_bf16_ ? LE_BF16 : LE_F32, 0, 0, 0};
+  le_step_plan plan{};
+  int st = le_plan_step(slices, n_slices, &cfg, nullptr, 0, &plan);
+  if (st != LE_ENOSPACE) le_ok(st, "le_plan_step");
+  void* host = plan_host_.get(static_cast<size_t>(plan.bytes));
+  le_ok(le_plan_step(slices, n_slices, &cfg, host, plan.bytes, &plan), "le_plan_step");
+  le_ok(le_plan_upload(&plan, host, plan_dev_.get(static_cast<size_t>(plan.bytes)), stream_), "le_plan_upload");
+  const int N = plan.n_tokens, R = plan.n_logits;
+  if (N == 0) return;
+  const int32_t* d_ids = le_plan_dev_array(&plan, plan.off_token_ids);
+  const int32_t* d_pos = le_plan_dev_array(&plan, plan.off_positions);
+  const int32_t* d_slots = le_plan_dev_array(&plan, plan.off_slots);
+  const int32_t* d_rows = le_plan_dev_array(&plan, plan.off_logit_rows);
+  const size_t n = static_cast<size_t>(N);
+  void* x = x_.get(n * H_ * act_);
+  void* h = h_.get(n * std::max(H_, QD_) * act_);
+  void* q = q_.get(n * QD_ * act_);
+  void* k = k_.get(n * KVD_ * act_);
+  void* v = v_.get(n * KVD_ * act_);
+  void* attn = attn_.get(n * QD_ * act_);
+  void* o = o_.get(n * std::max(H_, QD_) * act_);
+  void* gate = gate_.get(n * I_ * act_);
+  void* up = up_.get(n * I_ * act_);
+  const size_t ws_bytes = le_ragged_workspace_size(&plan);
+  void* ws = ws_bytes ? ws_.get(ws_bytes, /*zero=*/true, stream_) : nullptr;
+  const float scale = 1.0f / std::sqrt(static_cast<float>(hd_));
+  const int act_dt = bf16_ ? LE_BF16 : LE_F32, kv_dt = kv_bf16_ ? LE_BF16 : LE_F32;
+  const int64_t num_slots = static_cast<int64_t>(num_blocks_) * bs_;
+
+  hip_ok(gather_rows(embed_, d_ids, x, N, H_, bf16_, stream_), "embedding");
+  for (size_t l = 0; l < layers_.size(); l++) {
+    const Layer& L = layers_[l];
+    hip_ok(rmsnorm(x, L.in_norm, h, N, H_, d_.eps, bf16_, stream_), "rmsnorm");
+    gemm(h, L.wq, q, N, QD_, H_);
+    gemm(h, L.wk, k, N, KVD_, H_);
+    gemm(h, L.wv, v, N, KVD_, H_);
+    if (L.bq) {
+      hip_ok(add_bias(q, L.bq, N, QD_, bf16_, stream_), "bias");
+      hip_ok(add_bias(k, L.bk, N, KVD_, bf16_, stream_), "bias");
+      hip_ok(add_bias(v, L.bv, N, KVD_, bf16_, stream_), "bias");
+    }
+    // Every token's K/V is rotated and written before attention runs, so
+    // tokens of one step (a prefill chunk) attend to each other.
+    hip_ok(rope(q, d_pos, cos_, sin_, N, nh_, hd_, QD_, bf16_, stream_), "rope");
+    hip_ok(rope(k, d_pos, cos_, sin_, N, nkv_, hd_, KVD_, bf16_, stream_), "rope");
+    le_ok(le_kv_cache_write(k, v, static_cast<le_dtype>(act_dt), d_slots, kc_[l], vc_[l],
+                            static_cast<le_dtype>(kv_dt), N, KVD_, num_slots, stream_),
+          "le_kv_cache_write");
+    le_ok(le_ragged_paged_attention(q, static_cast<le_dtype>(act_dt), kc_[l], vc_[l],
+                                    static_cast<le_dtype>(kv_dt), num_blocks_, &plan, scale, attn, ws,
+                                    ws_bytes, stream_),
+          "le_ragged_paged_attention");
+    gemm(attn, L.wo, o, N, H_, QD_);
+    hip_ok(add_inplace(x, o, static_cast<int64_t>(N) * H_, bf16_, stream_), "residual");
+    hip_ok(rmsnorm(x, L.post_norm, h, N, H_, d_.eps, bf16_, stream_), "rmsnorm");
+    gemm(h, L.wgate, gate, N, I_, H_);
+    gemm(h, L.wup, up, N, I_, H_);
+    hip_ok(silu_mul(gate, up, static_cast<int64_t>(N) * I_, bf16_, stream_), "silu_mul");
+    gemm(gate, L.wdown, o, N, H_, I_);
+    hip_ok(add_inplace(x, o, static_cast<int64_t>(N) * H_, bf16_, stream_), "residual");
+  }
+  if (R > 0) {
+    void* rows = rows_.get(static_cast<size_t>(R) * H_ * act_);
+    hip_ok(gather_rows(x, d_rows, rows, R, H_, bf16_, stream_), "logit rows");
+    hip_ok(rmsnorm(rows, final_norm_, h, R, H_, d_.eps, bf16_, stream_), "final norm");
+    float* logits = static_cast<float*>(logits_.get(static_cast<size_t>(R) * V_ * 4));
+    gemm(h, lm_head_, logits, R, V_, H_, /*c_f32=*/true);
+    int32_t* dtok = static_cast<int32_t*>(tokens_.get(static_cast<size_t>(R) * 4));
+    hip_ok(argmax_rows(logits, R, V_, dtok, stream_), "argmax");
+    int32_t* htok = static_cast<int32_t*>(tokens_host_.get(static_cast<size_t>(R) * 4));
+    hip_ok(hipMemcpyAsync(htok, dtok, static_cast<size_t>(R) * 4, hipMemcpyDeviceToHost, stream_), "tokens");
+    if (logits_out)
+      hip_ok(hipMemcpyAsync(logits_out, logits, static_cast<size_t>(R) * V_ * 4, hipMemcpyDeviceToHost,
+                            stream_), "logits");
+    hip_ok(hipStreamSynchronize(stream_), "step sync");
+    if (tokens_out) std::memcpy(tokens_out, htok, static_cast<size_t>(R) * 4);
+  } else {
+    hip_ok(hipStreamSynchronize(stream_), "step sync");
+  }
+}
+
+}  // namespace le::engine
+
+using le::engine::Model;
+
+struct le_model {
+  std::unique_ptr<Model> impl;
+};
+
+namespace {
+int fail(const std::exception& e) {
+  std::fprintf(stderr, "llm-engine-amd: %s\n", e.what());
+  return LE_EINVAL;
+}
+}  // namespace
+
+extern "C" {
+
+le_model* le_model_create(const le_model_desc* desc, int num_blocks, int block_size, int* status) {
+  if (status) *status = LE_OK;
+  if (!desc || num_blocks <= 0 || block_size <= 0) {
+    if (status) *status = LE_EINVAL;
+    return nullptr;
+  }
+  try {
+    auto* m = new le_model;
+    m->impl = std::make_unique<Model>(*desc, num_blocks, block_size);
+    return m;
+  } catch (const std::exception& e) {
+    if (status) *status = fail(e);
+    return nullptr;
+  }
+}
+
+void le_model_destroy(le_model* m) { delete m; }
+
+int le_model_forward(le_model* m, const le_step_slice* slices, int n_slices, int32_t* tokens_out,
+                     float* logits_out) {
+  if (!m || (n_slices > 0 && !slices)) return LE_EINVAL;
+  try {
+    m->impl->forward(slices, n_slices, tokens_out, logits_out);
+    return LE_OK;
+  } catch (const std::exception& e) {
+    return fail(e);
+  }
+}
+
+int le_run_greedy(le_model* m, const le_sched_config* cfg, int prefix_caching, int fragment_blocks,
+                  int n_seqs, const int32_t* prompt_lens, const int32_t* prompts_flat,
+                  const int32_t* max_tokens, const double* arrival_s, int32_t* gen_out,
+                  le_run_stats* stats) {
+  using namespace le::engine;
+  if (!m || !cfg || n_seqs < 0 || (n_seqs > 0 && (!prompt_lens || !prompts_flat || !max_tokens || !gen_out)))
+    return LE_EINVAL;
+  try {
+    Model& model = *m->impl;
+    KVCacheManager kv(model.num_blocks(), model.block_size(), prefix_caching != 0);
+    // Pre-fragment the pool (test_cuda_invariance.cpp:98-105).
+    std::vector<BlockTable> held;
+    for (int i = 0; i < fragment_blocks; i++) {
+      BlockTable bt;
+      std::vector<int32_t> one(std::max(1, model.block_size() / 2), 7000 + i);
+      if (!kv.allocate_prompt(bt, one)) break;
+      held.push_back(bt);
+    }
+    for (size_t i = 0; i < held.size(); i += 2) kv.free(held[i]);
+
+    SchedulerConfig sc;
+    sc.continuous = cfg->continuous != 0;
+    sc.max_num_seqs = cfg->max_num_seqs;
+    sc.max_num_batched_tokens = cfg->max_num_batched_tokens;
+    sc.prefill_chunk_size = cfg->prefill_chunk_size;
+    sc.admission_lookahead = cfg->admission_lookahead;
+    sc.starvation_wait_steps = cfg->starvation_wait_steps;
+    sc.watermark_blocks = cfg->watermark_blocks;
+    sc.max_queue_wait_seconds = cfg->max_queue_wait_seconds;
+    Scheduler sch(sc, kv);
+
+    std::vector<SequencePtr> seqs(static_cast<size_t>(n_seqs));
+    size_t off = 0;
+    for (int i = 0; i < n_seqs; i++) {
+      auto s = std::make_shared<Sequence>();
+      s->id = static_cast<uint64_t>(i);
+      s->tokens.assign(prompts_flat + off, prompts_flat + off + prompt_lens[i]);
+      off += static_cast<size_t>(prompt_lens[i]);
+      s->prompt_len = prompt_lens[i];
+      s->params.max_tokens = max_tokens[i];
+      s->params.ignore_eos = true;
+      seqs[i] = s;
+    }
+    std::vector<int> order(static_cast<size_t>(n_seqs));
+    for (int i = 0; i < n_seqs; i++) order[i] = i;
+    if (arrival_s)
+      std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return arrival_s[a] < arrival_s[b]; });
+    size_t next = 0;
+
+    le_run_stats rs{};
+    const auto t0 = std::chrono::steady_clock::now();
+    auto elapsed = [&]() { return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count(); };
+    std::vector<le_step_slice> sl;
+    std::vector<int32_t> sampled;
+    for (int guard = 0; guard < 10000000; guard++) {
+      const double now = elapsed();
+      while (next < order.size() && (!arrival_s || arrival_s[order[next]] <= now)) sch.add(seqs[order[next++]]);
+      if (!sch.has_work()) {
+        if (next >= order.size()) break;
+        const double wait = arrival_s[order[next]] - elapsed();
+        if (wait > 0) std::this_thread::sleep_for(std::chrono::duration<double>(wait));
+        continue;
+      }
+      StepInput step = sch.schedule();
+      if (step.empty()) {
+        if (next >= order.size() && !sch.has_work()) break;
+        continue;
+      }
+      sl.clear();
+      for (const auto& s : step.slices)
+        sl.push_back({static_cast<int64_t>(s.seq->id), s.start, s.len, s.needs_logits ? 1 : 0,
+                      s.seq->block_table.num_blocks(), s.seq->block_table.blocks.data(),
+                      s.seq->tokens.data()});
+      sampled.assign(static_cast<size_t>(step.num_logits), 0);
+      const double ts = elapsed();
+      model.forward(sl.data(), static_cast<int>(sl.size()), sampled.data(), nullptr);
+      if (step.num_prefill_tokens == 0) rs.decode_seconds += elapsed() - ts;
+      rs.steps++;
+      rs.prompt_tokens += step.num_prefill_tokens;
+      rs.decode_tokens += step.num_logits;
+      sch.on_step_done(step, sampled);
+    }
+    rs.seconds = elapsed();
+    rs.preemptions = static_cast<int64_t>(sch.stats().preemptions);
+    for (size_t i = 1; i < held.size(); i += 2) kv.free(held[i]);
+    size_t out_off = 0;  // gen_out: max_tokens[i] entries per sequence, back to back
+    for (int i = 0; i < n_seqs; i++) {
+      const Sequence& s = *seqs[i];
+      for (int j = 0; j < max_tokens[i]; j++)
+        gen_out[out_off + j] = j < s.num_generated() ? s.tokens[s.prompt_len + j] : -1;
+      out_off += static_cast<size_t>(max_tokens[i]);
+    }
+    if (stats) *stats = rs;
+    return LE_OK;
+  } catch (const std::exception& e) {
+    return fail(e);
+  }
+}
+
+}  // extern "C"

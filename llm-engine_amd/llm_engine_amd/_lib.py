@@ -81,7 +81,41 @@ class StepPlan(ctypes.Structure):
     ]
 
 
-# name -> (restype, argtypes). Exactly the symbols include/llm_engine_amd.h declares.
+class SchedConfig(ctypes.Structure):
+    _fields_ = [
+        ("continuous", ctypes.c_int32),
+        ("max_num_seqs", ctypes.c_int32),
+        ("max_num_batched_tokens", ctypes.c_int32),
+        ("prefill_chunk_size", ctypes.c_int32),
+        ("admission_lookahead", ctypes.c_int32),
+        ("starvation_wait_steps", ctypes.c_int32),
+        ("watermark_blocks", ctypes.c_int32),
+        ("reserved_", ctypes.c_int32),
+        ("max_queue_wait_seconds", ctypes.c_double),
+    ]
+
+
+_fpp = ctypes.POINTER(ctypes.c_void_p)
+
+
+class ModelDesc(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("hidden", "inter", "layers", "q_heads", "kv_heads",
+                                              "head_dim", "vocab", "max_pos")] + [
+        ("eps", ctypes.c_float), ("theta", ctypes.c_float),
+        ("tie_word_embeddings", ctypes.c_int32), ("dtype", ctypes.c_int32),
+        ("kv_dtype", ctypes.c_int32), ("reserved_", ctypes.c_int32),
+        ("embed", ctypes.c_void_p), ("final_norm", ctypes.c_void_p), ("lm_head", ctypes.c_void_p),
+    ] + [(n, _fpp) for n in ("in_norm", "post_norm", "wq", "wk", "wv", "wo", "bq", "bk", "bv",
+                              "wgate", "wup", "wdown")]
+
+
+class RunStats(ctypes.Structure):
+    _fields_ = [("steps", ctypes.c_int64), ("prompt_tokens", ctypes.c_int64),
+                ("decode_tokens", ctypes.c_int64), ("preemptions", ctypes.c_int64),
+                ("seconds", ctypes.c_double), ("decode_seconds", ctypes.c_double)]
+
+
+# name -> (restype, argtypes). Exactly the symbols include/*.h declare.
 SIGNATURES = {
     "le_version": (ctypes.c_char_p, []),
     "le_status_string": (ctypes.c_char_p, [ctypes.c_int]),
@@ -102,6 +136,30 @@ SIGNATURES = {
     "le_plan_upload": (ctypes.c_int, [
         ctypes.POINTER(StepPlan), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]),
     "le_ragged_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(StepPlan)]),
+    "le_sched_trace": (ctypes.c_int64, [
+        ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(SchedConfig), ctypes.c_int,
+        ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+        ctypes.c_void_p, ctypes.c_int64]),
+    "le_sched_create": (ctypes.c_void_p, [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                          ctypes.POINTER(SchedConfig), ctypes.c_int]),
+    "le_sched_destroy": (None, [ctypes.c_void_p]),
+    "le_sched_add": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int,
+                                    ctypes.c_int]),
+    "le_sched_has_work": (ctypes.c_int, [ctypes.c_void_p]),
+    "le_sched_step": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(StepSlice), ctypes.c_int,
+                                     ctypes.POINTER(ctypes.c_int)]),
+    "le_sched_done": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]),
+    "le_sched_generated": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                          ctypes.c_int]),
+    "le_model_create": (ctypes.c_void_p, [ctypes.POINTER(ModelDesc), ctypes.c_int, ctypes.c_int,
+                                          ctypes.POINTER(ctypes.c_int)]),
+    "le_model_destroy": (None, [ctypes.c_void_p]),
+    "le_model_forward": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(StepSlice), ctypes.c_int,
+                                        ctypes.c_void_p, ctypes.c_void_p]),
+    "le_run_greedy": (ctypes.c_int, [
+        ctypes.c_void_p, ctypes.POINTER(SchedConfig), ctypes.c_int, ctypes.c_int, ctypes.c_int,
+        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+        ctypes.POINTER(RunStats)]),
     "le_ragged_paged_attention": (ctypes.c_int, [
         ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
         ctypes.c_int64, ctypes.POINTER(StepPlan), ctypes.c_float, ctypes.c_void_p,
