@@ -2,6 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--kv bf16|f32]
                     [--workload config2|target|config3] [--no-cpu-baseline]
+                    [--e2e decode64|config4|both|none]
 
 A step is one decode pass of the hot path over one ragged batch, for every
 layer of the model: the packed step metadata is uploaded once (one async
@@ -11,9 +12,15 @@ KV pool, so a step touches 24 distinct caches (>> the 256 MB Infinity Cache).
 
 Workloads (Qwen2.5-0.5B GQA: 14 q heads, 2 kv heads, head_dim 64, block 16):
   config2  64 seqs, context log-uniform in [64, 4096], tables from a
-           32768-block pool -- the default
+           32768-block pool (benchmark config 2) -- the default
   target   64 seqs x 4096 context (the >= 60 % of HBM peak target point)
   config3  32 decode rows + 2 prefill chunks of 512 (MFMA chunk rows)
+
+After the attention measurement, an end-to-end leg runs the whole engine
+(scheduler, packing, device model, greedy) on TinyLlama-1.1B with bf16
+weights and K/V (benchmark config 4 shape) and reports decode tok/s at
+64 sequences under "e2e_decode64" (and the Poisson serving run under
+"e2e_config4" with --e2e config4|both).
 
 Prints ONE JSON line. `value` is algorithmic HBM bytes per step / step time:
 K/V of each kv head once (the GQA-shared minimum), q, out, block tables and
@@ -113,6 +120,51 @@ def cpu_baseline(ctx, q_len, kv_bf16: bool, budget_s: float):
                       f"(token, head) loop on {threads} threads"}
 
 
+def e2e_decode(n_seqs=64, gen=256, seed=4, arrivals=None, layers=None):
+    """End-to-end continuous batching on the device model, config 4's shape:
+    TinyLlama-1.1B architecture, random-init weights N(0, 0.02) held as bf16 on
+    the device, bf16 K/V cache, block 16, chunked prefill budget 512 tokens per
+    step, at most 64 running, prompts uniform in [128, 1024].
+
+    Closed loop (arrivals None): n_seqs requests at t=0, `gen` greedy tokens
+    each; decode tok/s = tokens sampled in steps with no prefill / their wall
+    time (host scheduling, packing, upload, all layers, greedy read-back).
+    Serving (arrivals = Poisson rate, requests/s): output lengths uniform in
+    [64, 256]; tok/s = generated tokens / wall time of the loop."""
+    from llm_engine_amd.engine import Model, sched_config, synthetic_weights
+    rng = np.random.default_rng(seed)
+    t0 = time.perf_counter()
+    w = synthetic_weights("tinyllama-1.1b", seed, layers=layers)
+    V, L = w.arch["vocab"], w.arch["layers"]
+    lens = rng.integers(128, 1025, size=n_seqs)
+    prompts = [rng.integers(0, V, int(x)).astype(np.int32) for x in lens]
+    if arrivals:
+        out_lens = rng.integers(64, 257, size=n_seqs).tolist()
+        t_arr = np.cumsum(rng.exponential(1.0 / arrivals, size=n_seqs)).tolist()
+    else:
+        out_lens, t_arr = [gen] * n_seqs, None
+    blocks = int(64 * (1024 + 256) // 16 * 1.25)
+    m = Model(w, blocks, 16, dtype="bf16", kv_dtype="bf16")
+    del w
+    load_s = time.perf_counter() - t0
+    cfg = sched_config(max_num_seqs=64, max_num_batched_tokens=512, prefill_chunk_size=512)
+    m.run_greedy([p[:64] for p in prompts[:4]], [4] * 4, cfg)  # warm-up: code objects, rocBLAS
+    toks, st = m.run_greedy(prompts, out_lens, cfg, arrival_s=t_arr)
+    m.close()
+    gen_total = sum(len(t) for t in toks)
+    assert gen_total == sum(out_lens), "not every request finished"
+    r = {"model": f"tinyllama-1.1b, {L} layers, random-init bf16 weights, bf16 KV",
+         "requests": n_seqs, "arrivals_per_s": arrivals, "prompt_tokens": int(st.prompt_tokens),
+         "generated_tokens": gen_total, "steps": int(st.steps), "seconds": round(st.seconds, 3),
+         "tok_per_s": round(gen_total / st.seconds, 1),
+         "decode_steps": int(st.decode_steps),
+         "decode_tok_per_s": round(st.decode_step_tokens / st.decode_seconds, 1) if st.decode_seconds else None,
+         "decode_ms_per_step": round(1e3 * st.decode_seconds / st.decode_steps, 3) if st.decode_steps else None,
+         "ttft_mean_s": round(st.ttft_mean_s, 4), "latency_mean_s": round(st.latency_mean_s, 3),
+         "preemptions": int(st.preemptions), "setup_s": round(load_s, 1)}
+    return r
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -122,6 +174,9 @@ def main():
     ap.add_argument("--workload", choices=["config2", "target", "config3"], default="config2")
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--e2e", choices=["decode64", "config4", "both", "none"], default="decode64",
+                    help="end-to-end leg: closed-loop decode at 64 seqs, config-4 Poisson serving, both, none")
+    ap.add_argument("--e2e-layers", type=int, default=None, help="TinyLlama layers (default: all 22)")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--partition", type=int, default=0, help="decode partition tokens (0 = planner's choice)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -247,6 +302,12 @@ def main():
         res["cpu_baseline"] = cpu_baseline(ctx, q_len, kv_dt == torch.bfloat16, args.cpu_budget)
     else:
         res["cpu_baseline"] = None
+    del kc, vc, qs, knew, vnew, outs, ws, plan
+    torch.cuda.empty_cache()
+    if args.e2e in ("decode64", "both"):
+        res["e2e_decode64"] = e2e_decode(64, 256, layers=args.e2e_layers)
+    if args.e2e in ("config4", "both"):
+        res["e2e_config4"] = e2e_decode(256, arrivals=8.0, layers=args.e2e_layers)
     print(json.dumps(res), flush=True)
 
 

@@ -110,6 +110,10 @@ int le_model_forward(le_model* m, const le_step_slice* slices, int n_slices, int
 typedef struct le_run_stats {
   int64_t steps, prompt_tokens, decode_tokens, preemptions;
   double seconds, decode_seconds;  /* wall time of the loop; of steps with no prefill */
+  int64_t decode_steps;            /* steps with no prefill */
+  int64_t decode_step_tokens;      /* tokens sampled in those steps */
+  double ttft_mean_s;              /* arrival (or start) to first token, mean over sequences */
+  double latency_mean_s;           /* arrival (or start) to last token, mean over sequences */
 } le_run_stats;
 
 /* Greedy generation of n_seqs prompts through the scheduler and the model.

@@ -64,6 +64,32 @@ int le_kv_cache_write(const void* k, const void* v, le_dtype src_dtype,
                       hipStream_t stream);
 
 /* ------------------------------------------------------------------------
+ * (2) The scatter fused with what produces its rows.
+ * Replaces the reference's bias + RoPE + cache-write sequence of each layer
+ * (cuda_model.cu:358-368: launch_add_bias x3, launch_rope on q and k,
+ * launch_store_kv; kernels elementwise.cu:40, rope.cu:53, store_kv.cu:31)
+ * with one launch over the fused QKV projection output:
+ *     row t of qkv = [ q (q_heads*head_dim) | k (kv_heads*head_dim) | v (kv_heads*head_dim) ]
+ *     x += bias (if not NULL, fp32 [q_dim + 2*kv_dim]; rounded to act_dtype as
+ *                the separate add would store it)
+ *     q, k rotated by RoPE at positions[t] (rotate_half pairing i <-> i+half,
+ *        a' = a*cos - b*sin, b' = b*cos + a*sin, no fused multiply-add)
+ *     q_out[t] = q  (contiguous [n_tokens][q_heads*head_dim], act_dtype)
+ *     k_cache[slots[t]] = k, v_cache[slots[t]] = v  (cache_dtype)
+ * cos/sin tables are fp32 [max_positions][head_dim/2]. A negative slot skips
+ * the K/V write (padding), as does a slot >= num_slots. A position outside
+ * [0, max_positions) zero-fills that token's q row and skips its K/V write.
+ * head_dim a multiple of 8; qkv_row_stride (elements) >= (q_heads+2*kv_heads)*head_dim
+ * and a multiple of 8; all buffers 16-byte aligned.
+ * ------------------------------------------------------------------------ */
+int le_rope_kv_cache_write(const void* qkv, le_dtype act_dtype, int64_t qkv_row_stride,
+                           const float* bias, const int32_t* positions,
+                           const int32_t* slot_mapping, const float* cos_table,
+                           const float* sin_table, int max_positions, int n_tokens, int q_heads,
+                           int kv_heads, int head_dim, void* q_out, void* k_cache, void* v_cache,
+                           le_dtype cache_dtype, int64_t num_slots, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
  * (3)(4) Paged attention, reference-shaped.
  * Replaces launch_attention_decode and launch_attention_decode_gqa
  * (cuda_kernels.h:50-64, attention_decode.cu:45-161,

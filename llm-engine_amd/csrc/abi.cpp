@@ -89,6 +89,29 @@ int le_kv_cache_write(const void* k, const void* v, le_dtype src_dtype,
                                        stream));
 }
 
+int le_rope_kv_cache_write(const void* qkv, le_dtype act_dtype, int64_t qkv_row_stride,
+                           const float* bias, const int32_t* positions,
+                           const int32_t* slot_mapping, const float* cos_table,
+                           const float* sin_table, int max_positions, int n_tokens, int q_heads,
+                           int kv_heads, int head_dim, void* q_out, void* k_cache, void* v_cache,
+                           le_dtype cache_dtype, int64_t num_slots, hipStream_t stream) {
+  if (n_tokens < 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || num_slots < 0 ||
+      max_positions <= 0)
+    return LE_EINVAL;
+  if (!valid_dtype(act_dtype) || !valid_dtype(cache_dtype)) return LE_EINVAL;
+  if (head_dim % 8 != 0) return LE_EUNSUPPORTED;
+  if (qkv_row_stride < static_cast<int64_t>(q_heads + 2 * kv_heads) * head_dim) return LE_EINVAL;
+  if (qkv_row_stride % 8 != 0) return LE_EUNSUPPORTED;  // 16-byte vector rows
+  if (n_tokens == 0) return LE_OK;
+  if (!qkv || !positions || !slot_mapping || !cos_table || !sin_table || !q_out || !k_cache ||
+      !v_cache)
+    return LE_EINVAL;
+  return hip_status(le::rope_kv_cache_write(qkv, act_dtype == LE_BF16, qkv_row_stride, bias, positions,
+                                            slot_mapping, cos_table, sin_table, max_positions, n_tokens,
+                                            q_heads, kv_heads, head_dim, q_out, k_cache, v_cache,
+                                            cache_dtype == LE_BF16, num_slots, stream));
+}
+
 size_t le_attention_decode_workspace_size(int n_tokens, int q_heads, int kv_heads, int head_dim) {
   if (n_tokens <= 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0) return 0;
   const int ns = le::decode_nsplit(n_tokens, kv_heads);

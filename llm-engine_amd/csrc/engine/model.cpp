@@ -86,10 +86,13 @@ struct HostBuf {
   }
 };
 
+// Per-layer weights on the device. Q, K and V are stacked into one
+// [q_dim + 2*kv_dim][hidden] matrix and gate/up into one [2*inter][hidden]
+// matrix, so each is a single GEMM whose output rows feed the fused
+// bias/RoPE/cache-write and SiLU kernels directly.
 struct Layer {
-  void *wq = nullptr, *wk = nullptr, *wv = nullptr, *wo = nullptr;
-  void *wgate = nullptr, *wup = nullptr, *wdown = nullptr;
-  float *in_norm = nullptr, *post_norm = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr;
+  void *wqkv = nullptr, *wo = nullptr, *wgate_up = nullptr, *wdown = nullptr;
+  float *in_norm = nullptr, *post_norm = nullptr, *bqkv = nullptr;
 };
 
 }  // namespace
@@ -103,7 +106,8 @@ class Model {
   int block_size() const { return bs_; }
 
  private:
-  void* upload(const float* host, size_t n, bool as_bf16);
+  void* upload(const float* host, size_t n, bool as_bf16) { return upload_parts({{host, n}}, as_bf16); }
+  void* upload_parts(const std::vector<std::pair<const float*, size_t>>& parts, bool as_bf16);
   float* upload_f32(const float* host, size_t n) { return static_cast<float*>(upload(host, n, false)); }
   void gemm(const void* A, const void* B, void* C, int m, int n, int k, bool c_f32 = false);
 
@@ -120,7 +124,7 @@ class Model {
   float *cos_ = nullptr, *sin_ = nullptr;
   std::vector<Layer> layers_;
   std::vector<void*> kc_, vc_;
-  DevBuf x_, h_, q_, k_, v_, attn_, o_, gate_, up_, rows_, logits_, tokens_, plan_dev_, ws_;
+  DevBuf x_, h_, qkv_, q_, attn_, o_, gate_up_, act_buf_, logits_, tokens_, plan_dev_, ws_;
   HostBuf plan_host_, tokens_host_;
 };
 
@@ -151,17 +155,15 @@ Model::Model(const le_model_desc& d, int num_blocks, int block_size) : d_(d) {
     Layer& L = layers_[l];
     L.in_norm = upload_f32(d.in_norm[l], H_);
     L.post_norm = upload_f32(d.post_norm[l], H_);
-    L.wq = upload(d.wq[l], static_cast<size_t>(QD_) * H_, bf16_);
-    L.wk = upload(d.wk[l], static_cast<size_t>(KVD_) * H_, bf16_);
-    L.wv = upload(d.wv[l], static_cast<size_t>(KVD_) * H_, bf16_);
+    const size_t hq = static_cast<size_t>(QD_) * H_, hkv = static_cast<size_t>(KVD_) * H_;
+    L.wqkv = upload_parts({{d.wq[l], hq}, {d.wk[l], hkv}, {d.wv[l], hkv}}, bf16_);
     L.wo = upload(d.wo[l], static_cast<size_t>(H_) * QD_, bf16_);
-    if (d.bq && d.bq[l]) {
-      L.bq = upload_f32(d.bq[l], QD_);
-      L.bk = upload_f32(d.bk[l], KVD_);
-      L.bv = upload_f32(d.bv[l], KVD_);
-    }
-    L.wgate = upload(d.wgate[l], static_cast<size_t>(I_) * H_, bf16_);
-    L.wup = upload(d.wup[l], static_cast<size_t>(I_) * H_, bf16_);
+    if (d.bq && d.bq[l])
+      L.bqkv = static_cast<float*>(upload_parts(
+          {{d.bq[l], static_cast<size_t>(QD_)}, {d.bk[l], static_cast<size_t>(KVD_)},
+           {d.bv[l], static_cast<size_t>(KVD_)}}, false));
+    const size_t hi = static_cast<size_t>(I_) * H_;
+    L.wgate_up = upload_parts({{d.wgate[l], hi}, {d.wup[l], hi}}, bf16_);
     L.wdown = upload(d.wdown[l], static_cast<size_t>(H_) * I_, bf16_);
   }
   // RoPE tables as the reference builds them: angles in double, stored as
@@ -199,18 +201,28 @@ Model::~Model() {
   if (stream_) (void)hipStreamDestroy(stream_);
 }
 
-void* Model::upload(const float* host, size_t n, bool as_bf16) {
-  if (!host) throw std::invalid_argument("missing weight");
+// One device allocation holding the parts back to back (stacked matrices).
+void* Model::upload_parts(const std::vector<std::pair<const float*, size_t>>& parts, bool as_bf16) {
+  size_t n = 0;
+  for (const auto& [host, cnt] : parts) {
+    if (!host) throw std::invalid_argument("missing weight");
+    n += cnt;
+  }
+  const size_t esz = as_bf16 ? 2 : 4;
   void* p = nullptr;
-  const size_t bytes = n * (as_bf16 ? 2 : 4);
-  hip_ok(hipMalloc(&p, bytes), "hipMalloc weight");
+  hip_ok(hipMalloc(&p, n * esz), "hipMalloc weight");
   owned_.push_back(p);
-  if (as_bf16) {
-    std::vector<uint16_t> b(n);
-    for (size_t i = 0; i < n; i++) b[i] = to_bf16(host[i]);
-    hip_ok(hipMemcpy(p, b.data(), bytes, hipMemcpyHostToDevice), "upload");
-  } else {
-    hip_ok(hipMemcpy(p, host, bytes, hipMemcpyHostToDevice), "upload");
+  size_t off = 0;
+  for (const auto& [host, cnt] : parts) {
+    char* dst = static_cast<char*>(p) + off * esz;
+    if (as_bf16) {
+      std::vector<uint16_t> b(cnt);
+      for (size_t i = 0; i < cnt; i++) b[i] = to_bf16(host[i]);
+      hip_ok(hipMemcpy(dst, b.data(), cnt * 2, hipMemcpyHostToDevice), "upload");
+    } else {
+      hip_ok(hipMemcpy(dst, host, cnt * 4, hipMemcpyHostToDevice), "upload");
+    }
+    off += cnt;
   }
   return p;
 }
@@ -248,57 +260,52 @@ void Model::forward(const le_step_slice* slices, int n_slices, int32_t* tokens_o
   const int32_t* d_slots = le_plan_dev_array(&plan, plan.off_slots);
   const int32_t* d_rows = le_plan_dev_array(&plan, plan.off_logit_rows);
   const size_t n = static_cast<size_t>(N);
+  const int QKV = QD_ + 2 * KVD_;
   void* x = x_.get(n * H_ * act_);
-  void* h = h_.get(n * std::max(H_, QD_) * act_);
+  void* h = h_.get(n * H_ * act_);
+  void* qkv = qkv_.get(n * QKV * act_);
   void* q = q_.get(n * QD_ * act_);
-  void* k = k_.get(n * KVD_ * act_);
-  void* v = v_.get(n * KVD_ * act_);
   void* attn = attn_.get(n * QD_ * act_);
-  void* o = o_.get(n * std::max(H_, QD_) * act_);
-  void* gate = gate_.get(n * I_ * act_);
-  void* up = up_.get(n * I_ * act_);
+  void* o = o_.get(n * H_ * act_);
+  void* gate_up = gate_up_.get(n * 2 * I_ * act_);
+  void* act = act_buf_.get(n * I_ * act_);
   const size_t ws_bytes = le_ragged_workspace_size(&plan);
   void* ws = ws_bytes ? ws_.get(ws_bytes, /*zero=*/true, stream_) : nullptr;
   const float scale = 1.0f / std::sqrt(static_cast<float>(hd_));
-  const int act_dt = bf16_ ? LE_BF16 : LE_F32, kv_dt = kv_bf16_ ? LE_BF16 : LE_F32;
+  const le_dtype act_dt = bf16_ ? LE_BF16 : LE_F32, kv_dt = kv_bf16_ ? LE_BF16 : LE_F32;
   const int64_t num_slots = static_cast<int64_t>(num_blocks_) * bs_;
+  const int L_n = static_cast<int>(layers_.size());
 
+  // Per layer: norm (fused with the previous residual add), one QKV GEMM, one
+  // bias+RoPE+cache-write launch, attention, O GEMM, residual+norm, one
+  // gate|up GEMM, SiLU product, down GEMM.
   hip_ok(gather_rows(embed_, d_ids, x, N, H_, bf16_, stream_), "embedding");
-  for (size_t l = 0; l < layers_.size(); l++) {
+  hip_ok(residual_rmsnorm(x, nullptr, nullptr, layers_[0].in_norm, h, N, H_, d_.eps, false, bf16_, stream_),
+         "rmsnorm");
+  for (int l = 0; l < L_n; l++) {
     const Layer& L = layers_[l];
-    hip_ok(rmsnorm(x, L.in_norm, h, N, H_, d_.eps, bf16_, stream_), "rmsnorm");
-    gemm(h, L.wq, q, N, QD_, H_);
-    gemm(h, L.wk, k, N, KVD_, H_);
-    gemm(h, L.wv, v, N, KVD_, H_);
-    if (L.bq) {
-      hip_ok(add_bias(q, L.bq, N, QD_, bf16_, stream_), "bias");
-      hip_ok(add_bias(k, L.bk, N, KVD_, bf16_, stream_), "bias");
-      hip_ok(add_bias(v, L.bv, N, KVD_, bf16_, stream_), "bias");
-    }
+    gemm(h, L.wqkv, qkv, N, QKV, H_);
     // Every token's K/V is rotated and written before attention runs, so
     // tokens of one step (a prefill chunk) attend to each other.
-    hip_ok(rope(q, d_pos, cos_, sin_, N, nh_, hd_, QD_, bf16_, stream_), "rope");
-    hip_ok(rope(k, d_pos, cos_, sin_, N, nkv_, hd_, KVD_, bf16_, stream_), "rope");
-    le_ok(le_kv_cache_write(k, v, static_cast<le_dtype>(act_dt), d_slots, kc_[l], vc_[l],
-                            static_cast<le_dtype>(kv_dt), N, KVD_, num_slots, stream_),
-          "le_kv_cache_write");
-    le_ok(le_ragged_paged_attention(q, static_cast<le_dtype>(act_dt), kc_[l], vc_[l],
-                                    static_cast<le_dtype>(kv_dt), num_blocks_, &plan, scale, attn, ws,
+    le_ok(le_rope_kv_cache_write(qkv, act_dt, QKV, L.bqkv, d_pos, d_slots, cos_, sin_, d_.max_pos, N,
+                                 nh_, nkv_, hd_, q, kc_[l], vc_[l], kv_dt, num_slots, stream_),
+          "le_rope_kv_cache_write");
+    le_ok(le_ragged_paged_attention(q, act_dt, kc_[l], vc_[l], kv_dt, num_blocks_, &plan, scale, attn, ws,
                                     ws_bytes, stream_),
           "le_ragged_paged_attention");
     gemm(attn, L.wo, o, N, H_, QD_);
-    hip_ok(add_inplace(x, o, static_cast<int64_t>(N) * H_, bf16_, stream_), "residual");
-    hip_ok(rmsnorm(x, L.post_norm, h, N, H_, d_.eps, bf16_, stream_), "rmsnorm");
-    gemm(h, L.wgate, gate, N, I_, H_);
-    gemm(h, L.wup, up, N, I_, H_);
-    hip_ok(silu_mul(gate, up, static_cast<int64_t>(N) * I_, bf16_, stream_), "silu_mul");
-    gemm(gate, L.wdown, o, N, H_, I_);
-    hip_ok(add_inplace(x, o, static_cast<int64_t>(N) * H_, bf16_, stream_), "residual");
+    hip_ok(residual_rmsnorm(x, o, nullptr, L.post_norm, h, N, H_, d_.eps, true, bf16_, stream_), "residual");
+    gemm(h, L.wgate_up, gate_up, N, 2 * I_, H_);
+    hip_ok(silu_mul_split(gate_up, act, N, I_, bf16_, stream_), "silu_mul");
+    gemm(act, L.wdown, o, N, H_, I_);
+    if (l + 1 < L_n)
+      hip_ok(residual_rmsnorm(x, o, nullptr, layers_[l + 1].in_norm, h, N, H_, d_.eps, true, bf16_, stream_),
+             "residual");
   }
   if (R > 0) {
-    void* rows = rows_.get(static_cast<size_t>(R) * H_ * act_);
-    hip_ok(gather_rows(x, d_rows, rows, R, H_, bf16_, stream_), "logit rows");
-    hip_ok(rmsnorm(rows, final_norm_, h, R, H_, d_.eps, bf16_, stream_), "final norm");
+    // The last residual add and the final norm, on the logit rows only.
+    hip_ok(residual_rmsnorm(x, o, d_rows, final_norm_, h, R, H_, d_.eps, false, bf16_, stream_),
+           "final norm");
     float* logits = static_cast<float*>(logits_.get(static_cast<size_t>(R) * V_ * 4));
     gemm(h, lm_head_, logits, R, V_, H_, /*c_f32=*/true);
     int32_t* dtok = static_cast<int32_t*>(tokens_.get(static_cast<size_t>(R) * 4));
@@ -411,6 +418,7 @@ int le_run_greedy(le_model* m, const le_sched_config* cfg, int prefix_caching, i
     size_t next = 0;
 
     le_run_stats rs{};
+    std::vector<double> first_tok(static_cast<size_t>(n_seqs), -1.0), last_tok(static_cast<size_t>(n_seqs), -1.0);
     const auto t0 = std::chrono::steady_clock::now();
     auto elapsed = [&]() { return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count(); };
     std::vector<le_step_slice> sl;
@@ -437,13 +445,36 @@ int le_run_greedy(le_model* m, const le_sched_config* cfg, int prefix_caching, i
       sampled.assign(static_cast<size_t>(step.num_logits), 0);
       const double ts = elapsed();
       model.forward(sl.data(), static_cast<int>(sl.size()), sampled.data(), nullptr);
-      if (step.num_prefill_tokens == 0) rs.decode_seconds += elapsed() - ts;
+      const double te = elapsed();
+      if (step.num_prefill_tokens == 0) {
+        rs.decode_seconds += te - ts;
+        rs.decode_steps++;
+        rs.decode_step_tokens += step.num_logits;
+      }
       rs.steps++;
       rs.prompt_tokens += step.num_prefill_tokens;
       rs.decode_tokens += step.num_logits;
       sch.on_step_done(step, sampled);
+      for (const auto& s : step.slices) {
+        if (!s.needs_logits) continue;
+        const size_t i = static_cast<size_t>(s.seq->id);
+        if (first_tok[i] < 0) first_tok[i] = te;
+        last_tok[i] = te;
+      }
     }
     rs.seconds = elapsed();
+    int n_done = 0;
+    for (int i = 0; i < n_seqs; i++) {
+      if (first_tok[i] < 0) continue;
+      const double arr = arrival_s ? arrival_s[i] : 0.0;
+      rs.ttft_mean_s += first_tok[i] - arr;
+      rs.latency_mean_s += last_tok[i] - arr;
+      n_done++;
+    }
+    if (n_done) {
+      rs.ttft_mean_s /= n_done;
+      rs.latency_mean_s /= n_done;
+    }
     rs.preemptions = static_cast<int64_t>(sch.stats().preemptions);
     for (size_t i = 1; i < held.size(); i += 2) kv.free(held[i]);
     size_t out_off = 0;  // gen_out: max_tokens[i] entries per sequence, back to back

@@ -1,6 +1,7 @@
 // Layer kernels around the attention path for the device model: embedding
-// gather, RMSNorm, RoPE, SiLU-gated product, residual and bias adds, logit-row
-// gather and greedy argmax. Each restates one reference op (ops.h, the CUDA
+// gather, residual add + RMSNorm (optionally over gathered logit rows), the
+// SiLU-gated product and greedy argmax. Bias and RoPE are fused into the K/V
+// cache write (rope_kv_write.hip). Each restates one reference op (ops.h, the CUDA
 // kernels in src/kernels/) for fp32 or bf16 activations; the math is fp32.
 #include <float.h>
 
@@ -26,16 +27,32 @@ __global__ void gather_rows_kernel(const T* __restrict__ table, const int32_t* _
   for (int j = threadIdx.x; j < cols; j += blockDim.x) out[dst + j] = table[src + j];
 }
 
-// out[r] = x[r] * rsqrt(mean(x[r]^2) + eps) * w (ops.h:22-31); one workgroup per row,
-// fp32 sum of squares.
+// Residual add fused with the RMSNorm that follows it: cuda_model.cu:381+384,
+// 390 + the next layer's 353, and 390 + the head's 404-409 (only the logit
+// rows are added and normalised there).
+// Output row b reads source row r = rows ? rows[b] : b; v = x[r] + y[r] rounded to T as the separate add
+// stores it, written back to x[r] when write_x; out[b] = rmsnorm(v) * w with
+// a thread-strided fp32 sum of squares reduced per wave, then across the
+// four waves. y == nullptr is a plain norm.
 template <typename T>
-__global__ __launch_bounds__(256) void rmsnorm_kernel(const T* __restrict__ x, const float* __restrict__ w,
-                                                      T* __restrict__ out, int cols, float eps) {
-  const T* xr = x + static_cast<int64_t>(blockIdx.x) * cols;
+__global__ __launch_bounds__(256) void residual_rmsnorm_kernel(T* __restrict__ x, const T* __restrict__ y,
+                                                               const int32_t* __restrict__ rows,
+                                                               const float* __restrict__ w,
+                                                               T* __restrict__ out, int cols, float eps,
+                                                               int write_x) {
+  const int64_t r = rows ? rows[blockIdx.x] : blockIdx.x;
+  T* xr = x + r * cols;
+  const T* yr = y ? y + r * cols : nullptr;
   T* o = out + static_cast<int64_t>(blockIdx.x) * cols;
   float ss = 0.f;
   for (int j = threadIdx.x; j < cols; j += 256) {
-    const float v = ld(xr + j);
+    float v = ld(xr + j);
+    if (yr) {
+      T tmp;
+      st(&tmp, v + ld(yr + j));
+      v = ld(&tmp);
+      if (write_x) xr[j] = tmp;
+    }
     ss += v * v;
   }
   __shared__ float part[4];
@@ -44,50 +61,32 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const T* __restrict__ x, c
   __syncthreads();
   const float tot = (part[0] + part[1]) + (part[2] + part[3]);
   const float inv = 1.0f / sqrtf(tot / cols + eps);
-  for (int j = threadIdx.x; j < cols; j += 256) st(o + j, ld(xr + j) * inv * w[j]);
-}
-
-// rotate_half RoPE in place on `heads` heads of each row (ops.h:55-66).
-template <typename T>
-__global__ void rope_kernel(T* __restrict__ x, const int32_t* __restrict__ positions,
-                            const float* __restrict__ cos_t, const float* __restrict__ sin_t,
-                            int heads, int head_dim, int row_stride) {
-  const int half = head_dim / 2;
-  const int t = blockIdx.x;
-  const int64_t tab = static_cast<int64_t>(positions[t]) * half;
-  T* row = x + static_cast<int64_t>(t) * row_stride;
-  for (int i = threadIdx.x; i < heads * half; i += blockDim.x) {
-    const int h = i / half, k = i - h * half;
-    T* v = row + h * head_dim;
-    const float c = cos_t[tab + k], s = sin_t[tab + k];
-    const float a = ld(v + k), b = ld(v + k + half);
-    st(v + k, a * c - b * s);
-    st(v + k + half, b * c + a * s);
+  for (int j = threadIdx.x; j < cols; j += 256) {
+    float v;
+    if (yr && write_x) {
+      v = ld(xr + j);  // this thread's own store above
+    } else if (yr) {
+      T tmp;
+      st(&tmp, ld(xr + j) + ld(yr + j));
+      v = ld(&tmp);
+    } else {
+      v = ld(xr + j);
+    }
+    st(o + j, v * inv * w[j]);
   }
 }
 
-// gate = silu(gate) * up (ops.h:69-74)
+// act[t][j] = silu(gu[t][j]) * gu[t][inter + j]: the SiLU-gated product over
+// the fused gate|up projection output (ops.h:69-74, elementwise.cu).
 template <typename T>
-__global__ void silu_mul_kernel(T* __restrict__ gate, const T* __restrict__ up, int64_t n) {
+__global__ void silu_mul_split_kernel(const T* __restrict__ gu, T* __restrict__ act, int inter, int64_t n) {
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const float g = ld(gate + i);
-    st(gate + i, g / (1.0f + expf(-g)) * ld(up + i));
+    const int64_t t = i / inter, j = i - t * inter;
+    const T* row = gu + t * 2 * inter;
+    const float g = ld(row + j);
+    st(act + i, g / (1.0f + expf(-g)) * ld(row + inter + j));
   }
-}
-
-template <typename T>
-__global__ void add_kernel(T* __restrict__ x, const T* __restrict__ y, int64_t n) {
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
-    st(x + i, ld(x + i) + ld(y + i));
-}
-
-template <typename T>
-__global__ void add_bias_kernel(T* __restrict__ x, const float* __restrict__ bias, int cols, int64_t n) {
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
-    st(x + i, ld(x + i) + bias[i % cols]);
 }
 
 // Greedy token per logits row: the first maximum wins (sampler.cpp:9-13).
@@ -139,40 +138,20 @@ hipError_t gather_rows(const void* table, const int32_t* ids, void* out, int n, 
   return hipGetLastError();
 }
 
-hipError_t rmsnorm(const void* x, const float* w, void* out, int rows, int cols, float eps, bool bf16,
-                   hipStream_t s) {
-  if (rows <= 0) return hipSuccess;
-  LE_DISPATCH(bf16, rmsnorm_kernel<T><<<rows, 256, 0, s>>>(static_cast<const T*>(x), w,
-                                                           static_cast<T*>(out), cols, eps));
+hipError_t residual_rmsnorm(void* x, const void* y, const int32_t* rows, const float* w, void* out,
+                            int n_out, int cols, float eps, bool write_x, bool bf16, hipStream_t s) {
+  if (n_out <= 0) return hipSuccess;
+  LE_DISPATCH(bf16, residual_rmsnorm_kernel<T><<<n_out, 256, 0, s>>>(
+                        static_cast<T*>(x), static_cast<const T*>(y), rows, w, static_cast<T*>(out), cols,
+                        eps, write_x ? 1 : 0));
   return hipGetLastError();
 }
 
-hipError_t rope(void* x, const int32_t* positions, const float* cos_t, const float* sin_t, int n,
-                int heads, int head_dim, int row_stride, bool bf16, hipStream_t s) {
+hipError_t silu_mul_split(const void* gate_up, void* act, int rows, int inter, bool bf16, hipStream_t s) {
+  const int64_t n = static_cast<int64_t>(rows) * inter;
   if (n <= 0) return hipSuccess;
-  LE_DISPATCH(bf16, rope_kernel<T><<<n, 256, 0, s>>>(static_cast<T*>(x), positions, cos_t, sin_t,
-                                                      heads, head_dim, row_stride));
-  return hipGetLastError();
-}
-
-hipError_t silu_mul(void* gate, const void* up, int64_t n, bool bf16, hipStream_t s) {
-  if (n <= 0) return hipSuccess;
-  LE_DISPATCH(bf16, silu_mul_kernel<T><<<grid_for(n), 256, 0, s>>>(static_cast<T*>(gate),
-                                                                    static_cast<const T*>(up), n));
-  return hipGetLastError();
-}
-
-hipError_t add_inplace(void* x, const void* y, int64_t n, bool bf16, hipStream_t s) {
-  if (n <= 0) return hipSuccess;
-  LE_DISPATCH(bf16, add_kernel<T><<<grid_for(n), 256, 0, s>>>(static_cast<T*>(x),
-                                                               static_cast<const T*>(y), n));
-  return hipGetLastError();
-}
-
-hipError_t add_bias(void* x, const float* bias, int rows, int cols, bool bf16, hipStream_t s) {
-  const int64_t n = static_cast<int64_t>(rows) * cols;
-  if (n <= 0) return hipSuccess;
-  LE_DISPATCH(bf16, add_bias_kernel<T><<<grid_for(n), 256, 0, s>>>(static_cast<T*>(x), bias, cols, n));
+  LE_DISPATCH(bf16, silu_mul_split_kernel<T><<<grid_for(n), 256, 0, s>>>(
+                        static_cast<const T*>(gate_up), static_cast<T*>(act), inter, n));
   return hipGetLastError();
 }
 

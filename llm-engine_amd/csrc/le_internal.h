@@ -43,6 +43,11 @@ struct CombineItem {
 hipError_t kv_cache_write(const void* k, const void* v, int src_bf16, const int32_t* slots,
                           void* kc, void* vc, int cache_bf16, int n_tokens, int kv_dim,
                           int64_t num_slots, hipStream_t stream);
+hipError_t rope_kv_cache_write(const void* qkv, int act_bf16, int64_t row_stride, const float* bias,
+                               const int32_t* positions, const int32_t* slots, const float* cos_t,
+                               const float* sin_t, int max_pos, int n_tokens, int q_heads,
+                               int kv_heads, int head_dim, void* q_out, void* kc, void* vc,
+                               int cache_bf16, int64_t num_slots, hipStream_t stream);
 
 struct DecodeParams {
   const void* q;

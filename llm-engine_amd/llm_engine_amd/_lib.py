@@ -112,7 +112,9 @@ class ModelDesc(ctypes.Structure):
 class RunStats(ctypes.Structure):
     _fields_ = [("steps", ctypes.c_int64), ("prompt_tokens", ctypes.c_int64),
                 ("decode_tokens", ctypes.c_int64), ("preemptions", ctypes.c_int64),
-                ("seconds", ctypes.c_double), ("decode_seconds", ctypes.c_double)]
+                ("seconds", ctypes.c_double), ("decode_seconds", ctypes.c_double),
+                ("decode_steps", ctypes.c_int64), ("decode_step_tokens", ctypes.c_int64),
+                ("ttft_mean_s", ctypes.c_double), ("latency_mean_s", ctypes.c_double)]
 
 
 # name -> (restype, argtypes). Exactly the symbols include/*.h declare.
@@ -123,6 +125,11 @@ SIGNATURES = {
         ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
         ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64,
         ctypes.c_void_p]),
+    "le_rope_kv_cache_write": (ctypes.c_int, [
+        ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+        ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+        ctypes.c_int64, ctypes.c_void_p]),
     "le_attention_decode_workspace_size": (ctypes.c_size_t, [
         ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "le_attention_decode": (ctypes.c_int, [

@@ -63,6 +63,37 @@ def store_kv(k: torch.Tensor, v: torch.Tensor, slots: torch.Tensor, k_cache: tor
         num_slots, _stream(stream)))
 
 
+def rope_store_kv(qkv: torch.Tensor, positions: torch.Tensor, slots: torch.Tensor, cos_t: torch.Tensor,
+                  sin_t: torch.Tensor, q_heads: int, kv_heads: int, head_dim: int, k_cache: torch.Tensor,
+                  v_cache: torch.Tensor, bias: torch.Tensor | None = None, q_out: torch.Tensor | None = None,
+                  stream=None) -> torch.Tensor:
+    """Bias + RoPE + cache-write scatter over fused QKV rows
+    (cuda_model.cu:358-368 as one launch). qkv: [N, >= (q_heads + 2*kv_heads)*head_dim]
+    laid out [q | k | v]; cos_t/sin_t: fp32 [max_pos, head_dim/2]. Returns q: [N, q_heads*head_dim]."""
+    _req(qkv.dim() == 2 and qkv.stride(1) == 1, "qkv: [N, row] with unit column stride")
+    n = qkv.shape[0]
+    _req(qkv.shape[1] >= (q_heads + 2 * kv_heads) * head_dim, "qkv rows too short")
+    _req(cos_t.dtype == torch.float32 and cos_t.shape == sin_t.shape and cos_t.is_contiguous()
+         and sin_t.is_contiguous() and cos_t.shape[1] == head_dim // 2, "cos/sin: fp32 [max_pos, head_dim/2]")
+    kv_dim = kv_heads * head_dim
+    _req(k_cache.shape == v_cache.shape and k_cache.dtype == v_cache.dtype and k_cache.is_contiguous()
+         and v_cache.is_contiguous(), "k/v caches must match and be contiguous")
+    num_slots = k_cache.shape[0]
+    _req(k_cache.numel() == num_slots * kv_dim, "cache row size must equal kv_dim")
+    _dev_i32(positions, "positions", n)
+    _dev_i32(slots, "slots", n)
+    if bias is not None:
+        _req(bias.dtype == torch.float32 and bias.is_contiguous()
+             and bias.numel() == (q_heads + 2 * kv_heads) * head_dim, "bias: fp32 [q_dim + 2*kv_dim]")
+    if q_out is None:
+        q_out = torch.empty(n, q_heads * head_dim, dtype=qkv.dtype, device=qkv.device)
+    check("le_rope_kv_cache_write", _lib.load().le_rope_kv_cache_write(
+        _p(qkv), _dt(qkv), qkv.stride(0), None if bias is None else _p(bias), _p(positions), _p(slots),
+        _p(cos_t), _p(sin_t), cos_t.shape[0], n, q_heads, kv_heads, head_dim, _p(q_out), _p(k_cache),
+        _p(v_cache), _dt(k_cache), num_slots, _stream(stream)))
+    return q_out
+
+
 def new_workspace(nbytes: int, device="cuda") -> torch.Tensor:
     """A workspace for the attention calls: zero-filled once, as the ABI requires
     (the kernels leave its arrival counters at zero after every launch)."""

@@ -200,6 +200,19 @@ def rope_tables(head_dim, max_pos, theta):
     return c, s
 
 
+def rope(x, positions, cos_t, sin_t, heads, head_dim):
+    """RoPE (rotate_half) in place on the first heads*head_dim columns of each
+    row of x (fp32 [N, cols]) at positions[t]."""
+    assert x.dtype == np.float32 and x.flags.c_contiguous
+    L = lib()
+    row_bytes = x.strides[0]
+    base = x.ctypes.data
+    for t, p in enumerate(np.asarray(positions, dtype=np.int64)):
+        L.orc_rope_inplace(ctypes.c_void_p(base + t * row_bytes), heads, head_dim, int(p), ptr(cos_t),
+                           ptr(sin_t))
+    return x
+
+
 def linear(a, b, bias=None, threads=None):
     a = np.ascontiguousarray(a, dtype=np.float32)
     b = np.ascontiguousarray(b, dtype=np.float32)

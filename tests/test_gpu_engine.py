@@ -127,3 +127,56 @@ def test_first_step_logits_close(gpu):
         assert err < 1e-3
         sch.done(toks)
     m.close()
+
+
+def _round_weights_bf16(w):
+    """The same model with every weight rounded to bf16 (round to nearest
+    even), held in fp32: what the bf16 device model computes with."""
+    import oracle
+    r = lambda a: oracle.bf16_to_f32(oracle.f32_to_bf16(a)).reshape(a.shape)
+    w.embed = r(w.embed)
+    if w.lm_head is not None:
+        w.lm_head = r(w.lm_head)
+    for L in w.layers:
+        for k in ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown"):
+            L[k] = r(L[k])
+    return w
+
+
+@pytest.mark.parametrize("arch", ["qwen2.5-0.5b", "tinyllama-1.1b"])
+def test_bf16_model_logits_close(gpu, arch):
+    """bf16 weights, activations and K/V (the config-4 precision) against the
+    fp32 oracle run on the same bf16-rounded weights with a bf16 K/V cache:
+    the difference is the rounding of activations between ops, so the
+    tolerance is relative to the logit scale: max|err| <= 5 % of max|logit|
+    over three steps (mixed prefill + decode), and the greedy tokens agree
+    wherever the oracle's top-2 margin exceeds twice that error."""
+    from e2e_util import OracleModel, top2_margin
+    from llm_engine_amd.engine import Model, Scheduler, sched_config, synthetic_weights
+    w = _round_weights_bf16(synthetic_weights(arch, 21, layers=2))
+    prompts = prompts_of(8, (90, 33, 260), w.arch["vocab"])
+    m = Model(w, 128, 16, dtype="bf16", kv_dtype="bf16")
+    o = OracleModel(w, 128, kv_bf16=True)
+    sch = Scheduler(128, 16, sched_config(max_num_batched_tokens=256), fragment_blocks=12)
+    for i, p in enumerate(prompts):
+        sch.add(i, p, 6)
+    checked = 0
+    for _ in range(5):
+        if not sch.has_work():
+            break
+        sl = sch.step()
+        n = sum(int(s.needs_logits) for s in sl)
+        toks, lg = m.forward(sl, n, want_logits=True)
+        want = o.logits(sl)
+        err = float(np.max(np.abs(lg - want))) if n else 0.0
+        scale = float(np.abs(want).max()) if n else 1.0
+        print(f"{arch} bf16 step: {n} rows, max|err| {err:.3e}, max|logit| {scale:.3f}")
+        assert err <= 0.05 * scale
+        for r in range(n):
+            if top2_margin(want[r]) > 2 * err:
+                assert toks[r] == int(np.argmax(want[r]))
+                checked += 1
+        # both models continue from the device's tokens
+        sch.done(toks)
+    m.close()
+    print(f"{arch}: {checked} greedy tokens checked against clear oracle margins")

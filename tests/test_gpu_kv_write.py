@@ -53,3 +53,78 @@ def test_kv_write_padding_and_shapes(gpu):
     _run(False, True, 1000, 256, 512, 16, seed=2, pad_every=7)  # TinyLlama kv_dim 256
     _run(False, False, 1, 128, 4, 16, seed=3)
     _run(True, True, 4096, 128, 4096, 16, seed=4)
+
+
+def _run_fused(act_bf16, cache_bf16, n_tokens, q_heads, kv_heads, head_dim, num_blocks, seed,
+               bias=True, pad_every=0, bad_pos_every=0, stride_pad=0, max_pos=4096, theta=1e6):
+    """le_rope_kv_cache_write against the oracle's own sequence: bias add
+    (rounded to the activation dtype, as a separate add stores it), RoPE
+    (ops.h:55-66), store_kv (store_kv.cu:20-36). Bit-exact: q, and every slot
+    of both caches."""
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(seed)
+    bs = 16
+    qd, kvd = q_heads * head_dim, kv_heads * head_dim
+    row = qd + 2 * kvd + stride_pad
+    slots_total = num_blocks * bs
+    slots = rng.permutation(slots_total)[:n_tokens].astype(np.int32)
+    pos = rng.integers(0, max_pos, size=n_tokens).astype(np.int32)
+    if pad_every:
+        slots[::pad_every] = -1
+    if bad_pos_every:
+        pos[1::bad_pos_every] = max_pos + 3
+        pos[2::bad_pos_every] = -1
+    qkv = rng.standard_normal((n_tokens, row), dtype=np.float32)
+    b = rng.standard_normal(qd + 2 * kvd, dtype=np.float32) if bias else None
+    rnd = (lambda a: oracle.bf16_to_f32(oracle.f32_to_bf16(a))) if act_bf16 else (lambda a: a)
+    qkv = rnd(qkv)
+    cos_t, sin_t = oracle.rope_tables(head_dim, max_pos, theta)
+
+    # oracle side
+    x = qkv[:, :qd + 2 * kvd].copy()
+    if b is not None:
+        x = rnd(x + b[None, :])
+    x = np.ascontiguousarray(x)
+    ok_pos = (pos >= 0) & (pos < max_pos)
+    xr = x.copy()
+    oracle.rope(xr, np.where(ok_pos, pos, 0), cos_t, sin_t, q_heads + kv_heads, head_dim)
+    want_q = rnd(np.where(ok_pos[:, None], xr[:, :qd], 0.0).astype(np.float32))
+    k_rows, v_rows = xr[:, qd:qd + kvd], x[:, qd + kvd:]
+    cdt = np.uint16 if cache_bf16 else np.float32
+    init_k = rng.integers(0, 2**16, size=(slots_total, kvd)).astype(cdt) if cache_bf16 else \
+        rng.standard_normal((slots_total, kvd), dtype=np.float32)
+    init_v = init_k[::-1].copy()
+    want_k, want_v = init_k.copy(), init_v.copy()
+    ok = (slots >= 0) & ok_pos
+    oracle.store_kv(np.ascontiguousarray(k_rows[ok]), np.ascontiguousarray(v_rows[ok]), slots[ok], want_k, want_v)
+
+    from llm_engine_amd import kernels
+    tdt = torch.bfloat16 if act_bf16 else torch.float32
+    qkv_d = torch.from_numpy(qkv).to(dev).to(tdt)
+    kc, vc = to_dev_cache(init_k, dev), to_dev_cache(init_v, dev)
+    bias_d = None if b is None else torch.from_numpy(b).to(dev)
+    q = kernels.rope_store_kv(qkv_d, i32(pos, dev), i32(slots, dev), torch.from_numpy(cos_t).to(dev),
+                              torch.from_numpy(sin_t).to(dev), q_heads, kv_heads, head_dim, kc, vc, bias=bias_d)
+    torch.cuda.synchronize()
+    got_q = q.float().cpu().numpy()
+    assert np.array_equal(got_q.view(np.uint32), want_q.view(np.uint32)), \
+        f"q mismatch: max|diff| {np.abs(got_q - want_q).max()}"
+    got_k = kc.cpu().view(torch.int16).numpy().view(np.uint16) if cache_bf16 else kc.cpu().numpy()
+    got_v = vc.cpu().view(torch.int16).numpy().view(np.uint16) if cache_bf16 else vc.cpu().numpy()
+    assert np.array_equal(got_k.view(np.uint8), want_k.view(np.uint8))
+    assert np.array_equal(got_v.view(np.uint8), want_v.view(np.uint8))
+
+
+@pytest.mark.parametrize("act_bf16,cache_bf16", [(False, False), (False, True), (True, True)])
+def test_rope_kv_write_qwen_step(gpu, act_bf16, cache_bf16):
+    """Qwen2.5-0.5B shape (14/2 x 64, qkv bias), a 544-row mixed step into a
+    fragmented 16384-block pool."""
+    _run_fused(act_bf16, cache_bf16, 544, 14, 2, 64, 16384, seed=5)
+
+
+def test_rope_kv_write_edges(gpu):
+    """TinyLlama shape without bias; padding slots, out-of-range positions,
+    a padded qkv row stride, a single token, head_dim 128."""
+    _run_fused(True, True, 300, 32, 4, 64, 1024, seed=6, bias=False, pad_every=5, theta=1e4, max_pos=2048)
+    _run_fused(False, False, 257, 14, 2, 64, 512, seed=7, bad_pos_every=9, stride_pad=8)
+    _run_fused(False, True, 1, 8, 1, 128, 4, seed=8)
