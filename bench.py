@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--kv bf16|f32]
                     [--workload config2|target|config3] [--no-cpu-baseline]
-                    [--e2e decode64|config4|both|none]
+                    [--e2e decode64|config4|config5|all|none]
 
 A step is one decode pass of the hot path over one ragged batch, for every
 layer of the model: the packed step metadata is uploaded once (one async
@@ -19,8 +19,9 @@ Workloads (Qwen2.5-0.5B GQA: 14 q heads, 2 kv heads, head_dim 64, block 16):
 After the attention measurement, an end-to-end leg runs the whole engine
 (scheduler, packing, device model, greedy) on TinyLlama-1.1B with bf16
 weights and K/V (benchmark config 4 shape) and reports decode tok/s at
-64 sequences under "e2e_decode64" (and the Poisson serving run under
-"e2e_config4" with --e2e config4|both).
+64 sequences under "e2e_decode64"; --e2e config4 / config5 / all run the
+Poisson serving workload and the shared-prefix + preemption stress instead
+or as well.
 
 Prints ONE JSON line. `value` is algorithmic HBM bytes per step / step time:
 K/V of each kv head once (the GQA-shared minimum), q, out, block tables and
@@ -120,49 +121,65 @@ def cpu_baseline(ctx, q_len, kv_bf16: bool, budget_s: float):
                       f"(token, head) loop on {threads} threads"}
 
 
-def e2e_decode(n_seqs=64, gen=256, seed=4, arrivals=None, layers=None):
-    """End-to-end continuous batching on the device model, config 4's shape:
-    TinyLlama-1.1B architecture, random-init weights N(0, 0.02) held as bf16 on
-    the device, bf16 K/V cache, block 16, chunked prefill budget 512 tokens per
-    step, at most 64 running, prompts uniform in [128, 1024].
-
-    Closed loop (arrivals None): n_seqs requests at t=0, `gen` greedy tokens
-    each; decode tok/s = tokens sampled in steps with no prefill / their wall
-    time (host scheduling, packing, upload, all layers, greedy read-back).
-    Serving (arrivals = Poisson rate, requests/s): output lengths uniform in
-    [64, 256]; tok/s = generated tokens / wall time of the loop."""
+def e2e_run(arch, prompts, out_lens, pool_blocks, max_seqs=64, budget=512, arrivals_s=None,
+            prefix_caching=False, seed=4, layers=None):
+    """One end-to-end run of the engine: scheduler, packing, device model,
+    device greedy. Random-init weights N(0, 0.02) held as bf16 on the device,
+    bf16 K/V cache, block 16, chunked prefill budget `budget` tokens/step."""
     from llm_engine_amd.engine import Model, sched_config, synthetic_weights
-    rng = np.random.default_rng(seed)
     t0 = time.perf_counter()
-    w = synthetic_weights("tinyllama-1.1b", seed, layers=layers)
-    V, L = w.arch["vocab"], w.arch["layers"]
-    lens = rng.integers(128, 1025, size=n_seqs)
-    prompts = [rng.integers(0, V, int(x)).astype(np.int32) for x in lens]
-    if arrivals:
-        out_lens = rng.integers(64, 257, size=n_seqs).tolist()
-        t_arr = np.cumsum(rng.exponential(1.0 / arrivals, size=n_seqs)).tolist()
-    else:
-        out_lens, t_arr = [gen] * n_seqs, None
-    blocks = int(64 * (1024 + 256) // 16 * 1.25)
-    m = Model(w, blocks, 16, dtype="bf16", kv_dtype="bf16")
+    w = synthetic_weights(arch, seed, layers=layers)
+    L = w.arch["layers"]
+    m = Model(w, pool_blocks, 16, dtype="bf16", kv_dtype="bf16")
     del w
-    load_s = time.perf_counter() - t0
-    cfg = sched_config(max_num_seqs=64, max_num_batched_tokens=512, prefill_chunk_size=512)
+    setup_s = time.perf_counter() - t0
+    cfg = sched_config(max_num_seqs=max_seqs, max_num_batched_tokens=budget, prefill_chunk_size=budget)
     m.run_greedy([p[:64] for p in prompts[:4]], [4] * 4, cfg)  # warm-up: code objects, rocBLAS
-    toks, st = m.run_greedy(prompts, out_lens, cfg, arrival_s=t_arr)
+    toks, st = m.run_greedy(prompts, out_lens, cfg, prefix_caching=prefix_caching, arrival_s=arrivals_s)
     m.close()
     gen_total = sum(len(t) for t in toks)
-    assert gen_total == sum(out_lens), "not every request finished"
-    r = {"model": f"tinyllama-1.1b, {L} layers, random-init bf16 weights, bf16 KV",
-         "requests": n_seqs, "arrivals_per_s": arrivals, "prompt_tokens": int(st.prompt_tokens),
-         "generated_tokens": gen_total, "steps": int(st.steps), "seconds": round(st.seconds, 3),
-         "tok_per_s": round(gen_total / st.seconds, 1),
-         "decode_steps": int(st.decode_steps),
-         "decode_tok_per_s": round(st.decode_step_tokens / st.decode_seconds, 1) if st.decode_seconds else None,
-         "decode_ms_per_step": round(1e3 * st.decode_seconds / st.decode_steps, 3) if st.decode_steps else None,
-         "ttft_mean_s": round(st.ttft_mean_s, 4), "latency_mean_s": round(st.latency_mean_s, 3),
-         "preemptions": int(st.preemptions), "setup_s": round(load_s, 1)}
-    return r
+    if gen_total != sum(out_lens):
+        raise SystemExit("bench.py: not every request finished")
+    return {"model": f"{arch}, {L} layers, random-init bf16 weights, bf16 KV",
+            "requests": len(prompts), "pool_blocks": pool_blocks, "max_running": max_seqs,
+            "prefix_caching": prefix_caching, "prompt_tokens_computed": int(st.prompt_tokens),
+            "generated_tokens": gen_total, "steps": int(st.steps), "seconds": round(st.seconds, 3),
+            "tok_per_s": round(gen_total / st.seconds, 1), "decode_steps": int(st.decode_steps),
+            "decode_tok_per_s": round(st.decode_step_tokens / st.decode_seconds, 1) if st.decode_seconds else None,
+            "decode_ms_per_step": round(1e3 * st.decode_seconds / st.decode_steps, 3) if st.decode_steps else None,
+            "ttft_mean_s": round(st.ttft_mean_s, 4), "latency_mean_s": round(st.latency_mean_s, 3),
+            "preemptions": int(st.preemptions), "setup_s": round(setup_s, 1)}
+
+
+def e2e_leg(which, layers=None):
+    """The end-to-end workloads (TinyLlama-1.1B for decode64/config4, Qwen2.5-0.5B
+    for config5):
+      decode64  closed loop: 64 requests at t=0, prompts U[128, 1024], 256 greedy
+                tokens each, at most 64 running; decode tok/s = tokens sampled in
+                steps with no prefill / their wall time (host scheduling, packing,
+                upload, all layers, greedy read-back)
+      config4   256 requests, Poisson arrivals at 8/s, prompts U[128, 1024],
+                outputs U[64, 256], at most 64 running, budget 512
+      config5   128 requests sharing a 512-token prefix (prefix caching on) plus
+                unique suffixes U[64, 7680], 256 tokens each (contexts up to
+                8192), 16384-block pool: preemption and recompute under pressure."""
+    rng = np.random.default_rng(4)
+    if which in ("decode64", "config4"):
+        n = 64 if which == "decode64" else 256
+        V = 32000
+        prompts = [rng.integers(0, V, int(x)).astype(np.int32) for x in rng.integers(128, 1025, size=n)]
+        if which == "decode64":
+            return e2e_run("tinyllama-1.1b", prompts, [256] * n, 5120, layers=layers)
+        outs = rng.integers(64, 257, size=n).tolist()
+        arr = np.cumsum(rng.exponential(1.0 / 8.0, size=n)).tolist()
+        return e2e_run("tinyllama-1.1b", prompts, outs, 5120, arrivals_s=arr, layers=layers) | \
+            {"arrivals_per_s": 8.0}
+    V = 151936
+    prefix = rng.integers(0, V, 512)
+    prompts = [np.concatenate([prefix, rng.integers(0, V, int(x))]).astype(np.int32)
+               for x in rng.integers(64, 7681, size=128)]
+    return e2e_run("qwen2.5-0.5b", prompts, [256] * 128, 16384, max_seqs=128, prefix_caching=True,
+                   layers=layers)
 
 
 def main():
@@ -174,9 +191,9 @@ def main():
     ap.add_argument("--workload", choices=["config2", "target", "config3"], default="config2")
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--e2e", choices=["decode64", "config4", "both", "none"], default="decode64",
-                    help="end-to-end leg: closed-loop decode at 64 seqs, config-4 Poisson serving, both, none")
-    ap.add_argument("--e2e-layers", type=int, default=None, help="TinyLlama layers (default: all 22)")
+    ap.add_argument("--e2e", choices=["decode64", "config4", "config5", "all", "none"], default="decode64",
+                    help="end-to-end leg after the attention measurement (see e2e_leg)")
+    ap.add_argument("--e2e-layers", type=int, default=None, help="model layers (default: all)")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--partition", type=int, default=0, help="decode partition tokens (0 = planner's choice)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -304,10 +321,9 @@ def main():
         res["cpu_baseline"] = None
     del kc, vc, qs, knew, vnew, outs, ws, plan
     torch.cuda.empty_cache()
-    if args.e2e in ("decode64", "both"):
-        res["e2e_decode64"] = e2e_decode(64, 256, layers=args.e2e_layers)
-    if args.e2e in ("config4", "both"):
-        res["e2e_config4"] = e2e_decode(256, arrivals=8.0, layers=args.e2e_layers)
+    for leg in (["decode64", "config4", "config5"] if args.e2e == "all" else [args.e2e]):
+        if leg != "none":
+            res["e2e_" + leg] = e2e_leg(leg, layers=args.e2e_layers)
     print(json.dumps(res), flush=True)
 
 

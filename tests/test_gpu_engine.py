@@ -180,3 +180,32 @@ def test_bf16_model_logits_close(gpu, arch):
         sch.done(toks)
     m.close()
     print(f"{arch}: {checked} greedy tokens checked against clear oracle margins")
+
+
+@pytest.mark.parametrize("kv", ["f32", "bf16"])
+def test_config5_shared_prefix_preemption(gpu, kv):
+    """Config 5 at a size the oracle finishes in seconds: 128 sequences share a
+    512-token prefix (32 refcounted blocks, prefix caching on) plus unique
+    suffixes, in a pool small enough that the scheduler preempts and
+    recomputes. Qwen2.5-0.5B attention shape (14/2 x 64), 2 layers, vocab cut
+    to 8192 to keep the oracle's LM head cheap. Token for token against the
+    oracle driven by the same scheduler (fp32 path: exact; bf16 K/V: the
+    oracle stores bf16 too, agreement >= 90 %)."""
+    from llm_engine_amd.engine import ARCHS, sched_config, synthetic_weights
+    arch = dict(ARCHS["qwen2.5-0.5b"], vocab=8192)
+    w = synthetic_weights(arch, 31, layers=2)
+    rng = np.random.default_rng(12)
+    prefix = rng.integers(0, 8192, 512).tolist()
+    prompts = [prefix + rng.integers(0, 8192, int(n)).tolist() for n in rng.integers(16, 129, 128)]
+    cfg = sched_config(max_num_seqs=128, max_num_batched_tokens=2048)
+    gpu_t, cpu_t, st = run_both(w, prompts, [24] * 128, 200, cfg, prefix=True, kv=kv)
+    print(f"config5 small ({kv}): {st.steps} steps, {st.preemptions} preemptions, "
+          f"{st.prompt_tokens} prompt tokens computed")
+    assert st.preemptions > 0
+    assert all(len(t) == 24 for t in gpu_t)
+    if kv == "f32":
+        assert gpu_t == cpu_t
+    else:
+        agree = sum(a == b for g, c in zip(gpu_t, cpu_t) for a, b in zip(g, c))
+        print(f"bf16 K/V: {agree}/{24 * 128} tokens agree")
+        assert agree >= 0.9 * 24 * 128
