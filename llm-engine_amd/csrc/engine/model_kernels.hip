@@ -76,6 +76,110 @@ __global__ __launch_bounds__(256) void residual_rmsnorm_kernel(T* __restrict__ x
   }
 }
 
+// Vector form of residual_rmsnorm_kernel for rows of at most 4 x 256 x VEC
+// elements with cols % VEC == 0 (VEC = elements per 16 bytes): each thread
+// loads its pieces of x and y with 16-byte accesses, keeps the row in
+// registers between the sum of squares and the scaling, and stores with
+// 16-byte accesses. Same rounding of the residual sum as the scalar kernel;
+// the sum of squares is accumulated per thread over its pieces in order,
+// then reduced per wave and across the four waves.
+template <typename T> struct vec16;
+template <> struct vec16<float> {
+  static constexpr int N = 4;
+  __device__ __forceinline__ static void load(const float* p, float* o) {
+    const float4 r = *reinterpret_cast<const float4*>(p);
+    o[0] = r.x; o[1] = r.y; o[2] = r.z; o[3] = r.w;
+  }
+  __device__ __forceinline__ static void store(float* p, const float* v) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+  __device__ __forceinline__ static float round(float x) { return x; }
+};
+template <> struct vec16<bf16_t> {
+  static constexpr int N = 8;
+  __device__ __forceinline__ static void load(const bf16_t* p, float* o) { elem<bf16_t>::widen(ld16(p), o); }
+  __device__ __forceinline__ static void store(bf16_t* p, const float* v) {
+    *reinterpret_cast<uint4*>(p) = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                              pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
+  }
+  __device__ __forceinline__ static float round(float x) { return __uint_as_float(f32_to_bf16_bits(x) << 16); }
+};
+
+constexpr int kNormPieces = 4;  // 16-byte pieces per thread at most
+
+template <typename T>
+__global__ __launch_bounds__(256) void residual_rmsnorm_vec_kernel(T* __restrict__ x, const T* __restrict__ y,
+                                                                   const int32_t* __restrict__ rows,
+                                                                   const float* __restrict__ w,
+                                                                   T* __restrict__ out, int cols, float eps,
+                                                                   int write_x) {
+  constexpr int V = vec16<T>::N;
+  const int64_t r = rows ? rows[blockIdx.x] : blockIdx.x;
+  T* xr = x + r * cols;
+  const T* yr = y ? y + r * cols : nullptr;
+  T* o = out + static_cast<int64_t>(blockIdx.x) * cols;
+  const int pieces = cols / V;
+  float v[kNormPieces][V];
+  float yv[kNormPieces][V];
+#pragma unroll
+  for (int i = 0; i < kNormPieces; i++) {
+    const int pc = threadIdx.x + i * 256;
+    if (pc < pieces) {
+      vec16<T>::load(xr + pc * V, v[i]);
+      if (yr) vec16<T>::load(yr + pc * V, yv[i]);
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormPieces; i++) {
+    const int pc = threadIdx.x + i * 256;
+    if (pc < pieces) {
+      if (yr) {
+#pragma unroll
+        for (int e = 0; e < V; e++) v[i][e] = vec16<T>::round(v[i][e] + yv[i][e]);
+        if (write_x) vec16<T>::store(xr + pc * V, v[i]);
+      }
+#pragma unroll
+      for (int e = 0; e < V; e++) ss += v[i][e] * v[i][e];
+    }
+  }
+  __shared__ float part[4];
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float tot = (part[0] + part[1]) + (part[2] + part[3]);
+  const float inv = 1.0f / sqrtf(tot / cols + eps);
+#pragma unroll
+  for (int i = 0; i < kNormPieces; i++) {
+    const int pc = threadIdx.x + i * 256;
+    if (pc < pieces) {
+      float ov[V];
+#pragma unroll
+      for (int e = 0; e < V; e++) ov[e] = v[i][e] * inv * w[pc * V + e];
+      vec16<T>::store(o + pc * V, ov);
+    }
+  }
+}
+
+// act[t][j] = silu(gu[t][j]) * gu[t][inter + j], 16 bytes of output per
+// thread (inter % VEC == 0).
+template <typename T>
+__global__ void silu_mul_split_vec_kernel(const T* __restrict__ gu, T* __restrict__ act, int inter, int64_t n_pieces) {
+  constexpr int V = vec16<T>::N;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n_pieces) return;
+  const int per_row = inter / V;
+  const int64_t t = i / per_row;
+  const int j = static_cast<int>(i - t * per_row) * V;
+  const T* row = gu + t * 2 * inter;
+  float g[V], u[V], o[V];
+  vec16<T>::load(row + j, g);
+  vec16<T>::load(row + inter + j, u);
+#pragma unroll
+  for (int e = 0; e < V; e++) o[e] = g[e] / (1.0f + expf(-g[e])) * u[e];
+  vec16<T>::store(act + t * inter + j, o);
+}
+
 // act[t][j] = silu(gu[t][j]) * gu[t][inter + j]: the SiLU-gated product over
 // the fused gate|up projection output (ops.h:69-74, elementwise.cu).
 template <typename T>
@@ -141,6 +245,15 @@ hipError_t gather_rows(const void* table, const int32_t* ids, void* out, int n, 
 hipError_t residual_rmsnorm(void* x, const void* y, const int32_t* rows, const float* w, void* out,
                             int n_out, int cols, float eps, bool write_x, bool bf16, hipStream_t s) {
   if (n_out <= 0) return hipSuccess;
+  const int V = bf16 ? 8 : 4;
+  const bool aligned = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out) |
+                         reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(w)) & 15) == 0;
+  if (aligned && cols % V == 0 && cols <= 256 * V * kNormPieces) {
+    LE_DISPATCH(bf16, residual_rmsnorm_vec_kernel<T><<<n_out, 256, 0, s>>>(
+                          static_cast<T*>(x), static_cast<const T*>(y), rows, w, static_cast<T*>(out), cols,
+                          eps, write_x ? 1 : 0));
+    return hipGetLastError();
+  }
   LE_DISPATCH(bf16, residual_rmsnorm_kernel<T><<<n_out, 256, 0, s>>>(
                         static_cast<T*>(x), static_cast<const T*>(y), rows, w, static_cast<T*>(out), cols,
                         eps, write_x ? 1 : 0));
@@ -150,6 +263,13 @@ hipError_t residual_rmsnorm(void* x, const void* y, const int32_t* rows, const f
 hipError_t silu_mul_split(const void* gate_up, void* act, int rows, int inter, bool bf16, hipStream_t s) {
   const int64_t n = static_cast<int64_t>(rows) * inter;
   if (n <= 0) return hipSuccess;
+  const int V = bf16 ? 8 : 4;
+  if (inter % V == 0 && ((reinterpret_cast<uintptr_t>(gate_up) | reinterpret_cast<uintptr_t>(act)) & 15) == 0) {
+    const int64_t pieces = n / V;
+    LE_DISPATCH(bf16, silu_mul_split_vec_kernel<T><<<static_cast<unsigned>((pieces + 255) / 256), 256, 0, s>>>(
+                          static_cast<const T*>(gate_up), static_cast<T*>(act), inter, pieces));
+    return hipGetLastError();
+  }
   LE_DISPATCH(bf16, silu_mul_split_kernel<T><<<grid_for(n), 256, 0, s>>>(
                         static_cast<const T*>(gate_up), static_cast<T*>(act), inter, n));
   return hipGetLastError();
