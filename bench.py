@@ -191,6 +191,7 @@ def main():
     ap.add_argument("--workload", choices=["config2", "target", "config3"], default="config2")
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--graph", action="store_true", help="replay the step as one captured HIP graph")
     ap.add_argument("--e2e", choices=["decode64", "config4", "config5", "all", "none"], default="decode64",
                     help="end-to-end leg after the attention measurement (see e2e_leg)")
     ap.add_argument("--e2e-layers", type=int, default=None, help="model layers (default: all)")
@@ -246,26 +247,43 @@ def main():
     slots = plan.dev_array("slots")
     ws = kernels.new_workspace(plan.workspace_size(), dev)
     stream = torch.cuda.current_stream()
+    if args.graph:
+        stream = torch.cuda.Stream()  # capture needs a stream other than the legacy default
+        stream.wait_stream(torch.cuda.current_stream())
 
-    def attn(l):
+    def attn(l, st=None):
         kernels.ragged_paged_attention(qs[l], kc[l], vc[l], plan, case.scale, out=outs[l],
-                                       workspace=ws, stream=stream)
+                                       workspace=ws, stream=st or stream)
 
-    def step():
+    def eager_step():
         plan.upload(stream)
         for l in range(L):
             kernels.store_kv(knew[l], vnew[l], slots, kc[l], vc[l], stream=stream)
             attn(l)
 
-    for _ in range(args.warmup):
-        step()
+    step = eager_step
+    if args.graph:
+        # The whole step (upload + 24 x (scatter, attention)) as one HIP graph,
+        # replayed per step. Nothing in it allocates or clears memory: the
+        # workspace counters reset themselves.
+        with torch.cuda.stream(stream):
+            eager_step()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                eager_step()
+        step = graph.replay
+
+    with torch.cuda.stream(stream):
+        for _ in range(args.warmup):
+            step()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(args.steps):
-        step()
-    e1.record(stream)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for _ in range(args.steps):
+            step()
+        e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / args.steps
 
@@ -277,12 +295,20 @@ def main():
     # Dominant kernel alone: the attention call per layer, back to back, timed
     # with events on the stream it is launched on.
     reps = max(4, args.steps // 2)
+    attn_loop = lambda: [attn(l) for l in range(L)]
+    if args.graph:
+        with torch.cuda.stream(stream):
+            agraph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(agraph, stream=stream):
+                attn_loop()
+        attn_loop = agraph.replay
     a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a0.record(stream)
-    for _ in range(reps):
-        for l in range(L):
-            attn(l)
-    a1.record(stream)
+    with torch.cuda.stream(stream):
+        attn_loop()
+        a0.record(stream)
+        for _ in range(reps):
+            attn_loop()
+        a1.record(stream)
     torch.cuda.synchronize()
     attn_us = a0.elapsed_time(a1) * 1e3 / (reps * L)
     achieved = attn_b / (attn_us * 1e-6) / 1e9

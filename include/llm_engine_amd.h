@@ -8,6 +8,13 @@
  * in through an explicit workspace argument whose size a *_workspace_size call
  * reports. Exceptions never cross this boundary.
  *
+ * Attention workspaces: zero-fill a workspace once, before its first use;
+ * every launch leaves it that way again. Its first 256 KiB hold arrival
+ * counters (one per (row, kv head); at most 65536 of them, else
+ * LE_EUNSUPPORTED) at the same place for every plan, then the split-K
+ * partials, so one workspace of the largest size needed can serve steps of
+ * any shape. Launches that share a workspace must be ordered on one stream.
+ *
  * Return value of every int-returning call:
  *     0            LE_OK
  *     < 0          a LE_E* code: bad shape or argument, nothing was launched
@@ -98,8 +105,9 @@ int le_rope_kv_cache_write(const void* qkv, le_dtype act_dtype, int64_t qkv_row_
  * whose block table starts at block_tables + table_offset[token_seq[t]];
  * kv_head = head / (q_heads / kv_heads). One K/V read serves the whole GQA
  * group. The context of each token is split across workgroups (split-K), the
- * partial results merged by a second kernel, so `workspace` must hold
- * le_attention_decode_workspace_size(n_tokens, q_heads, head_dim) bytes.
+ * partial results merged inside the launch by the last partition to finish,
+ * so `workspace` must hold le_attention_decode_workspace_size(n_tokens,
+ * q_heads, kv_heads, head_dim) bytes.
  * q/out dtype `act_dtype`, caches `kv_dtype`. head_dim 64 or 128;
  * q_heads / kv_heads <= 8; block_size a multiple of 8 (16 in every config).
  * num_cache_blocks bounds the block ids read from the tables.
@@ -137,7 +145,7 @@ typedef struct le_plan_config {
   int32_t q_heads, kv_heads, head_dim, block_size;
   int32_t kv_dtype;            /* le_dtype of the cache the plan will be run against */
   int32_t partition_tokens;    /* split-K partition of decode rows; 0 = default */
-  int32_t chunk_q_tile;        /* query rows per chunk tile (16); 0 = default */
+  int32_t chunk_q_tile;        /* query rows per chunk tile (16 or 32); 0 = default (32) */
   int32_t chunk_partition_tokens; /* key partition of chunk tiles; 0 = default */
 } le_plan_config;
 
@@ -147,15 +155,18 @@ typedef struct le_step_plan {
   int32_t n_seqs;        /* distinct sequences (tables), first-seen order */
   int32_t n_table;       /* entries of the concatenated block tables */
   int32_t n_logits;      /* logit rows */
-  int32_t n_decode_items, n_chunk_items, n_combine_items, n_parts;
+  int32_t n_decode_items, n_chunk_items;
+  int32_t n_combine_items; /* always 0: split rows merge inside their launch (kept for layout) */
+  int32_t n_parts;
   int32_t max_pos;
   int32_t n_slices;      /* entries of cu_seqlens_q minus one, and of seq_lens_k */
   /* byte offsets of each array inside the packed buffer */
   int64_t off_token_ids, off_positions, off_slots, off_token_seq, off_tables,
       off_table_offset, off_cu_seqlens_q, off_seq_lens_k, off_logit_rows, off_decode_items,
       off_chunk_items, off_combine_items;
-  int64_t off_decode_ids;     /* block ids of each decode item, decode_ids_stride apart */
-  int32_t decode_ids_stride;  /* entries per decode item in that array (padded with -1) */
+  int64_t off_decode_ids;     /* block ids of each decode item, then of each chunk item,
+                                 decode_ids_stride apart */
+  int32_t decode_ids_stride;  /* entries per work item in that array (padded with -1) */
   int32_t reserved1_;
   int64_t bytes;         /* total size of the packed buffer */
   const void* dev;       /* device copy, set by le_plan_upload */
@@ -182,8 +193,8 @@ static inline const int32_t* le_plan_dev_array(const le_step_plan* plan, int64_t
  * (row, kv head, context partition), each K/V row read once for the whole
  * GQA group. Prefill-chunk rows run the MFMA kernel with a bf16 cache
  * (causal mask by absolute position against the cached prefix), and the
- * bandwidth kernel row by row with an fp32 cache. Split rows are merged by
- * the combine kernel. The result equals le_attention_decode on the same step.
+ * bandwidth kernel row by row with an fp32 cache. Split rows are merged
+ * inside their launch. The result equals le_attention_decode on the same step.
  * ------------------------------------------------------------------------ */
 size_t le_ragged_workspace_size(const le_step_plan* plan);
 

@@ -35,10 +35,15 @@ int check_attention_shape(int q_heads, int kv_heads, int head_dim, int block_siz
 
 size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
-// Workspace: arrival counters first (so their offset does not depend on the
-// partial count), then the partial accumulators and (max, sum) pairs.
-size_t counter_bytes(int64_t n_rows, int kv_heads) {
-  return align256(static_cast<size_t>(n_rows) * kv_heads * sizeof(int32_t));
+// Workspace: a fixed region of arrival counters first, then the partial
+// accumulators and (max, sum) pairs. The counter region has the same size for
+// every plan, so a workspace reused across steps of different shapes never
+// finds an earlier step's partials where this step's counters are: the
+// counters are zero at every launch because every launch leaves them zero.
+constexpr size_t kCounterRegion = 256 * 1024;  // 65536 (row, kv head) counters
+size_t counter_bytes(int64_t, int) { return kCounterRegion; }
+bool counters_fit(int64_t n_rows, int kv_heads) {
+  return static_cast<size_t>(n_rows) * kv_heads * sizeof(int32_t) <= kCounterRegion;
 }
 
 size_t partial_bytes(int64_t n_parts, int64_t n_rows, int q_heads, int kv_heads, int head_dim) {
@@ -133,6 +138,7 @@ int le_attention_decode(const void* q, le_dtype act_dtype, const void* k_cache,
       !out || !std::isfinite(scale) || num_cache_blocks <= 0)
     return LE_EINVAL;
   const size_t need = le_attention_decode_workspace_size(n_tokens, q_heads, kv_heads, head_dim);
+  if (!counters_fit(n_tokens, kv_heads)) return LE_EUNSUPPORTED;
   if (!workspace || workspace_bytes < need) return LE_ENOSPACE;
 
   le::DecodeParams p{};
@@ -177,6 +183,7 @@ int le_ragged_paged_attention(const void* q, le_dtype act_dtype, const void* k_c
       num_cache_blocks <= 0)
     return LE_EINVAL;
   const size_t need = le_ragged_workspace_size(plan);
+  if (need > 0 && !counters_fit(plan->n_tokens, cfg.kv_heads)) return LE_EUNSUPPORTED;
   if (need > 0 && (!workspace || workspace_bytes < need)) return LE_ENOSPACE;
 
   const char* dev = static_cast<const char*>(plan->dev);
@@ -208,6 +215,9 @@ int le_ragged_paged_attention(const void* q, le_dtype act_dtype, const void* k_c
     c.tables = d.tables; c.table_offset = d.table_offset; c.token_pos = d.token_pos;
     c.out = out; c.parts = parts;
     c.items = reinterpret_cast<const le::ChunkItem*>(dev + plan->off_chunk_items);
+    // chunk items' block ids follow the decode items' at the same stride
+    c.item_ids = d.item_ids + static_cast<int64_t>(plan->n_decode_items) * plan->decode_ids_stride;
+    c.ids_stride = plan->decode_ids_stride;
     c.n_items = plan->n_chunk_items;
     c.q_heads = cfg.q_heads; c.kv_heads = cfg.kv_heads; c.head_dim = cfg.head_dim;
     c.block_size = cfg.block_size; c.scale_log2 = scale_log2;
@@ -216,15 +226,6 @@ int le_ragged_paged_attention(const void* q, le_dtype act_dtype, const void* k_c
     if (e != hipSuccess) return hip_status(e);
   }
 
-  if (plan->n_combine_items > 0) {
-    le::CombineParams m{};
-    m.parts = parts;
-    m.items = reinterpret_cast<const le::CombineItem*>(dev + plan->off_combine_items);
-    m.token_pos = d.token_pos;
-    m.n_rows = plan->n_combine_items; m.nsplit = 1; m.block_size = cfg.block_size;
-    m.q_heads = cfg.q_heads; m.head_dim = cfg.head_dim; m.out = out;
-    e = le::attention_combine(m, act_dtype == LE_BF16, stream);
-  }
   return hip_status(e);
 }
 

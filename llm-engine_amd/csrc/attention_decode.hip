@@ -42,7 +42,12 @@
 namespace le {
 namespace {
 
-constexpr int kWaves = 4;
+#ifndef LE_DECODE_WAVES
+#define LE_DECODE_WAVES 4
+#endif
+constexpr int kWaves = 4;  // valu_kernel
+constexpr int kMfmaWaves = LE_DECODE_WAVES;  // mfma_kernel
+constexpr int kMfmaThreads = kMfmaWaves * 64;
 constexpr int kThreads = kWaves * kWave;
 constexpr int kChunk = 512;   // valu_kernel: scores held in LDS per pass
 constexpr int kTile = 64;     // mfma_kernel: keys per wave tile
@@ -106,14 +111,14 @@ __device__ __forceinline__ float ld_dev(const float* p) {
 // workgroup's unnormalised output for head g of the group, fin_ml[g] its
 // (max, sum). Writes the output (single partition) or the partial, and in the
 // latter case the last arriving workgroup of the row merges all partials.
-template <typename ACT, int HD>
+template <typename ACT, int HD, int NTHR>
 __device__ __forceinline__ void finish(const DecodeParams& p, const Work& w, int G, int kvh,
                                        const float* fin_acc, const float2* fin_ml,
                                        float2* merge_ml, float2* merge_w, int* flag) {
   const int tid = threadIdx.x;
   const int64_t head0 = static_cast<int64_t>(w.token) * p.q_heads + kvh * G;
   if (w.part < 0) {
-    for (int i = tid; i < G * HD; i += kThreads) {
+    for (int i = tid; i < G * HD; i += NTHR) {
       const int g = i / HD;
       elem<ACT>::store1(static_cast<ACT*>(p.out) + head0 * HD + i, fin_acc[i] / fin_ml[g].y);
     }
@@ -121,7 +126,7 @@ __device__ __forceinline__ void finish(const DecodeParams& p, const Work& w, int
   }
   const int64_t rec0 = static_cast<int64_t>(w.part) * p.q_heads + kvh * G;
   float* ml = reinterpret_cast<float*>(p.parts.ml);
-  for (int i = tid; i < G * HD; i += kThreads) st_dev(p.parts.acc + rec0 * HD + i, fin_acc[i]);
+  for (int i = tid; i < G * HD; i += NTHR) st_dev(p.parts.acc + rec0 * HD + i, fin_acc[i]);
   if (tid < G) {
     st_dev(ml + (rec0 + tid) * 2, fin_ml[tid].x);
     st_dev(ml + (rec0 + tid) * 2 + 1, fin_ml[tid].y);
@@ -146,18 +151,18 @@ __device__ __forceinline__ void finish(const DecodeParams& p, const Work& w, int
   // Every (m, l) pair and every accumulator value is requested before any is
   // used: one memory round trip for the whole merge (np <= kMergeBatch per
   // batch of accumulators; more partitions take more batches).
-  for (int i = tid; i < np * G; i += kThreads) {
+  for (int i = tid; i < np * G; i += NTHR) {
     const int j = i / G, g = i - j * G;
     const float* r = ml + (rbase + static_cast<int64_t>(j) * p.q_heads + g) * 2;
     merge_w[i] = make_float2(ld_dev(r), ld_dev(r + 1));  // (m, l) of partition j, head g
   }
-  constexpr int kOutPerThread = (kMaxG * HD + kThreads - 1) / kThreads;
+  constexpr int kOutPerThread = (kMaxG * HD + NTHR - 1) / NTHR;
   float o[kOutPerThread];
   float v0[kOutPerThread][kMergeBatch];
 #pragma unroll
   for (int u = 0; u < kOutPerThread; u++) {
     o[u] = 0.f;
-    const int i = min(tid + u * kThreads, G * HD - 1);
+    const int i = min(tid + u * NTHR, G * HD - 1);
 #pragma unroll
     for (int b = 0; b < kMergeBatch; b++) {
       const int j = min(b, np - 1);
@@ -173,14 +178,14 @@ __device__ __forceinline__ void finish(const DecodeParams& p, const Work& w, int
     merge_ml[tid] = make_float2(M, 1.f / L);
   }
   __syncthreads();
-  for (int i = tid; i < np * G; i += kThreads) {  // weights exp2(m_j - M) / L
+  for (int i = tid; i < np * G; i += NTHR) {  // weights exp2(m_j - M) / L
     const int g = i % G;
     merge_w[i].x = exp2f(merge_w[i].x - merge_ml[g].x) * merge_ml[g].y;
   }
   __syncthreads();
 #pragma unroll
   for (int u = 0; u < kOutPerThread; u++) {
-    const int i = tid + u * kThreads;
+    const int i = tid + u * NTHR;
     if (i >= G * HD) continue;
     const int g = i / HD;
 #pragma unroll
@@ -208,8 +213,8 @@ template <int HD> struct MfmaLds {
   static constexpr int V_STRIDE = HD * 2 + 16;           // bytes per key row of the V tile
   static constexpr int VT_BYTES = kTile * V_STRIDE;      // per wave
   static constexpr int RED_STRIDE = HD + 4;              // floats per head in the merge area
-  static constexpr int RED_BYTES = kWaves * kMaxG * RED_STRIDE * 4;
-  static constexpr int BYTES = (kWaves * VT_BYTES > RED_BYTES ? kWaves * VT_BYTES : RED_BYTES);
+  static constexpr int RED_BYTES = kMfmaWaves * kMaxG * RED_STRIDE * 4;
+  static constexpr int BYTES = (kMfmaWaves * VT_BYTES > RED_BYTES ? kMfmaWaves * VT_BYTES : RED_BYTES);
 };
 
 constexpr int kTabCap = 1024;  // block ids of a partition staged in LDS
@@ -371,7 +376,7 @@ __device__ __forceinline__ void compute_tile(WaveAcc<HD>& st, const TileRegs<HD 
 }
 
 template <typename ACT, int HD>
-__global__ __launch_bounds__(kThreads) void mfma_kernel(DecodeParams p) {
+__global__ __launch_bounds__(kMfmaThreads) void mfma_kernel(DecodeParams p) {
   using L = MfmaLds<HD>;
   constexpr int KS = HD / 32;  // MFMA k-steps over head dims
   constexpr int DT = HD / 16;  // 16-dim output tiles
@@ -389,13 +394,13 @@ __global__ __launch_bounds__(kThreads) void mfma_kernel(DecodeParams p) {
   // With a plan, the item's block ids sit at a fixed stride: fetch them now,
   // in the same memory round trip as the item itself.
   const bool item_ids = p.items != nullptr && p.item_ids != nullptr && p.ids_stride <= kTabCap;
-  constexpr int kIdsPerThread = kTabCap / kThreads;
+  constexpr int kIdsPerThread = kTabCap / kMfmaThreads;
   int pre_ids[kIdsPerThread];
   if (item_ids) {
     const int32_t* ids = p.item_ids + static_cast<int64_t>(blockIdx.x) * p.ids_stride;
 #pragma unroll
     for (int u = 0; u < kIdsPerThread; u++) {
-      const int i = threadIdx.x + u * kThreads;
+      const int i = threadIdx.x + u * kMfmaThreads;
       pre_ids[u] = i < p.ids_stride ? ids[i] : -1;
     }
   }
@@ -451,7 +456,7 @@ __global__ __launch_bounds__(kThreads) void mfma_kernel(DecodeParams p) {
 #endif
 
   const int bs_shift = __builtin_ctz(bs);  // block sizes are powers of two
-  const int stride = kWaves * kTile;
+  const int stride = kMfmaWaves * kTile;
   // The partition in segments of at most kTabCap blocks: each segment's block
   // ids are staged in LDS (invalid ids as -1), then streamed tile by tile.
   for (int sb0 = w.b_begin; sb0 < w.b_end; sb0 += kTabCap) {
@@ -461,10 +466,10 @@ __global__ __launch_bounds__(kThreads) void mfma_kernel(DecodeParams p) {
 #pragma unroll
       for (int u = 0; u < kIdsPerThread; u++) {
         const int bid = pre_ids[u];
-        tab[tid + u * kThreads] = (bid >= 0 && bid < p.num_cache_blocks) ? bid : -1;
+        tab[tid + u * kMfmaThreads] = (bid >= 0 && bid < p.num_cache_blocks) ? bid : -1;
       }
     } else {
-      for (int i = tid; i < sb1 - sb0; i += kThreads) {
+      for (int i = tid; i < sb1 - sb0; i += kMfmaThreads) {
         const int bid = gtab[sb0 + i];
         tab[i] = (bid >= 0 && bid < p.num_cache_blocks) ? bid : -1;
       }
@@ -519,22 +524,22 @@ __global__ __launch_bounds__(kThreads) void mfma_kernel(DecodeParams p) {
   if (tid < G) {
     float M = -FLT_MAX;
 #pragma unroll
-    for (int v = 0; v < kWaves; v++) M = fmaxf(M, red[(v * kMaxG + tid) * L::RED_STRIDE + HD]);
+    for (int v = 0; v < kMfmaWaves; v++) M = fmaxf(M, red[(v * kMaxG + tid) * L::RED_STRIDE + HD]);
     float Ls = 0.f;
 #pragma unroll
-    for (int v = 0; v < kWaves; v++) {
+    for (int v = 0; v < kMfmaWaves; v++) {
       const float* r = red + (v * kMaxG + tid) * L::RED_STRIDE;
       Ls += r[HD + 1] * exp2f(r[HD] - M);
     }
     fin_ml[tid] = make_float2(M, Ls);
   }
   __syncthreads();
-  for (int i = tid; i < G * HD; i += kThreads) {
+  for (int i = tid; i < G * HD; i += kMfmaThreads) {
     const int g = i / HD, d = i - g * HD;
     const float M = fin_ml[g].x;
     float o = 0.f;
 #pragma unroll
-    for (int v = 0; v < kWaves; v++) {
+    for (int v = 0; v < kMfmaWaves; v++) {
       const float* r = red + (v * kMaxG + g) * L::RED_STRIDE;
       o += r[d] * exp2f(r[HD] - M);
     }
@@ -542,7 +547,7 @@ __global__ __launch_bounds__(kThreads) void mfma_kernel(DecodeParams p) {
   }
   __syncthreads();
   PROBE_TS(3);
-  finish<ACT, HD>(p, w, G, kvh, fin_acc, fin_ml, merge_ml, merge_w, &flag);
+  finish<ACT, HD, kMfmaThreads>(p, w, G, kvh, fin_acc, fin_ml, merge_ml, merge_w, &flag);
   PROBE_TS(7);
 }
 
@@ -743,34 +748,7 @@ __global__ __launch_bounds__(kThreads) void valu_kernel(DecodeParams p) {
     fin_acc[i] = v;
   }
   __syncthreads();
-  finish<ACT, HD>(p, w, G, kvh, fin_acc, fin_ml, merge_ml, merge_w, &flag);
-}
-
-// Merge of split partitions for chunk rows: one wave per (row, q head).
-template <typename ACT, int HD>
-__global__ __launch_bounds__(kWave) void combine_kernel(CombineParams p) {
-  const CombineItem it = p.items[blockIdx.x];
-  const int h = blockIdx.y;
-  const int lane = threadIdx.x;
-  constexpr int DPL = HD / kWave;
-  float mx = -FLT_MAX;
-  for (int i = 0; i < it.n_parts; i++)
-    mx = fmaxf(mx, p.parts.ml[static_cast<int64_t>(it.part_begin + i) * p.q_heads + h].x);
-  float l = 0.f, o[DPL];
-#pragma unroll
-  for (int j = 0; j < DPL; j++) o[j] = 0.f;
-  for (int i = 0; i < it.n_parts; i++) {
-    const int64_t rec = static_cast<int64_t>(it.part_begin + i) * p.q_heads + h;
-    const float2 ml = p.parts.ml[rec];
-    const float wgt = exp2f(ml.x - mx);
-    l += ml.y * wgt;
-#pragma unroll
-    for (int j = 0; j < DPL; j++) o[j] += p.parts.acc[rec * HD + j * kWave + lane] * wgt;
-  }
-  const float inv = 1.f / l;
-  ACT* out = static_cast<ACT*>(p.out) + (static_cast<int64_t>(it.token) * p.q_heads + h) * HD;
-#pragma unroll
-  for (int j = 0; j < DPL; j++) elem<ACT>::store1(out + j * kWave + lane, o[j] * inv);
+  finish<ACT, HD, kThreads>(p, w, G, kvh, fin_acc, fin_ml, merge_ml, merge_w, &flag);
 }
 
 template <typename ACT, int HD, int G>
@@ -799,12 +777,13 @@ template <typename ACT>
 hipError_t dispatch(const DecodeParams& p, int kv_bf16, hipStream_t s) {
   const dim3 grid(p.n_rows, p.kv_heads, p.items ? 1 : p.nsplit);
   if (kv_bf16) {
-    if (p.head_dim == 64) mfma_kernel<ACT, 64><<<grid, kThreads, 0, s>>>(p);
-    else mfma_kernel<ACT, 128><<<grid, kThreads, 0, s>>>(p);
+    if (p.head_dim == 64) mfma_kernel<ACT, 64><<<grid, kMfmaThreads, 0, s>>>(p);
+    else mfma_kernel<ACT, 128><<<grid, kMfmaThreads, 0, s>>>(p);
     return hipGetLastError();
   }
   return p.head_dim == 64 ? dispatch_valu<ACT, 64>(p, s) : dispatch_valu<ACT, 128>(p, s);
 }
+
 
 }  // namespace
 
@@ -830,17 +809,5 @@ hipError_t attention_decode(const DecodeParams& p, int act_bf16, int kv_bf16, hi
   return act_bf16 ? dispatch<bf16_t>(p, kv_bf16, s) : dispatch<float>(p, kv_bf16, s);
 }
 
-hipError_t attention_combine(const CombineParams& p, int act_bf16, hipStream_t s) {
-  if (p.n_rows <= 0) return hipSuccess;
-  const dim3 grid(p.n_rows, p.q_heads);
-  if (p.head_dim == 64) {
-    if (act_bf16) combine_kernel<bf16_t, 64><<<grid, kWave, 0, s>>>(p);
-    else combine_kernel<float, 64><<<grid, kWave, 0, s>>>(p);
-  } else {
-    if (act_bf16) combine_kernel<bf16_t, 128><<<grid, kWave, 0, s>>>(p);
-    else combine_kernel<float, 128><<<grid, kWave, 0, s>>>(p);
-  }
-  return hipGetLastError();
-}
 
 }  // namespace le

@@ -135,4 +135,31 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
+// Device-coherent 16-byte accesses for data exchanged between workgroups
+// (possibly on different XCDs, whose L2s are not coherent with each other):
+// raw buffer loads/stores with the sc1 cache-policy bit, the same policy the
+// compiler gives agent-scope relaxed atomics, so a reader never hits a stale
+// line left in its own L2. The compiler tracks these loads like any other.
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7FFFFFFF, 0x00020000);
+}
+constexpr int kCachePolicySc1 = 16;
+typedef uint32_t u32x4raw __attribute__((vector_size(16)));  // the builtins' data type
+__device__ __forceinline__ f32x4v ld_coherent16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  const u32x4raw v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCachePolicySc1);
+  return __builtin_bit_cast(f32x4v, v);
+}
+__device__ __forceinline__ void st_coherent16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, f32x4v v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4raw, v), r, byte_off, 0, kCachePolicySc1);
+}
+typedef uint32_t u32x2raw __attribute__((vector_size(8)));
+__device__ __forceinline__ void st_coherent8(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, uint2 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2raw, v), r, byte_off, 0, kCachePolicySc1);
+}
+__device__ __forceinline__ uint4 ld_coherent16u(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  const u32x4raw v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCachePolicySc1);
+  return __builtin_bit_cast(uint4, v);
+}
+
 }  // namespace le

@@ -28,16 +28,14 @@ struct DecodeItem {
 };
 
 // Chunk work item: query rows [tok_begin, tok_begin + n_q) (consecutive
-// positions of one sequence) over key blocks [blk_begin, blk_end). Row
+// positions of one sequence, at most 32) over key blocks [blk_begin, blk_end)
+// of its table, partition `part` of the tile's part_stride partitions. Row
 // tok_begin + i writes partial part0 + i * part_stride, or, when part0 < 0,
-// its normalised output directly.
+// its normalised output directly; the last partition of the tile to arrive
+// (per kv head) merges partials [part0 - part + i * part_stride, ... +
+// part_stride) of each row.
 struct ChunkItem {
-  int32_t tok_begin, n_q, blk_begin, blk_end, part0, part_stride, seq, pad_;
-};
-
-// Rows whose context was split: partials [part_begin, part_begin + n_parts).
-struct CombineItem {
-  int32_t token, part_begin, n_parts, pad_;
+  int32_t tok_begin, n_q, blk_begin, blk_end, part0, part_stride, seq, part;
 };
 
 hipError_t kv_cache_write(const void* k, const void* v, int src_bf16, const int32_t* slots,
@@ -71,17 +69,6 @@ struct DecodeParams {
 
 hipError_t attention_decode(const DecodeParams& p, int act_bf16, int kv_bf16, hipStream_t stream);
 
-struct CombineParams {
-  PartialLayout parts;
-  const CombineItem* items;  // null: token = blockIdx.x with `nsplit` splits derived from pos
-  const int32_t* token_pos;
-  int n_rows, nsplit, block_size;
-  int q_heads, head_dim;
-  void* out;
-};
-
-hipError_t attention_combine(const CombineParams& p, int act_bf16, hipStream_t stream);
-
 struct ChunkParams {
   const void* q;
   const void* k_cache;
@@ -92,6 +79,8 @@ struct ChunkParams {
   void* out;
   PartialLayout parts;
   const ChunkItem* items;
+  const int32_t* item_ids;  // block ids of item i at item_ids[i * ids_stride + j]
+  int ids_stride;
   int n_items;
   int q_heads, kv_heads, head_dim, block_size;
   float scale_log2;

@@ -17,8 +17,8 @@
 // consecutive positions; each tile's keys 0..last position are cut into
 // partitions of ~chunk_partition_tokens, one ChunkItem each, run on MFMA.
 // With an fp32 cache, chunk rows are decode rows (exact fp32 arithmetic on the
-// vector ALUs). A chunk row with more than one partition gets a CombineItem;
-// a split decode row is merged inside the decode launch.
+// vector ALUs). Split rows of either kind are merged inside their launch by
+// the last partition to finish.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -36,8 +36,10 @@ constexpr int kMaxAutoPartition = 4096;      // decode rows: largest automatic p
 constexpr int kPartitionQuantum = 256;       // 4 waves x 64-key tiles
 constexpr int64_t kTargetItems = 256;        // workgroups per step the sizing aims for
 constexpr int kMaxMergeEntries = 1024;       // partitions x group the decode merge can stage
-constexpr int kDefaultChunkTile = 16;        // MFMA row tile
-constexpr int kDefaultChunkPartition = 256;  // chunk tiles
+constexpr int kDefaultChunkTile = 32;        // query rows per chunk item (two MFMA row tiles)
+constexpr int kDefaultChunkPartition = 256;  // keys per chunk item: one LDS stage
+constexpr int kMaxChunkParts = 16;           // partitions of a chunk tile the in-kernel merge stages
+constexpr int kMaxChunkItemBlocks = 1024;    // block ids of one chunk item the kernel stages
 
 int64_t align256(int64_t x) { return (x + 255) & ~static_cast<int64_t>(255); }
 
@@ -77,7 +79,7 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
   }
   if (cfg.chunk_q_tile <= 0) cfg.chunk_q_tile = kDefaultChunkTile;
   if (cfg.chunk_partition_tokens <= 0) cfg.chunk_partition_tokens = kDefaultChunkPartition;
-  if (cfg.chunk_q_tile != 16) return LE_EUNSUPPORTED;  // the MFMA tile height
+  if (cfg.chunk_q_tile != 16 && cfg.chunk_q_tile != 32) return LE_EUNSUPPORTED;  // MFMA row tiles
   const int dec_pb = round_to_blocks(cfg.partition_tokens, bs);
   const int chk_pb = round_to_blocks(cfg.chunk_partition_tokens, bs);
   const bool mfma_chunks = cfg.kv_dtype == LE_BF16;
@@ -123,7 +125,6 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
   // ---- work lists ----
   std::vector<le::DecodeItem> dec;
   std::vector<le::ChunkItem> chk;
-  std::vector<le::CombineItem> cmb;
   int32_t parts = 0;
   {
     int32_t t = 0;
@@ -134,7 +135,10 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
           const int nq = std::min(cfg.chunk_q_tile, s.len - q0);
           const int last = s.start + q0 + nq - 1;
           const int nb = last / bs + 1;
-          const int J = (nb + chk_pb - 1) / chk_pb;
+          // Long contexts get longer partitions rather than more of them.
+          const int pb = std::max(chk_pb, (nb + kMaxChunkParts - 1) / kMaxChunkParts);
+          if (pb > kMaxChunkItemBlocks) return LE_EUNSUPPORTED;  // the kernel stages an item's ids in LDS
+          const int J = (nb + pb - 1) / pb;
           const int base = J > 1 ? parts : -1;
           for (int j = 0; j < J; j++) {
             le::ChunkItem c{};
@@ -145,12 +149,10 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
             c.part0 = J > 1 ? base + j : -1;
             c.part_stride = J;
             c.seq = slice_seq[i];
+            c.part = j;
             chk.push_back(c);
           }
-          if (J > 1) {
-            for (int r = 0; r < nq; r++) cmb.push_back({t + q0 + r, base + r * J, J, 0});
-            parts += nq * J;
-          }
+          if (J > 1) parts += nq * J;
         }
       } else {
         for (int r = 0; r < s.len; r++) {
@@ -188,7 +190,7 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
   P.n_logits = n_logits;
   P.n_decode_items = static_cast<int32_t>(dec.size());
   P.n_chunk_items = static_cast<int32_t>(chk.size());
-  P.n_combine_items = static_cast<int32_t>(cmb.size());
+  P.n_combine_items = 0;  // chunk rows merge inside their launch
   P.n_parts = parts;
   P.max_pos = max_pos;
   P.n_slices = n_slices;
@@ -209,14 +211,16 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
   P.off_logit_rows = take(static_cast<int64_t>(n_logits) * 4);
   P.off_decode_items = take(static_cast<int64_t>(dec.size()) * sizeof(le::DecodeItem));
   P.off_chunk_items = take(static_cast<int64_t>(chk.size()) * sizeof(le::ChunkItem));
-  P.off_combine_items = take(static_cast<int64_t>(cmb.size()) * sizeof(le::CombineItem));
-  // Each decode item's block ids at a fixed stride, so a workgroup can fetch
-  // them in the same memory round trip as its item.
+  P.off_combine_items = take(0);
+  // Each work item's block ids at a fixed stride (decode items, then chunk
+  // items), so a workgroup can fetch them in the same memory round trip as
+  // its item.
   int32_t ids_stride = 0;
   for (const auto& d : dec) ids_stride = std::max(ids_stride, d.blk_end - d.blk_begin);
+  for (const auto& c : chk) ids_stride = std::max(ids_stride, c.blk_end - c.blk_begin);
   ids_stride = (ids_stride + 3) / 4 * 4;
   P.decode_ids_stride = ids_stride;
-  P.off_decode_ids = take(static_cast<int64_t>(dec.size()) * ids_stride * 4);
+  P.off_decode_ids = take(static_cast<int64_t>(dec.size() + chk.size()) * ids_stride * 4);
   P.bytes = off;
   P.dev = nullptr;
   if (!host_buf || host_cap < P.bytes) {
@@ -272,10 +276,17 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
         row[j] = j < d.blk_end - d.blk_begin ? tables[d.table_off + d.blk_begin + j] : -1;
     }
   }
-  if (!chk.empty())
+  if (!chk.empty()) {
     std::memcpy(base + P.off_chunk_items, chk.data(), chk.size() * sizeof(le::ChunkItem));
-  if (!cmb.empty())
-    std::memcpy(base + P.off_combine_items, cmb.data(), cmb.size() * sizeof(le::CombineItem));
+    int32_t* ids = arr(P.off_decode_ids) + dec.size() * static_cast<size_t>(ids_stride);
+    for (size_t k = 0; k < chk.size(); k++) {
+      const le::ChunkItem& c = chk[k];
+      const int32_t toff = table_offset[c.seq];
+      int32_t* row = ids + k * static_cast<size_t>(ids_stride);
+      for (int j = 0; j < ids_stride; j++)
+        row[j] = j < c.blk_end - c.blk_begin ? tables[toff + c.blk_begin + j] : -1;
+    }
+  }
   *plan = P;
   return LE_OK;
 }

@@ -64,14 +64,13 @@ def _plan(slices, kv=torch.bfloat16, **kw):
 def _items(plan, kind):
     P = plan.plan
     n, w, off = {"decode": (P.n_decode_items, 8, P.off_decode_items),
-                 "chunk": (P.n_chunk_items, 8, P.off_chunk_items),
-                 "combine": (P.n_combine_items, 4, P.off_combine_items)}[kind]
+                 "chunk": (P.n_chunk_items, 8, P.off_chunk_items)}[kind]
     return plan.host.numpy()[off:off + 4 * n * w].view(np.int32).reshape(n, w)
 
 
 def check_work_lists(plan, slices, bs=16):
     P = plan.plan
-    dec, chk, cmb = _items(plan, "decode"), _items(plan, "chunk"), _items(plan, "combine")
+    dec, chk = _items(plan, "decode"), _items(plan, "chunk")
     pos = plan.host_array("positions")
     toff = plan.host_array("table_offset")
     tseq = plan.host_array("token_seq")
@@ -92,17 +91,38 @@ def check_work_lists(plan, slices, bs=16):
             assert items[0][2] == -1
         else:
             assert sorted(i[2] for i in items) == list(range(items[0][3], items[0][3] + npart))
-    # chunk items: each tile's partitions tile the keys up to its last row
+    # chunk items: each tile's partitions tile the keys up to its last row,
+    # numbered 0..J-1 in key order, with part0 = base + j
     tiles = {}
     for it in chk:
-        tb, nq, b0, b1, p0, stride, seq, _ = (int(x) for x in it)
-        tiles.setdefault(tb, []).append((b0, b1, p0, stride, nq))
+        tb, nq, b0, b1, p0, stride, seq, part = (int(x) for x in it)
+        assert 1 <= nq <= 32 and all(pos[tb + r] == pos[tb] + r for r in range(nq))
+        tiles.setdefault(tb, []).append((b0, b1, p0, stride, nq, part))
     for tb, items in tiles.items():
         items.sort()
-        nq = items[0][4]
+        nq, J = items[0][4], items[0][3]
         assert items[0][0] == 0 and items[-1][1] == pos[tb + nq - 1] // bs + 1
         for a, b in zip(items, items[1:]):
             assert a[1] == b[0]
+        assert [i[5] for i in items] == list(range(len(items)))
+        if len(items) == 1:
+            assert items[0][2] == -1
+        else:
+            assert J == len(items) and len({i[2] - i[5] for i in items}) == 1
+    # every work item's block ids, at the shared stride: decode items, then chunk items
+    stride = P.decode_ids_stride
+    ids = plan.host.numpy()[P.off_decode_ids:P.off_decode_ids + 4 * (len(dec) + len(chk)) * stride]
+    ids = ids.view(np.int32).reshape(len(dec) + len(chk), stride)
+    tables = plan.host_array("tables")
+    for k, it in enumerate(dec):
+        b0, b1, to = int(it[3]), int(it[4]), int(it[2])
+        assert list(ids[k, :b1 - b0]) == list(tables[to + b0:to + b1]) and (ids[k, b1 - b0:] == -1).all()
+    for k, it in enumerate(chk):
+        b0, b1, seq = int(it[2]), int(it[3]), int(it[6])
+        to = int(toff[seq])
+        row = ids[len(dec) + k]
+        assert list(row[:b1 - b0]) == list(tables[to + b0:to + b1]) and (row[b1 - b0:] == -1).all()
+    assert P.n_combine_items == 0
     # every partial index is owned exactly once
     owned = []
     for it in dec:
@@ -112,8 +132,6 @@ def check_work_lists(plan, slices, bs=16):
         if it[4] >= 0:
             owned += [int(it[4]) + r * int(it[5]) for r in range(int(it[1]))]
     assert sorted(owned) == list(range(P.n_parts))
-    for it in cmb:
-        assert int(it[2]) > 1
 
 
 TRACES = np.load(ROOT / "tests" / "golden" / "schedule_ref.npz")

@@ -152,3 +152,33 @@ def test_mixed_step_config3(gpu, act):
     err = max_abs(got, want)
     print(f"config3 act={act}: max|err|={err:.3e}")
     assert err < tol_for(True, act)
+
+
+def test_workspace_reused_across_plans(gpu):
+    """One workspace serves steps of different shapes (as the engine uses it):
+    a step with few rows and many split partials, then a larger mixed step
+    whose split chunk tiles need the arrival counters. The counters must not
+    land on the first step's partials."""
+    from llm_engine_amd import kernels
+    a = make_case([4096, 3000, 2500], num_blocks=2048, seed=31, kv_bf16=True)
+    b = make_case([600, 700, 650] + [300] * 40, q_len=[100, 90, 70] + [1] * 40, num_blocks=4096,
+                  seed=32, kv_bf16=True)
+    plans, need = [], 0
+    for case, part in ((a, 256), (b, 0)):
+        q, qh = device_q(case, torch.float32, gpu)
+        kc, vc = to_dev_cache(case.k_cache, gpu), to_dev_cache(case.v_cache, gpu)
+        plan = kernels.Plan(slices_of(case), case.q_heads, case.kv_heads, case.head_dim,
+                            case.block_size, kc.dtype, partition_tokens=part).upload()
+        plans.append((case, q, qh, kc, vc, plan))
+        need = max(need, plan.workspace_size())
+    ws = kernels.new_workspace(need, gpu)
+    for rep in range(2):
+        for case, q, qh, kc, vc, plan in plans:
+            assert plan.plan.n_parts > 0
+            out = kernels.ragged_paged_attention(q, kc, vc, plan, case.scale, workspace=ws)
+            torch.cuda.synchronize()
+            err = max_abs(out.float().cpu().numpy(), oracle_out(case, qh))
+            print(f"rep {rep} rows {plan.plan.n_tokens} parts {plan.plan.n_parts} "
+                  f"chunk items {plan.plan.n_chunk_items}: max|err| {err:.3e}")
+            assert err < TOL_BF16
+    assert int(ws[:256 * 1024].count_nonzero().item()) == 0  # counters left at zero
