@@ -182,3 +182,49 @@ def test_workspace_reused_across_plans(gpu):
                   f"chunk items {plan.plan.n_chunk_items}: max|err| {err:.3e}")
             assert err < TOL_BF16
     assert int(ws[:256 * 1024].count_nonzero().item()) == 0  # counters left at zero
+
+
+@pytest.mark.parametrize("q_heads,kv_heads,head_dim", [(32, 4, 64), (8, 8, 64), (16, 2, 128), (4, 1, 128)])
+def test_chunk_rows_other_shapes(gpu, q_heads, kv_heads, head_dim):
+    """The MFMA chunk kernel beyond the Qwen shape: GQA group 8 and 1,
+    head_dim 128, with partial row tiles, split tiles (merged in-kernel) and a
+    cached prefix; bf16 K/V against the oracle."""
+    ctx = [700, 333, 90, 1]
+    q_len = [45, 333, 17, 1]  # chunk at offset 655, a whole-prompt chunk, a short tail, a decode row
+    case = make_case(ctx, q_len=q_len, q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim,
+                     num_blocks=512, seed=41, kv_bf16=True)
+    got, qh, plan = run_ragged(case, torch.float32, gpu)
+    want = oracle_out(case, qh)
+    err = max_abs(got, want)
+    print(f"chunk {q_heads}/{kv_heads}x{head_dim}: items {plan.plan.n_chunk_items} parts {plan.plan.n_parts} "
+          f"max|err| {err:.3e}")
+    assert plan.plan.n_chunk_items > 0 and plan.plan.n_parts > 0
+    assert err < TOL_BF16
+
+
+@pytest.mark.parametrize("block_size", [8, 32, 64])
+def test_chunk_rows_block_sizes(gpu, block_size):
+    ctx = [600, 129, 64]
+    q_len = [100, 129, 3]
+    case = make_case(ctx, q_len=q_len, block_size=block_size, num_blocks=256, seed=43, kv_bf16=True)
+    got, qh, plan = run_ragged(case, torch.bfloat16, gpu)
+    want = oracle_out(case, qh)
+    err = max_abs(got, want)
+    print(f"chunk block {block_size}: items {plan.plan.n_chunk_items} max|err| {err:.3e}")
+    assert plan.plan.n_chunk_items > 0
+    assert err < TOL_BF16_OUT
+
+
+def test_chunk_tile16_and_long_context(gpu):
+    """16-row chunk tiles (plan option), and a chunk over a 9000-token prefix:
+    longer partitions (several LDS stages per item) keep a tile's split count
+    within what the in-kernel merge stages."""
+    ctx = [9000 + 40, 300]
+    q_len = [40, 300]
+    case = make_case(ctx, q_len=q_len, num_blocks=1024, seed=47, kv_bf16=True)
+    for tile in (16, 32):
+        got, qh, plan = run_ragged(case, torch.float32, gpu, chunk_q_tile=tile)
+        want = oracle_out(case, qh)
+        err = max_abs(got, want)
+        print(f"tile {tile}: items {plan.plan.n_chunk_items} parts {plan.plan.n_parts} max|err| {err:.3e}")
+        assert err < TOL_BF16
