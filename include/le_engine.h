@@ -105,6 +105,15 @@ void le_model_destroy(le_model* m);
 int le_model_forward(le_model* m, const le_step_slice* slices, int n_slices, int32_t* tokens_out,
                      float* logits_out);
 
+/* ---- greedy selection on the device (reference: Sampler::argmax,
+ *      sampler.cpp:9-13, run on the host over copied-back logits) ----
+ * out[r] = index of the first maximum of logits[r][0..vocab) (fp32, rows
+ * contiguous), exactly as the reference's loop picks it: start at element 0,
+ * move only to a strictly greater value. So ties go to the lowest index, a
+ * NaN is never chosen past element 0, and a row whose element 0 is NaN (or
+ * with no greater value) gives 0. One launch for all rows. */
+int le_argmax_rows(const float* logits, int rows, int vocab, int32_t* out, hipStream_t stream);
+
 /* ---- serving loop (reference: greedy_run, test_cuda_invariance.cpp:90-143,
  *      and Engine::run_loop, engine.cpp:246) ---- */
 typedef struct le_run_stats {

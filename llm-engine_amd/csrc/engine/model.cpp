@@ -357,6 +357,14 @@ le_model* le_model_create(const le_model_desc* desc, int num_blocks, int block_s
 
 void le_model_destroy(le_model* m) { delete m; }
 
+int le_argmax_rows(const float* logits, int rows, int vocab, int32_t* out, hipStream_t stream) {
+  if (rows < 0 || vocab <= 0) return LE_EINVAL;
+  if (rows == 0) return LE_OK;
+  if (!logits || !out) return LE_EINVAL;
+  const hipError_t e = le::engine::argmax_rows(logits, rows, vocab, out, stream);
+  return e == hipSuccess ? LE_OK : static_cast<int>(e);
+}
+
 int le_model_forward(le_model* m, const le_step_slice* slices, int n_slices, int32_t* tokens_out,
                      float* logits_out) {
   if (!m || (n_slices > 0 && !slices)) return LE_EINVAL;

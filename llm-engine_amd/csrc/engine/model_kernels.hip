@@ -194,34 +194,57 @@ __global__ void silu_mul_split_kernel(const T* __restrict__ gu, T* __restrict__ 
 }
 
 // Greedy token per logits row: the first maximum wins (sampler.cpp:9-13).
-// One workgroup per row; each thread keeps its own (max, lowest index), then a
-// tree merge that prefers the lower index on ties. NaN never wins (as with the
-// reference's strict `>`, a NaN is never greater).
-__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ logits, int vocab,
-                                                     int32_t* __restrict__ out) {
+// One 1024-thread workgroup per row; each thread scans its 16-byte pieces in
+// index order keeping (max, lowest index), then the waves and the workgroup
+// merge with a rule that prefers the lower index on ties. NaN never wins (as
+// with the reference's strict `>`, a NaN is never greater), and a NaN in
+// element 0 is never replaced.
+constexpr int kArgmaxThreads = 1024;
+
+__device__ __forceinline__ void argmax_take(float& bv, int& bi, float v, int i, int none) {
+  if (i < none && (bi == none || v > bv || (v == bv && i < bi))) { bv = v; bi = i; }
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __restrict__ logits, int vocab,
+                                                                int32_t* __restrict__ out) {
   const float* row = logits + static_cast<int64_t>(blockIdx.x) * vocab;
   float best = -INFINITY;
   int idx = vocab;  // "none yet"
-  for (int j = threadIdx.x; j < vocab; j += 256) {
-    const float v = row[j];
+  auto scan = [&](float v, int j) {
     if (v > best || (idx == vocab && v == v)) { best = v; idx = j; }
-  }
-  __shared__ float sv[256];
-  __shared__ int si[256];
-  sv[threadIdx.x] = best;
-  si[threadIdx.x] = idx;
-  __syncthreads();
-  for (int s = 128; s > 0; s >>= 1) {
-    if (threadIdx.x < s) {
-      const float ov = sv[threadIdx.x + s];
-      const int oi = si[threadIdx.x + s];
-      const bool take = oi < vocab && (si[threadIdx.x] == vocab || ov > sv[threadIdx.x] ||
-                                       (ov == sv[threadIdx.x] && oi < si[threadIdx.x]));
-      if (take) { sv[threadIdx.x] = ov; si[threadIdx.x] = oi; }
+  };
+  if (vocab % 4 == 0) {
+    const float4* r4 = reinterpret_cast<const float4*>(row);
+    for (int j4 = threadIdx.x; j4 < vocab / 4; j4 += kArgmaxThreads) {
+      const float4 v = r4[j4];
+      scan(v.x, 4 * j4); scan(v.y, 4 * j4 + 1); scan(v.z, 4 * j4 + 2); scan(v.w, 4 * j4 + 3);
     }
-    __syncthreads();
+  } else {
+    for (int j = threadIdx.x; j < vocab; j += kArgmaxThreads) scan(row[j], j);
   }
-  if (threadIdx.x == 0) out[blockIdx.x] = si[0] == vocab ? 0 : si[0];
+  // a thread's candidate has the lowest index among its equal maxima; merge
+  // across lanes, then across the waves
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(best, off, kWave);
+    const int oi = __shfl_xor(idx, off, kWave);
+    argmax_take(best, idx, ov, oi, vocab);
+  }
+  __shared__ float sv[kArgmaxThreads / kWave];
+  __shared__ int si[kArgmaxThreads / kWave];
+  const int wave = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    sv[wave] = best;
+    si[wave] = idx;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float bv = sv[0];
+    int bi = si[0];
+    for (int w = 1; w < kArgmaxThreads / kWave; w++) argmax_take(bv, bi, sv[w], si[w], vocab);
+    // the reference starts from element 0 and replaces it only by a greater
+    // value, so a NaN there is never replaced
+    out[blockIdx.x] = (bi == vocab || row[0] != row[0]) ? 0 : bi;
+  }
 }
 
 int grid_for(int64_t n) {
@@ -277,7 +300,7 @@ hipError_t silu_mul_split(const void* gate_up, void* act, int rows, int inter, b
 
 hipError_t argmax_rows(const float* logits, int rows, int vocab, int32_t* out, hipStream_t s) {
   if (rows <= 0) return hipSuccess;
-  argmax_kernel<<<rows, 256, 0, s>>>(logits, vocab, out);
+  argmax_kernel<<<rows, kArgmaxThreads, 0, s>>>(logits, vocab, out);
   return hipGetLastError();
 }
 

@@ -94,6 +94,16 @@ def rope_store_kv(qkv: torch.Tensor, positions: torch.Tensor, slots: torch.Tenso
     return q_out
 
 
+def argmax_rows(logits: torch.Tensor, stream=None) -> torch.Tensor:
+    """First-maximum index of each row of fp32 logits [rows, vocab] (sampler.cpp:9-13)."""
+    _req(logits.dtype == torch.float32 and logits.dim() == 2 and logits.is_contiguous() and logits.is_cuda,
+         "logits: contiguous fp32 cuda [rows, vocab]")
+    out = torch.empty(logits.shape[0], dtype=torch.int32, device=logits.device)
+    check("le_argmax_rows", _lib.load().le_argmax_rows(_p(logits), logits.shape[0], logits.shape[1], _p(out),
+                                                       _stream(stream)))
+    return out
+
+
 def new_workspace(nbytes: int, device="cuda") -> torch.Tensor:
     """A workspace for the attention calls: zero-filled once, as the ABI requires
     (the kernels leave its arrival counters at zero after every launch)."""
