@@ -7,8 +7,10 @@
 A step is one decode pass of the hot path over one ragged batch, for every
 layer of the model: the packed step metadata is uploaded once (one async
 copy), then per layer the new K/V rows are scattered into that layer's paged
-cache and ragged paged attention runs over the batch. Each layer has its own
-KV pool, so a step touches 24 distinct caches (>> the 256 MB Infinity Cache).
+cache and ragged paged attention runs over the batch -- one launch per layer
+(le_ragged_paged_attention_store; --separate-scatter runs le_kv_cache_write
+then the attention). Each layer has its own KV pool, so a step touches 24
+distinct caches (>> the 256 MB Infinity Cache).
 
 Workloads (Qwen2.5-0.5B GQA: 14 q heads, 2 kv heads, head_dim 64, block 16):
   config2  64 seqs, context log-uniform in [64, 4096], tables from a
@@ -192,6 +194,8 @@ def main():
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--graph", action="store_true", help="replay the step as one captured HIP graph")
+    ap.add_argument("--separate-scatter", action="store_true",
+                    help="scatter with le_kv_cache_write, then attend (instead of the fused entry point)")
     ap.add_argument("--e2e", choices=["decode64", "config4", "config5", "all", "none"], default="decode64",
                     help="end-to-end leg after the attention measurement (see e2e_leg)")
     ap.add_argument("--e2e-layers", type=int, default=None, help="model layers (default: all)")
@@ -258,8 +262,12 @@ def main():
     def eager_step():
         plan.upload(stream)
         for l in range(L):
-            kernels.store_kv(knew[l], vnew[l], slots, kc[l], vc[l], stream=stream)
-            attn(l)
+            if args.separate_scatter:
+                kernels.store_kv(knew[l], vnew[l], slots, kc[l], vc[l], stream=stream)
+                attn(l)
+            else:  # le_ragged_paged_attention_store: the scatter folded into the attention launch
+                kernels.ragged_paged_attention(qs[l], kc[l], vc[l], plan, case.scale, out=outs[l],
+                                               workspace=ws, stream=stream, k_new=knew[l], v_new=vnew[l])
 
     step = eager_step
     if args.graph:

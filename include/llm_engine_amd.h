@@ -203,6 +203,24 @@ int le_ragged_paged_attention(const void* q, le_dtype act_dtype, const void* k_c
                               const le_step_plan* plan, float scale, void* out, void* workspace,
                               size_t workspace_bytes, hipStream_t stream);
 
+/* ------------------------------------------------------------------------
+ * (2)+(3) The scatter and the attention of a step in one call.
+ * Equals le_kv_cache_write(k_new, v_new, new_dtype, <plan slots>, k_cache,
+ * v_cache, kv_dtype, n_tokens, kv_heads*head_dim, num_cache_blocks*block_size)
+ * followed by le_ragged_paged_attention on the same plan (the reference's
+ * launch_store_kv + attention launch, cuda_model.cu:368-377). When every
+ * sequence has one row in the step (decode rows only), the store happens
+ * inside the attention launch: the workgroup that owns a row's last context
+ * partition writes the row before its first K/V load. Otherwise it is a
+ * separate launch first (rows of one prefill chunk read each other's new keys). k_new, v_new: [n_tokens][kv_heads *
+ * head_dim] in new_dtype.
+ * ------------------------------------------------------------------------ */
+int le_ragged_paged_attention_store(const void* q, le_dtype act_dtype, const void* k_new,
+                                    const void* v_new, le_dtype new_dtype, void* k_cache,
+                                    void* v_cache, le_dtype kv_dtype, int64_t num_cache_blocks,
+                                    const le_step_plan* plan, float scale, void* out,
+                                    void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

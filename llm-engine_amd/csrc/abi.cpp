@@ -168,10 +168,17 @@ size_t le_ragged_workspace_size(const le_step_plan* plan) {
                        plan->cfg.head_dim);
 }
 
-int le_ragged_paged_attention(const void* q, le_dtype act_dtype, const void* k_cache,
-                              const void* v_cache, le_dtype kv_dtype, int64_t num_cache_blocks,
-                              const le_step_plan* plan, float scale, void* out, void* workspace,
-                              size_t workspace_bytes, hipStream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// Ragged attention over a packed step; with k_new, the step's new K/V rows are
+// stored at the plan's slots first (inside the decode launch on a pure decode
+// step, by a scatter launch otherwise).
+int ragged_attention(const void* q, le_dtype act_dtype, const void* k_new, const void* v_new,
+                     le_dtype new_dtype, const void* k_cache, const void* v_cache, le_dtype kv_dtype,
+                     int64_t num_cache_blocks, const le_step_plan* plan, float scale, void* out,
+                     void* workspace, size_t workspace_bytes, hipStream_t stream) {
   if (!plan || !valid_dtype(act_dtype) || !valid_dtype(kv_dtype)) return LE_EINVAL;
   if (plan->n_tokens == 0) return LE_OK;
   const le_plan_config& cfg = plan->cfg;
@@ -205,7 +212,23 @@ int le_ragged_paged_attention(const void* q, le_dtype act_dtype, const void* k_c
   d.n_rows = plan->n_decode_items; d.nsplit = 1;
   d.q_heads = cfg.q_heads; d.kv_heads = cfg.kv_heads; d.head_dim = cfg.head_dim;
   d.block_size = cfg.block_size; d.scale_log2 = scale_log2; d.num_cache_blocks = num_cache_blocks;
-  hipError_t e = le::attention_decode(d, act_dtype == LE_BF16, kv_dtype == LE_BF16, stream);
+  const int64_t num_slots = num_cache_blocks * cfg.block_size;
+  hipError_t e = hipSuccess;
+  if (k_new) {
+    // Inside the launch only if every sequence has a single row in the step:
+    // rows of one sequence (a prefill chunk, which an fp32 cache runs as
+    // decode rows) read each other's new keys across workgroups.
+    if (plan->n_tokens != plan->n_seqs || plan->n_decode_items == 0) {
+      e = le::kv_cache_write(k_new, v_new, new_dtype == LE_BF16, arr(plan->off_slots),
+                             const_cast<void*>(k_cache), const_cast<void*>(v_cache), kv_dtype == LE_BF16,
+                             plan->n_tokens, cfg.kv_heads * cfg.head_dim, num_slots, stream);
+      if (e != hipSuccess) return hip_status(e);
+    } else {
+      d.k_new = k_new; d.v_new = v_new; d.new_bf16 = new_dtype == LE_BF16;
+      d.slots = arr(plan->off_slots); d.num_slots = num_slots;
+    }
+  }
+  e = le::attention_decode(d, act_dtype == LE_BF16, kv_dtype == LE_BF16, stream);
   if (e != hipSuccess) return hip_status(e);
 
   if (plan->n_chunk_items > 0) {
@@ -227,6 +250,29 @@ int le_ragged_paged_attention(const void* q, le_dtype act_dtype, const void* k_c
   }
 
   return hip_status(e);
+}
+
+}  // namespace
+
+extern "C" {
+
+int le_ragged_paged_attention(const void* q, le_dtype act_dtype, const void* k_cache,
+                              const void* v_cache, le_dtype kv_dtype, int64_t num_cache_blocks,
+                              const le_step_plan* plan, float scale, void* out, void* workspace,
+                              size_t workspace_bytes, hipStream_t stream) {
+  return ragged_attention(q, act_dtype, nullptr, nullptr, LE_F32, k_cache, v_cache, kv_dtype,
+                          num_cache_blocks, plan, scale, out, workspace, workspace_bytes, stream);
+}
+
+int le_ragged_paged_attention_store(const void* q, le_dtype act_dtype, const void* k_new,
+                                    const void* v_new, le_dtype new_dtype, void* k_cache,
+                                    void* v_cache, le_dtype kv_dtype, int64_t num_cache_blocks,
+                                    const le_step_plan* plan, float scale, void* out,
+                                    void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (!k_new || !v_new || !valid_dtype(new_dtype)) return LE_EINVAL;
+  if (plan && plan->cfg.head_dim % 8 != 0) return LE_EUNSUPPORTED;
+  return ragged_attention(q, act_dtype, k_new, v_new, new_dtype, k_cache, v_cache, kv_dtype,
+                          num_cache_blocks, plan, scale, out, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

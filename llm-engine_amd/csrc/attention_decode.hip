@@ -94,6 +94,44 @@ __device__ __forceinline__ Work resolve(const DecodeParams& p) {
               ns == 1 ? -1 : pb + split, pb, ns, split < ns};
 }
 
+// The new K/V row of a decode row, for kv head kvh, stored by the workgroup
+// of the row's last partition (the only one whose keys reach the row's own
+// position) before it loads anything from the cache: the scatter of
+// le_kv_cache_write (store_kv.cu:20-36) folded into the attention launch.
+// One thread per 8-element piece; the caller waits for the stores and
+// synchronises the workgroup before its first K/V load, so the row is read
+// back from the cache like every other key (no other workgroup reads its
+// lines in this launch).
+template <typename C>
+__device__ __forceinline__ void store_new_row(const DecodeParams& p, const Work& w, int kvh, int hd) {
+  if (p.k_new == nullptr || !(w.part < 0 || w.part == w.part_begin + w.n_parts - 1)) return;
+  const int pieces = hd / 8;
+  const int t = threadIdx.x;
+  if (t >= 2 * pieces) return;
+  const int64_t slot = p.slots[w.token];
+  if (slot < 0 || slot >= p.num_slots) return;
+  const int which = t >= pieces;  // 0 = K, 1 = V
+  const int c = t - which * pieces;
+  const int64_t src = (static_cast<int64_t>(w.token) * p.kv_heads + kvh) * hd + c * 8;
+  const int64_t dst = (slot * p.kv_heads + kvh) * hd + c * 8;
+  float v[8];
+  if (p.new_bf16) {
+    elem<bf16_t>::widen(ld16(static_cast<const bf16_t*>(which ? p.v_new : p.k_new) + src), v);
+  } else {
+    const float* f = static_cast<const float*>(which ? p.v_new : p.k_new) + src;
+    elem<float>::widen(ld16(f), v);
+    elem<float>::widen(ld16(f + 4), v + 4);
+  }
+  C* out = static_cast<C*>(const_cast<void*>(which ? p.v_cache : p.k_cache)) + dst;
+  if constexpr (sizeof(C) == 2) {
+    *reinterpret_cast<uint4*>(out) = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                                pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
+  } else {
+    reinterpret_cast<float4*>(out)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4*>(out)[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+}
+
 // Partials cross workgroups (and XCDs, whose L2s are not coherent with each
 // other) through device-coherent accesses: relaxed atomic stores and loads at
 // agent scope, which the hardware performs at the coherence point. This avoids
@@ -424,6 +462,7 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_kernel(DecodeParams p) {
   const bf16_t* kc = static_cast<const bf16_t*>(p.k_cache) + kvh * HD + grp * 8;
   const bf16_t* vc = static_cast<const bf16_t*>(p.v_cache) + kvh * HD + grp * 8;
   char* vt = lds + wave * L::VT_BYTES;
+  store_new_row<bf16_t>(p, w, kvh, HD);
 
   // Q^T (B operand): column `col` = head kvh*G + col, 8 dims per k-step.
   bf16x8 qb[KS];
@@ -474,6 +513,7 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_kernel(DecodeParams p) {
         tab[i] = (bid >= 0 && bid < p.num_cache_blocks) ? bid : -1;
       }
     }
+    if (p.k_new != nullptr) __builtin_amdgcn_s_waitcnt(0);  // the new row is stored
     __syncthreads();
     PROBE_TS(1);
     const int key_end = min(sb1 << bs_shift, w.pos + 1);
@@ -586,6 +626,11 @@ __global__ __launch_bounds__(kThreads) void valu_kernel(DecodeParams p) {
   const int kv_stride = p.kv_heads * HD;
   const KV* kc = static_cast<const KV*>(p.k_cache) + kvh * HD + sub * VEC;
   const KV* vc = static_cast<const KV*>(p.v_cache) + kvh * HD + sub * VEC;
+  if (p.k_new != nullptr) {
+    store_new_row<float>(p, w, kvh, HD);
+    __builtin_amdgcn_s_waitcnt(0);  // the new row is stored before any wave loads it
+    __syncthreads();
+  }
 
   float qf[G][VEC];
   {

@@ -57,6 +57,15 @@ struct DecodeParams {
   const int32_t* token_pos;
   void* out;
   PartialLayout parts;
+  // With a plan and a pure decode step: the step's new K/V rows ([n_tokens]
+  // [kv_heads * head_dim], dtype new_bf16 ? bf16 : fp32). The last partition
+  // of each row stores its row (for its kv head) at slots[token] before any
+  // K/V load of the launch reads it. Null: the rows are already in the cache.
+  const void* k_new;
+  const void* v_new;
+  const int32_t* slots;
+  int new_bf16;
+  int64_t num_slots;
   const DecodeItem* items;  // null: one item per (token, split) with `nsplit` splits
   const int32_t* item_ids;  // with items: block ids of item i at item_ids[i * ids_stride + j]
   int ids_stride;

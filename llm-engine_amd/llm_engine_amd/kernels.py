@@ -218,7 +218,12 @@ class Plan:
 
 def ragged_paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                            plan: Plan, scale: float, out: torch.Tensor | None = None,
-                           workspace: torch.Tensor | None = None, stream=None) -> torch.Tensor:
+                           workspace: torch.Tensor | None = None, stream=None,
+                           k_new: torch.Tensor | None = None, v_new: torch.Tensor | None = None) -> torch.Tensor:
+    """Ragged paged attention over a packed step. With k_new/v_new ([N, kv_dim],
+    the step's new rows), the rows are first stored at the plan's slots
+    (le_ragged_paged_attention_store: inside the attention launch on a decode
+    step)."""
     P = plan.plan
     cfg = P.cfg
     n = P.n_tokens
@@ -232,6 +237,14 @@ def ragged_paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     need = plan.workspace_size()
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = torch.zeros(max(need, 1), dtype=torch.uint8, device=q.device)
+    if k_new is not None:
+        _req(v_new is not None and k_new.shape == v_new.shape == (n, kv_dim) and k_new.dtype == v_new.dtype
+             and k_new.is_contiguous() and v_new.is_contiguous(), "k_new, v_new: [N, kv_dim], same dtype")
+        check("le_ragged_paged_attention_store", _lib.load().le_ragged_paged_attention_store(
+            _p(q), _dt(q), _p(k_new), _p(v_new), _dt(k_new), _p(k_cache), _p(v_cache), _dt(k_cache), num_blocks,
+            ctypes.byref(P), float(scale), _p(out), _p(workspace), workspace.numel() * workspace.element_size(),
+            _stream(stream)))
+        return out
     check("le_ragged_paged_attention", _lib.load().le_ragged_paged_attention(
         _p(q), _dt(q), _p(k_cache), _p(v_cache), _dt(k_cache), num_blocks, ctypes.byref(P),
         float(scale), _p(out), _p(workspace), workspace.numel() * workspace.element_size(),

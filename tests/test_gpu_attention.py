@@ -228,3 +228,49 @@ def test_chunk_tile16_and_long_context(gpu):
         err = max_abs(got, want)
         print(f"tile {tile}: items {plan.plan.n_chunk_items} parts {plan.plan.n_parts} max|err| {err:.3e}")
         assert err < TOL_BF16
+
+
+@pytest.mark.parametrize("kv_bf16,new_bf16", [(True, False), (True, True), (False, False)])
+@pytest.mark.parametrize("mixed", [False, True])
+def test_store_then_attend(gpu, kv_bf16, new_bf16, mixed):
+    """le_ragged_paged_attention_store: the step's new K/V rows are stored at
+    the plan's slots (inside the decode launch on a decode-only step) and
+    attended to. Equal to the oracle's store_kv then attention: the caches
+    bit-exact on every slot, the outputs within tolerance. Split rows
+    (partition 256) put the new row in the last partition."""
+    import oracle
+    from llm_engine_amd import kernels
+    rng = np.random.default_rng(51)
+    ctx = [1, 17, 300, 1500, 64, 2049] + ([600] if mixed else [])
+    q_len = [1] * 6 + ([70] if mixed else [])
+    case = make_case(ctx, q_len=q_len, num_blocks=1024, seed=52, kv_bf16=kv_bf16)
+    n, kv_dim = len(case.token_pos), case.kv_heads * case.head_dim
+    k_new = rng.standard_normal((n, kv_dim), dtype=np.float32)
+    v_new = rng.standard_normal((n, kv_dim), dtype=np.float32)
+    if new_bf16:
+        k_new = oracle.bf16_to_f32(oracle.f32_to_bf16(k_new))
+        v_new = oracle.bf16_to_f32(oracle.f32_to_bf16(v_new))
+    slots = np.array([case.blocks_of(s)[p // 16] * 16 + p % 16 for s, p in zip(case.token_seq, case.token_pos)],
+                     dtype=np.int32)
+    want_k, want_v = case.k_cache.copy(), case.v_cache.copy()
+    oracle.store_kv(k_new, v_new, slots, want_k, want_v)
+    case.k_cache, case.v_cache = want_k, want_v  # the oracle attends over the stored rows
+    q, qh = device_q(case, torch.float32, gpu)
+    old_k = make_case(ctx, q_len=q_len, num_blocks=1024, seed=52, kv_bf16=kv_bf16)
+    kc, vc = to_dev_cache(old_k.k_cache, gpu), to_dev_cache(old_k.v_cache, gpu)
+    plan = kernels.Plan(slices_of(case), case.q_heads, case.kv_heads, case.head_dim, case.block_size,
+                        kc.dtype, partition_tokens=256).upload()
+    assert np.array_equal(plan.host_array("slots"), slots)
+    nd = torch.bfloat16 if new_bf16 else torch.float32
+    out = kernels.ragged_paged_attention(q, kc, vc, plan, case.scale,
+                                         k_new=torch.from_numpy(k_new).to(gpu).to(nd),
+                                         v_new=torch.from_numpy(v_new).to(gpu).to(nd))
+    torch.cuda.synchronize()
+    got_k = kc.cpu().view(torch.int16).numpy().view(np.uint16) if kv_bf16 else kc.cpu().numpy()
+    got_v = vc.cpu().view(torch.int16).numpy().view(np.uint16) if kv_bf16 else vc.cpu().numpy()
+    assert np.array_equal(got_k.view(np.uint8), want_k.view(np.uint8))
+    assert np.array_equal(got_v.view(np.uint8), want_v.view(np.uint8))
+    err = max_abs(out.float().cpu().numpy(), oracle_out(case, qh))
+    print(f"store+attend kv_bf16={kv_bf16} new_bf16={new_bf16} mixed={mixed}: parts {plan.plan.n_parts} "
+          f"max|err| {err:.3e}")
+    assert err < tol_for(kv_bf16, torch.float32)
