@@ -12,20 +12,19 @@
 // workgroup. Each K/V element of a kv head is read from HBM once and serves
 // the whole GQA group.
 //
-//   bf16 cache -> mfma_kernel. The G query heads of the group are the N=16
-//     columns of v_mfma_f32_16x16x32_bf16: S^T = K . Q^T takes K rows straight
-//     from HBM into A-operand registers (16 keys x 8 dims per lane group), so
-//     the score of a key for all G heads costs no vector-ALU work; the softmax
-//     runs on the 16 x 16 accumulator (one head per lane column); V is
-//     transposed through a wave-private LDS tile and O^T = V^T . P^T reuses the
-//     accumulator of P^T directly as the B operand (an MFMA only needs A and B
-//     to agree on the order of k inside a lane group). Each wave runs its own
-//     online softmax over 64-key tiles; the four waves merge at the end.
-//   fp32 cache -> valu_kernel. Exact fp32 products: a K/V row is read with
-//     16-byte loads by LPT lanes, q . k partial sums are reduced inside the
-//     row's lanes with DPP moves, scores go to LDS, the softmax runs over the
-//     whole partition at once, then V is streamed with the probabilities
-//     broadcast from LDS.
+//   mfma_kernel, templated on the cache element type. The G query heads of
+//     the group are the N = 16 columns of the MFMA: S^T = K . Q^T takes K rows
+//     straight from HBM into A-operand registers, so the score of a key for
+//     all G heads costs no vector-ALU work; the softmax runs on the 16 x 16
+//     accumulator (one head per lane column); V is staged in a wave-private
+//     LDS tile and O^T = V^T . P^T reuses the accumulator of P^T directly as
+//     the B operand (an MFMA only needs A and B to agree on the order of k
+//     inside a lane group). Each wave runs its own online softmax over its
+//     tiles; the four waves merge at the end.
+//       bf16 cache: 64-key tiles on v_mfma_f32_16x16x32_bf16, V^T read with
+//       the transposing ds_read_b64_tr_b16.
+//       fp32 cache: 32-key tiles on v_mfma_f32_16x16x4_f32 (exact fp32
+//       products), V^T read as single floats of the row-major tile.
 //
 // Split rows are merged inside the same launch: each partition writes its
 // unnormalised partial (acc, running max, sum), and the last workgroup of the
@@ -45,12 +44,9 @@ namespace {
 #ifndef LE_DECODE_WAVES
 #define LE_DECODE_WAVES 4
 #endif
-constexpr int kWaves = 4;  // valu_kernel
-constexpr int kMfmaWaves = LE_DECODE_WAVES;  // mfma_kernel
+constexpr int kMfmaWaves = LE_DECODE_WAVES;
 constexpr int kMfmaThreads = kMfmaWaves * 64;
-constexpr int kThreads = kWaves * kWave;
-constexpr int kChunk = 512;   // valu_kernel: scores held in LDS per pass
-constexpr int kTile = 64;     // mfma_kernel: keys per wave tile
+constexpr int kTile = 64;     // bf16 tiles: keys per wave tile
 constexpr int kMaxG = 16;     // heads per kv head the MFMA columns can hold
 constexpr int kMergeBatch = 8;       // partial accumulators loaded per batch in the merge
 constexpr int kMaxMergeEntries = 1024;  // n_parts * G the merge stages in LDS
@@ -247,13 +243,13 @@ __device__ __forceinline__ void finish(const DecodeParams& p, const Work& w, int
 // ---------------------------------------------------------------------------
 // bf16 cache: MFMA kernel
 // ---------------------------------------------------------------------------
-template <int HD> struct MfmaLds {
-  static constexpr int V_STRIDE = HD * 2 + 16;           // bytes per key row of the V tile
-  static constexpr int VT_BYTES = kTile * V_STRIDE;      // per wave
+template <int HD, int VT_BYTES> struct MfmaLds {
   static constexpr int RED_STRIDE = HD + 4;              // floats per head in the merge area
   static constexpr int RED_BYTES = kMfmaWaves * kMaxG * RED_STRIDE * 4;
   static constexpr int BYTES = (kMfmaWaves * VT_BYTES > RED_BYTES ? kMfmaWaves * VT_BYTES : RED_BYTES);
 };
+// bytes per key row of a wave's V tile: the row plus 16 bytes against bank conflicts
+template <int HD> constexpr int kVStrideBf16 = HD * 2 + 16;
 
 constexpr int kTabCap = 1024;  // block ids of a partition staged in LDS
 
@@ -288,10 +284,6 @@ template <int HD> struct WaveAcc {
 // is past the end (or whose block id is invalid) reads a valid address of the
 // cache and is masked afterwards. Branches around loads would make the
 // compiler wait for all outstanding loads at every join, serialising them.
-// Issues the tile's 8 * KS 16-byte loads without any branch: a lane whose key
-// is past the end (or whose block id is invalid) reads a valid address of the
-// cache and is masked afterwards. Branches around loads would make the
-// compiler wait for all outstanding loads at every join, serialising them.
 // Block ids come from the LDS copy of the table (`tab`, indexed from the
 // segment's first block), never through a generic pointer: a flat load would
 // count against the global-load counter and stall behind the K/V loads.
@@ -319,7 +311,7 @@ template <int HD>
 __device__ __forceinline__ void compute_tile(WaveAcc<HD>& st, const TileRegs<HD / 32>& r,
                                              const bf16x8* qb, int key0, int key_end,
                                              float scale_log2, char* vt, int col, int grp) {
-  using L = MfmaLds<HD>;
+  constexpr int V_STRIDE = kVStrideBf16<HD>;
   constexpr int KS = HD / 32;
   constexpr int DT = HD / 16;
 #ifdef LE_PROBE_NOCOMPUTE
@@ -378,7 +370,7 @@ __device__ __forceinline__ void compute_tile(WaveAcc<HD>& st, const TileRegs<HD 
 #pragma unroll
     for (int ks = 0; ks < KS; ks++) {
       const bool vlive = key0 + i * 16 + col < key_end && r.ok[i];
-      *reinterpret_cast<uint4*>(vt + (i * 16 + col) * L::V_STRIDE + (ks * 32 + grp * 8) * 2) =
+      *reinterpret_cast<uint4*>(vt + (i * 16 + col) * V_STRIDE + (ks * 32 + grp * 8) * 2) =
           vlive ? r.v[i][ks] : make_uint4(0, 0, 0, 0);
     }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -398,8 +390,8 @@ __device__ __forceinline__ void compute_tile(WaveAcc<HD>& st, const TileRegs<HD 
       pb[j] = static_cast<__bf16>(s[2 * kk][j]);
       pb[4 + j] = static_cast<__bf16>(s[2 * kk + 1][j]);
     }
-    const char* r_lo = vt + (kk * 32 + grp * 4 + (col >> 2)) * L::V_STRIDE + (col & 3) * 8;
-    const char* r_hi = r_lo + 16 * L::V_STRIDE;
+    const char* r_lo = vt + (kk * 32 + grp * 4 + (col >> 2)) * V_STRIDE + (col & 3) * 8;
+    const char* r_hi = r_lo + 16 * V_STRIDE;
 #pragma unroll
     for (int d = 0; d < DT; d++) {
       const bf16x4 lo = lds_read_tr(r_lo + d * 32);
@@ -413,13 +405,168 @@ __device__ __forceinline__ void compute_tile(WaveAcc<HD>& st, const TileRegs<HD 
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <typename ACT, int HD>
+// Tile operations of the MFMA decode kernel, per cache element type. A tile is
+// one wave's kKeys consecutive keys; the kernel around it (item, block ids,
+// pipelining, cross-wave and cross-workgroup merge) is shared.
+template <typename KV, int HD> struct DecodeTile;
+
+// bf16 cache: 64-key tiles on v_mfma_f32_16x16x32_bf16 (load_tile,
+// compute_tile above).
+template <int HD> struct DecodeTile<bf16_t, HD> {
+  static constexpr int kKeys = kTile;
+  static constexpr int VT_BYTES = kKeys * kVStrideBf16<HD>;
+  static constexpr bool kPipe = HD == 64;  // double-buffered where the registers allow it
+  static constexpr int kLaneElems = 8;     // dims per lane group and k-step
+  using Regs = TileRegs<HD / 32>;
+  struct QOp { bf16x8 b[HD / 32]; };
+  template <typename ACT>
+  __device__ __forceinline__ static void load_q(QOp& q, const ACT* row, bool ok, int grp) {
+    const ACT* r = row + grp * 8;
+#pragma unroll
+    for (int ks = 0; ks < HD / 32; ks++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) q.b[ks][e] = static_cast<__bf16>(ok ? elem<ACT>::load1(r + ks * 32 + e) : 0.f);
+  }
+  __device__ __forceinline__ static const bf16_t* lane_base(const void* cache, int kvh, int grp) {
+    return static_cast<const bf16_t*>(cache) + kvh * HD + grp * 8;
+  }
+  __device__ __forceinline__ static void load(Regs& r, const bf16_t* kc, const bf16_t* vc, int key0, int key_end,
+                                              int kv_stride, int bs_shift, const int* tab, int tab_base, int col) {
+    load_tile<HD>(r, kc, vc, key0, key_end, kv_stride, bs_shift, tab, tab_base, col);
+  }
+  __device__ __forceinline__ static void compute(WaveAcc<HD>& st, const Regs& r, const QOp& q, int key0, int key_end,
+                                                 float scale_log2, char* vt, int col, int grp) {
+    compute_tile<HD>(st, r, q.b, key0, key_end, scale_log2, vt, col, grp);
+  }
+};
+
+// fp32 cache: 32-key tiles on v_mfma_f32_16x16x4_f32, exact fp32 products.
+//   S^T = K . Q^T: lane (col, grp) holds key col of each 16-key subtile with
+//   its dims [grp*HD/4, (grp+1)*HD/4) (contiguous, 16-byte loads); k-step j
+//   takes dim grp*HD/4 + j from both K (A) and Q^T (B), so the sum over
+//   lane groups and steps covers every dim once.
+//   O^T += V^T . P^T: k-step j of the product covers keys
+//   16*(j/4) + 4*grp + j%4, which are exactly the scores the lane's S^T
+//   accumulators hold, so P^T needs no shuffle; the V^T operand reads
+//   single floats of the row-major V tile staged in LDS.
+template <int HD> struct DecodeTile<float, HD> {
+  static constexpr int kKeys = 32;
+  static constexpr int kSub = kKeys / 16;   // 16-key subtiles
+  static constexpr int kLaneDims = HD / 4;  // dims per lane per key
+  static constexpr int kPieces = kLaneDims / 4;  // 16-byte loads per lane per key
+  static constexpr int V_STRIDE = HD * 4 + 16;   // bytes per key row of the V tile
+  static constexpr int VT_BYTES = kKeys * V_STRIDE;
+  static constexpr bool kPipe = HD == 64;
+  struct Regs {
+    float4 k[kSub][kPieces], v[kSub][kPieces];
+    bool ok[kSub];
+  };
+  struct QOp { float q[kLaneDims]; };
+  template <typename ACT>
+  __device__ __forceinline__ static void load_q(QOp& q, const ACT* row, bool ok, int grp) {
+    const ACT* r = row + grp * kLaneDims;
+#pragma unroll
+    for (int j = 0; j < kLaneDims; j++) q.q[j] = ok ? elem<ACT>::load1(r + j) : 0.f;
+  }
+  __device__ __forceinline__ static const float* lane_base(const void* cache, int kvh, int grp) {
+    return static_cast<const float*>(cache) + kvh * HD + grp * kLaneDims;
+  }
+  // Branch-free like the bf16 tile: a lane whose key is past the end (or in
+  // an invalid block) reads a valid address and is masked afterwards.
+  __device__ __forceinline__ static void load(Regs& r, const float* kc, const float* vc, int key0, int key_end,
+                                              int kv_stride, int bs_shift, const int* tab, int tab_base, int col) {
+    const int bs_mask = (1 << bs_shift) - 1;
+#pragma unroll
+    for (int i = 0; i < kSub; i++) {
+      const int key = min(key0 + i * 16 + col, key_end - 1);
+      const int bid = tab[(key >> bs_shift) - tab_base];
+      r.ok[i] = bid >= 0;
+      const int64_t slot = (static_cast<int64_t>(r.ok[i] ? bid : 0) << bs_shift) + (key & bs_mask);
+#pragma unroll
+      for (int c = 0; c < kPieces; c++) {
+        const uint4 kk = ld16_stream(kc + slot * kv_stride + c * 4);
+        const uint4 vv = ld16_stream(vc + slot * kv_stride + c * 4);
+        r.k[i][c] = make_float4(__uint_as_float(kk.x), __uint_as_float(kk.y), __uint_as_float(kk.z), __uint_as_float(kk.w));
+        r.v[i][c] = make_float4(__uint_as_float(vv.x), __uint_as_float(vv.y), __uint_as_float(vv.z), __uint_as_float(vv.w));
+      }
+    }
+  }
+  __device__ __forceinline__ static void compute(WaveAcc<HD>& st, const Regs& r, const QOp& q, int key0, int key_end,
+                                                 float scale_log2, char* vt, int col, int grp) {
+    constexpr int DT = HD / 16;
+    // ---- S^T: kSub subtiles of 16 keys x 16 heads ----
+    f32x4 s[kSub];
+#pragma unroll
+    for (int i = 0; i < kSub; i++) {
+      s[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < kPieces; c++) {
+        const float kv4[4] = {r.k[i][c].x, r.k[i][c].y, r.k[i][c].z, r.k[i][c].w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) s[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv4[e], q.q[c * 4 + e], s[i], 0, 0, 0);
+      }
+    }
+    float mt = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kSub; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int key = key0 + i * 16 + grp * 4 + j;
+        const float v = key < key_end ? s[i][j] * scale_log2 : -INFINITY;
+        s[i][j] = v;
+        mt = fmaxf(mt, v);
+      }
+    mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+    const float m_new = fmaxf(st.m, mt);
+    const float alpha = exp2f(st.m - m_new);
+    st.m = m_new;
+    float ls = 0.f;
+#pragma unroll
+    for (int i = 0; i < kSub; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float e = exp2f(s[i][j] - m_new);
+        s[i][j] = e;
+        ls += e;
+      }
+    st.l = st.l * alpha + ls;
+#pragma unroll
+    for (int d = 0; d < DT; d++) st.acc[d] *= alpha;
+
+    // V rows into this wave's LDS tile (row-major); a dead key's row is zeros.
+#pragma unroll
+    for (int i = 0; i < kSub; i++) {
+      const bool vlive = key0 + i * 16 + col < key_end && r.ok[i];
+#pragma unroll
+      for (int c = 0; c < kPieces; c++)
+        *reinterpret_cast<float4*>(vt + (i * 16 + col) * V_STRIDE + (grp * kLaneDims + c * 4) * 4) =
+            vlive ? r.v[i][c] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- O^T += V^T . P^T: k-step j covers keys 16*(j/4) + 4*grp + j%4 ----
+#pragma unroll
+    for (int j = 0; j < kSub * 4; j++) {
+      const float pb = s[j >> 2][j & 3];
+      const float* vrow = reinterpret_cast<const float*>(vt + (16 * (j >> 2) + 4 * grp + (j & 3)) * V_STRIDE);
+#pragma unroll
+      for (int d = 0; d < DT; d++) st.acc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vrow[d * 16 + col], pb, st.acc[d], 0, 0, 0);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();  // the tile is read before the next one overwrites it
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+};
+
+template <typename ACT, typename KV, int HD>
 __global__ __launch_bounds__(kMfmaThreads) void mfma_kernel(DecodeParams p) {
-  using L = MfmaLds<HD>;
-  constexpr int KS = HD / 32;  // MFMA k-steps over head dims
+  using T = DecodeTile<KV, HD>;
+  using L = MfmaLds<HD, T::VT_BYTES>;
   constexpr int DT = HD / 16;  // 16-dim output tiles
-  // Double-buffered tiles only where the registers allow it.
-  constexpr bool kPipe = HD == 64;
+  constexpr bool kPipe = T::kPipe;
   __shared__ __attribute__((aligned(16))) char lds[L::BYTES];
   __shared__ float fin_acc[kMaxG * HD];
   __shared__ float2 fin_ml[kMaxG];
@@ -459,22 +606,18 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_kernel(DecodeParams p) {
   const int bs = p.block_size;
   const int32_t* gtab = p.tables + w.table_off;
   const int kv_stride = p.kv_heads * HD;
-  const bf16_t* kc = static_cast<const bf16_t*>(p.k_cache) + kvh * HD + grp * 8;
-  const bf16_t* vc = static_cast<const bf16_t*>(p.v_cache) + kvh * HD + grp * 8;
-  char* vt = lds + wave * L::VT_BYTES;
-  store_new_row<bf16_t>(p, w, kvh, HD);
+  const KV* kc = T::lane_base(p.k_cache, kvh, grp);
+  const KV* vc = T::lane_base(p.v_cache, kvh, grp);
+  char* vt = lds + wave * T::VT_BYTES;
+  store_new_row<KV>(p, w, kvh, HD);
 
-  // Q^T (B operand): column `col` = head kvh*G + col, 8 dims per k-step.
-  bf16x8 qb[KS];
+  // Q^T (B operand): column `col` = head kvh*G + col.
+  typename T::QOp qb;
   {
     const bool ok = col < G;
-    const ACT* q = static_cast<const ACT*>(p.q) +
-                   (static_cast<int64_t>(w.token) * p.q_heads + kvh * G + (ok ? col : 0)) * HD + grp * 8;
-#pragma unroll
-    for (int ks = 0; ks < KS; ks++)
-#pragma unroll
-      for (int e = 0; e < 8; e++)
-        qb[ks][e] = static_cast<__bf16>(ok ? elem<ACT>::load1(q + ks * 32 + e) : 0.f);
+    T::template load_q<ACT>(qb, static_cast<const ACT*>(p.q) +
+                                    (static_cast<int64_t>(w.token) * p.q_heads + kvh * G + (ok ? col : 0)) * HD,
+                            ok, grp);
   }
 
   WaveAcc<HD> st;
@@ -485,8 +628,7 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_kernel(DecodeParams p) {
 #ifdef LE_PROBE_TIMING
   {
     float qs = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < KS; ks++) qs += static_cast<float>(qb[ks][0]);
+    qs += static_cast<float>(reinterpret_cast<const float*>(&qb)[0]);
     if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 16384)
       g_probe_ts[blockIdx.x][5] = __builtin_amdgcn_s_memrealtime() + (qs == 12345.f);
     if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 16384)
@@ -495,7 +637,7 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_kernel(DecodeParams p) {
 #endif
 
   const int bs_shift = __builtin_ctz(bs);  // block sizes are powers of two
-  const int stride = kMfmaWaves * kTile;
+  const int stride = kMfmaWaves * T::kKeys;
   // The partition in segments of at most kTabCap blocks: each segment's block
   // ids are staged in LDS (invalid ids as -1), then streamed tile by tile.
   for (int sb0 = w.b_begin; sb0 < w.b_end; sb0 += kTabCap) {
@@ -517,31 +659,31 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_kernel(DecodeParams p) {
     __syncthreads();
     PROBE_TS(1);
     const int key_end = min(sb1 << bs_shift, w.pos + 1);
-    int key0 = (sb0 << bs_shift) + wave * kTile;
+    int key0 = (sb0 << bs_shift) + wave * T::kKeys;
     if (key0 >= key_end) continue;
-    TileRegs<KS> ra;
-    load_tile<HD>(ra, kc, vc, key0, key_end, kv_stride, bs_shift, tab, sb0, col);
+    typename T::Regs ra;
+    T::load(ra, kc, vc, key0, key_end, kv_stride, bs_shift, tab, sb0, col);
     if constexpr (kPipe) {
       // The next tile's loads are issued unconditionally (clamped to valid
       // addresses past the end) so every path reaches each compute with the
       // same loads outstanding and the wait before it covers only the tile
       // being computed.
-      TileRegs<KS> rb;
+      typename T::Regs rb;
       while (true) {
-        load_tile<HD>(rb, kc, vc, key0 + stride, key_end, kv_stride, bs_shift, tab, sb0, col);
-        compute_tile<HD>(st, ra, qb, key0, key_end, p.scale_log2, vt, col, grp);
+        T::load(rb, kc, vc, key0 + stride, key_end, kv_stride, bs_shift, tab, sb0, col);
+        T::compute(st, ra, qb, key0, key_end, p.scale_log2, vt, col, grp);
         if (key0 + stride >= key_end) break;
-        load_tile<HD>(ra, kc, vc, key0 + 2 * stride, key_end, kv_stride, bs_shift, tab, sb0, col);
-        compute_tile<HD>(st, rb, qb, key0 + stride, key_end, p.scale_log2, vt, col, grp);
+        T::load(ra, kc, vc, key0 + 2 * stride, key_end, kv_stride, bs_shift, tab, sb0, col);
+        T::compute(st, rb, qb, key0 + stride, key_end, p.scale_log2, vt, col, grp);
         if (key0 + 2 * stride >= key_end) break;
         key0 += 2 * stride;
       }
     } else {
       while (true) {
-        compute_tile<HD>(st, ra, qb, key0, key_end, p.scale_log2, vt, col, grp);
+        T::compute(st, ra, qb, key0, key_end, p.scale_log2, vt, col, grp);
         key0 += stride;
         if (key0 >= key_end) break;
-        load_tile<HD>(ra, kc, vc, key0, key_end, kv_stride, bs_shift, tab, sb0, col);
+        T::load(ra, kc, vc, key0, key_end, kv_stride, bs_shift, tab, sb0, col);
       }
     }
   }
@@ -591,242 +733,17 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_kernel(DecodeParams p) {
   PROBE_TS(7);
 }
 
-// ---------------------------------------------------------------------------
-// fp32 cache: vector-ALU kernel (exact fp32 products)
-// ---------------------------------------------------------------------------
-template <typename ACT, int HD, int G>
-__global__ __launch_bounds__(kThreads) void valu_kernel(DecodeParams p) {
-  using KV = float;
-  constexpr int VEC = elem<KV>::VEC;  // elements per 16-byte load
-  constexpr int LPT = HD / VEC;       // lanes per K/V row
-  constexpr int TPW = kWave / LPT;    // rows per wave load
-  static_assert(LPT <= kWave && (kWave % LPT) == 0, "head_dim too large for one wave");
-  static_assert(kChunk * 8 >= kWaves * 8 * HD, "LDS reuse for the cross-wave merge");
-
-  __shared__ float sbuf[kChunk * 8];  // [token][8 heads] scores, then probabilities
-  __shared__ float wred[kWaves][8];
-  __shared__ float fin_acc[8 * HD];
-  __shared__ float2 fin_ml[8];
-  __shared__ float2 merge_ml[8];
-  __shared__ float2 merge_w[kMaxMergeEntries];
-  __shared__ int flag;
-
-  const Work w = resolve(p);
-  if (!w.valid) return;
-  const int tid = threadIdx.x;
-  const int lane = tid & (kWave - 1);
-  const int wave = tid >> 6;
-  const int sub = lane % LPT;
-  const int row = lane / LPT;
-  const int kvh = blockIdx.y;
-  const int bs = p.block_size;
-  const int token = w.token;
-  const int pos = w.pos;
-  const int32_t* table = p.tables + w.table_off;
-  const int kv_stride = p.kv_heads * HD;
-  const KV* kc = static_cast<const KV*>(p.k_cache) + kvh * HD + sub * VEC;
-  const KV* vc = static_cast<const KV*>(p.v_cache) + kvh * HD + sub * VEC;
-  if (p.k_new != nullptr) {
-    store_new_row<float>(p, w, kvh, HD);
-    __builtin_amdgcn_s_waitcnt(0);  // the new row is stored before any wave loads it
-    __syncthreads();
-  }
-
-  float qf[G][VEC];
-  {
-    const ACT* q = static_cast<const ACT*>(p.q) +
-                   (static_cast<int64_t>(token) * p.q_heads + kvh * G) * HD + sub * VEC;
-#pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-      for (int e = 0; e < VEC; e++) qf[g][e] = elem<ACT>::load1(q + g * HD + e);
-  }
-
-  float acc[G][VEC];
-  float m_run[G], l_run[G];
-#pragma unroll
-  for (int g = 0; g < G; g++) {
-    m_run[g] = -FLT_MAX;
-    l_run[g] = 0.f;
-#pragma unroll
-    for (int e = 0; e < VEC; e++) acc[g][e] = 0.f;
-  }
-
-  const int ntok = (w.b_end - w.b_begin) * bs;
-  for (int c0 = 0; c0 < ntok; c0 += kChunk) {
-    const int cn = min(kChunk, ntok - c0);
-    const int cb0 = w.b_begin + c0 / bs;
-    const int cnb = cn / bs;
-
-    // ---- scores: s = (q . k) * scale * log2(e), masked past pos ----
-    for (int bi = wave; bi < cnb; bi += kWaves) {
-      const int blk = cb0 + bi;
-      const int bid = __builtin_amdgcn_readfirstlane(table[blk]);
-      const bool ok = bid >= 0 && bid < p.num_cache_blocks;
-      const int64_t slot0 = static_cast<int64_t>(ok ? bid : 0) * bs;
-      for (int r = 0; r < bs; r += TPW) {
-        const int tb = r + row;
-        float kf[VEC];
-        elem<KV>::widen(ld16_stream(kc + (slot0 + tb) * kv_stride), kf);
-        float s[G];
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-          float d = 0.f;
-#pragma unroll
-          for (int e = 0; e < VEC; e++) d += qf[g][e] * kf[e];
-          s[g] = group_sum<LPT>(d);
-        }
-        const bool live = ok && (blk * bs + tb) <= pos;
-        float mine = -INFINITY;
-#pragma unroll
-        for (int g = 0; g < G; g++)
-          if (sub == g) mine = live ? s[g] * p.scale_log2 : -INFINITY;
-        if (sub < G) sbuf[(bi * bs + tb) * 8 + sub] = mine;
-      }
-    }
-    __syncthreads();
-
-    // ---- softmax over the chunk: one max and one exp2 per score ----
-    float mloc[G];
-#pragma unroll
-    for (int g = 0; g < G; g++) mloc[g] = -INFINITY;
-    for (int t = tid; t < cn; t += kThreads) {
-#pragma unroll
-      for (int g = 0; g < G; g++) mloc[g] = fmaxf(mloc[g], sbuf[t * 8 + g]);
-    }
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-      const float wm = wave_max(mloc[g]);
-      if (lane == 0) wred[wave][g] = wm;
-    }
-    __syncthreads();
-    float m_new[G], alpha[G];
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-      float mc = wred[0][g];
-#pragma unroll
-      for (int v = 1; v < kWaves; v++) mc = fmaxf(mc, wred[v][g]);
-      m_new[g] = fmaxf(m_run[g], mc);
-      alpha[g] = exp2f(m_run[g] - m_new[g]);
-    }
-    float lsum[G];
-#pragma unroll
-    for (int g = 0; g < G; g++) lsum[g] = 0.f;
-    for (int t = tid; t < cn; t += kThreads) {
-#pragma unroll
-      for (int g = 0; g < G; g++) {
-        const float e = exp2f(sbuf[t * 8 + g] - m_new[g]);
-        sbuf[t * 8 + g] = e;
-        lsum[g] += e;
-      }
-    }
-    __syncthreads();  // every thread has read wred's maxima
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-      const float ws = wave_sum(lsum[g]);
-      if (lane == 0) wred[wave][g] = ws;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-      float lc = 0.f;
-#pragma unroll
-      for (int v = 0; v < kWaves; v++) lc += wred[v][g];
-      l_run[g] = l_run[g] * alpha[g] + lc;
-      m_run[g] = m_new[g];
-#pragma unroll
-      for (int e = 0; e < VEC; e++) acc[g][e] *= alpha[g];
-    }
-
-    // ---- acc += p * v ----
-    for (int bi = wave; bi < cnb; bi += kWaves) {
-      const int blk = cb0 + bi;
-      const int bid = __builtin_amdgcn_readfirstlane(table[blk]);
-      const bool ok = bid >= 0 && bid < p.num_cache_blocks;
-      if (!ok) continue;  // every score of the block is -inf, so p = 0
-      const int64_t slot0 = static_cast<int64_t>(bid) * bs;
-      for (int r = 0; r < bs; r += TPW) {
-        const int tb = r + row;
-        float vf[VEC];
-        elem<KV>::widen(ld16_stream(vc + (slot0 + tb) * kv_stride), vf);
-        const float4* pr = reinterpret_cast<const float4*>(sbuf + (bi * bs + tb) * 8);
-        const float4 p0 = pr[0], p1 = pr[1];
-        const float pg[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-#pragma unroll
-        for (int g = 0; g < G; g++)
-#pragma unroll
-          for (int e = 0; e < VEC; e++) acc[g][e] += pg[g] * vf[e];
-      }
-    }
-    __syncthreads();  // sbuf is rewritten by the next chunk
-  }
-
-  // ---- merge the TPW rows of each wave (lanes with one `sub`), then the waves ----
-#pragma unroll
-  for (int g = 0; g < G; g++)
-#pragma unroll
-    for (int e = 0; e < VEC; e++) {
-      float a = acc[g][e];
-#pragma unroll
-      for (int off = LPT; off < kWave; off <<= 1) {
-        if (off == 8) a += dpp::mov<0x128>(a);  // row_ror:8 == lane ^ 8 inside a row
-        else a += __shfl_xor(a, off, kWave);
-      }
-      acc[g][e] = a;
-    }
-  float* red = sbuf;  // [wave][8][HD]
-  if (row == 0) {
-#pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-      for (int e = 0; e < VEC; e++) red[(wave * 8 + g) * HD + sub * VEC + e] = acc[g][e];
-  }
-#pragma unroll
-  for (int g = 0; g < G; g++)
-    if (tid == g) fin_ml[g] = make_float2(m_run[g], l_run[g]);
-  __syncthreads();
-  for (int i = tid; i < G * HD; i += kThreads) {
-    const int g = i / HD, d = i % HD;
-    float v = red[g * HD + d];
-#pragma unroll
-    for (int u = 1; u < kWaves; u++) v += red[(u * 8 + g) * HD + d];
-    fin_acc[i] = v;
-  }
-  __syncthreads();
-  finish<ACT, HD, kThreads>(p, w, G, kvh, fin_acc, fin_ml, merge_ml, merge_w, &flag);
-}
-
-template <typename ACT, int HD, int G>
-hipError_t launch_valu(const DecodeParams& p, hipStream_t s) {
-  const dim3 grid(p.n_rows, p.kv_heads, p.items ? 1 : p.nsplit);
-  valu_kernel<ACT, HD, G><<<grid, kThreads, 0, s>>>(p);
-  return hipGetLastError();
-}
-
-template <typename ACT, int HD>
-hipError_t dispatch_valu(const DecodeParams& p, hipStream_t s) {
-  switch (p.q_heads / p.kv_heads) {
-    case 1: return launch_valu<ACT, HD, 1>(p, s);
-    case 2: return launch_valu<ACT, HD, 2>(p, s);
-    case 3: return launch_valu<ACT, HD, 3>(p, s);
-    case 4: return launch_valu<ACT, HD, 4>(p, s);
-    case 5: return launch_valu<ACT, HD, 5>(p, s);
-    case 6: return launch_valu<ACT, HD, 6>(p, s);
-    case 7: return launch_valu<ACT, HD, 7>(p, s);
-    case 8: return launch_valu<ACT, HD, 8>(p, s);
-    default: return hipErrorInvalidValue;
-  }
-}
-
 template <typename ACT>
 hipError_t dispatch(const DecodeParams& p, int kv_bf16, hipStream_t s) {
   const dim3 grid(p.n_rows, p.kv_heads, p.items ? 1 : p.nsplit);
   if (kv_bf16) {
-    if (p.head_dim == 64) mfma_kernel<ACT, 64><<<grid, kMfmaThreads, 0, s>>>(p);
-    else mfma_kernel<ACT, 128><<<grid, kMfmaThreads, 0, s>>>(p);
+    if (p.head_dim == 64) mfma_kernel<ACT, bf16_t, 64><<<grid, kMfmaThreads, 0, s>>>(p);
+    else mfma_kernel<ACT, bf16_t, 128><<<grid, kMfmaThreads, 0, s>>>(p);
     return hipGetLastError();
   }
-  return p.head_dim == 64 ? dispatch_valu<ACT, 64>(p, s) : dispatch_valu<ACT, 128>(p, s);
+  if (p.head_dim == 64) mfma_kernel<ACT, float, 64><<<grid, kMfmaThreads, 0, s>>>(p);
+  else mfma_kernel<ACT, float, 128><<<grid, kMfmaThreads, 0, s>>>(p);
+  return hipGetLastError();
 }
 
 

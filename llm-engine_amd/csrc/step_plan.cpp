@@ -16,8 +16,8 @@
 // rows of a longer slice (a prefill chunk) are cut into tiles of chunk_q_tile
 // consecutive positions; each tile's keys 0..last position are cut into
 // partitions of ~chunk_partition_tokens, one ChunkItem each, run on MFMA.
-// With an fp32 cache, chunk rows are decode rows (exact fp32 arithmetic on the
-// vector ALUs). Split rows of either kind are merged inside their launch by
+// With an fp32 cache, chunk rows are decode rows (exact fp32 products on the
+// fp32 MFMA). Split rows of either kind are merged inside their launch by
 // the last partition to finish.
 #include <hip/hip_runtime.h>
 
@@ -180,6 +180,16 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
       t += s.len;
     }
   }
+
+  // Longest work first: workgroups start over a couple of microseconds in
+  // launch order, so the items on the critical path (most keys) go first.
+  // Merges do not depend on the order (partials are addressed by index).
+  std::stable_sort(dec.begin(), dec.end(), [](const le::DecodeItem& a, const le::DecodeItem& b) {
+    return a.blk_end - a.blk_begin > b.blk_end - b.blk_begin;
+  });
+  std::stable_sort(chk.begin(), chk.end(), [](const le::ChunkItem& a, const le::ChunkItem& b) {
+    return a.blk_end - a.blk_begin > b.blk_end - b.blk_begin;
+  });
 
   // ---- layout: every array 256-byte aligned in one buffer ----
   le_step_plan P{};
