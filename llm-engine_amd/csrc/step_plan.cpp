@@ -31,9 +31,9 @@
 
 namespace {
 
-constexpr int kDefaultPartition = 1024;      // decode rows: smallest automatic partition
+constexpr int kDefaultPartition = 640;       // decode rows: smallest automatic partition
 constexpr int kMaxAutoPartition = 4096;      // decode rows: largest automatic partition
-constexpr int kPartitionQuantum = 256;       // 4 waves x 64-key tiles
+constexpr int kPartitionQuantum = 128;       // 4 waves x 32-key fp32 tiles
 constexpr int64_t kTargetItems = 256;        // workgroups per step the sizing aims for
 constexpr int kMaxMergeEntries = 1024;       // partitions x group the decode merge can stage
 constexpr int kDefaultChunkTile = 32;        // query rows per chunk item (two MFMA row tiles)
@@ -66,7 +66,8 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
     // round trips (block ids, then K/V; partial store, arrival counter, merge)
     // of several microseconds, so on MI355X a few long partitions stream
     // faster than many short ones (measured: 64 x 4096 rows, 2048-token
-    // partitions 4.1 TB/s, 256-token 2.2 TB/s).
+    // partitions 4.1 TB/s, 256-token 2.2 TB/s; config 2, 640-768 tokens
+    // 16.3 us, 1024 17.1 us, 512 18.0 us).
     int64_t ctx = 0;
     for (int i = 0; i < n_slices; i++)
       if (slices[i].len == 1 || cfg.kv_dtype != LE_BF16)
