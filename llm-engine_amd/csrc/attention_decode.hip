@@ -95,12 +95,16 @@ __device__ __forceinline__ Work resolve(const DecodeParams& p) {
 // position) before it loads anything from the cache: the scatter of
 // le_kv_cache_write (store_kv.cu:20-36) folded into the attention launch.
 // One thread per 8-element piece; the caller waits for the stores and
-// synchronises the workgroup before its first K/V load, so the row is read
-// back from the cache like every other key (no other workgroup reads its
-// lines in this launch).
+// synchronises the workgroup before any K/V load issued after it, so those
+// read the row back from the cache like every other key (no other workgroup
+// reads its lines in this launch). A first tile loaded before the store is
+// loaded again in that workgroup.
+__device__ __forceinline__ bool stores_new_row(const DecodeParams& p, const Work& w) {
+  return p.k_new != nullptr && (w.part < 0 || w.part == w.part_begin + w.n_parts - 1);
+}
 template <typename C>
 __device__ __forceinline__ void store_new_row(const DecodeParams& p, const Work& w, int kvh, int hd) {
-  if (p.k_new == nullptr || !(w.part < 0 || w.part == w.part_begin + w.n_parts - 1)) return;
+  if (!stores_new_row(p, w)) return;
   const int pieces = hd / 8;
   const int t = threadIdx.x;
   if (t >= 2 * pieces) return;
@@ -416,16 +420,26 @@ template <int HD> struct DecodeTile<bf16_t, HD> {
   static constexpr int kKeys = kTile;
   static constexpr int VT_BYTES = kKeys * kVStrideBf16<HD>;
   static constexpr bool kPipe = HD == 64;  // double-buffered where the registers allow it
+  static constexpr bool kEarly = HD == 64;  // first tile issued before the item is read (HD 128: too many registers)
   static constexpr int kLaneElems = 8;     // dims per lane group and k-step
   using Regs = TileRegs<HD / 32>;
   struct QOp { bf16x8 b[HD / 32]; };
   template <typename ACT>
   __device__ __forceinline__ static void load_q(QOp& q, const ACT* row, bool ok, int grp) {
+    // unconditional 16-byte loads (the row pointer is valid for every
+    // lane), selected afterwards: a load under a branch is waited for
+    // before the next one is issued
     const ACT* r = row + grp * 8;
+    constexpr int V = elem<ACT>::VEC;
+    float f[HD / 32][8];
 #pragma unroll
     for (int ks = 0; ks < HD / 32; ks++)
 #pragma unroll
-      for (int e = 0; e < 8; e++) q.b[ks][e] = static_cast<__bf16>(ok ? elem<ACT>::load1(r + ks * 32 + e) : 0.f);
+      for (int e = 0; e < 8; e += V) elem<ACT>::widen(ld16(r + ks * 32 + e), &f[ks][e]);
+#pragma unroll
+    for (int ks = 0; ks < HD / 32; ks++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) q.b[ks][e] = static_cast<__bf16>(ok ? f[ks][e] : 0.f);
   }
   __device__ __forceinline__ static const bf16_t* lane_base(const void* cache, int kvh, int grp) {
     return static_cast<const bf16_t*>(cache) + kvh * HD + grp * 8;
@@ -437,6 +451,27 @@ template <int HD> struct DecodeTile<bf16_t, HD> {
   __device__ __forceinline__ static void compute(WaveAcc<HD>& st, const Regs& r, const QOp& q, int key0, int key_end,
                                                  float scale_log2, char* vt, int col, int grp) {
     compute_tile<HD>(st, r, q.b, key0, key_end, scale_log2, vt, col, grp);
+  }
+  // The first tile, addressed without the item: key rel0 + 16i + col of the
+  // item reads block ids[rel >> bs_shift] (the plan pads ids with -1 past
+  // the item, so those keys read block 0 and are masked by the caller).
+  __device__ __forceinline__ static void load_direct(Regs& r, const bf16_t* kc, const bf16_t* vc, int rel0,
+                                                     const int32_t* ids, int n_ids, int bs_shift, int kv_stride,
+                                                     int64_t num_blocks, int col) {
+    constexpr int KS = HD / 32;
+    const int bs_mask = (1 << bs_shift) - 1;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int rel = rel0 + i * 16 + col;
+      const int bid = ids[min(rel >> bs_shift, n_ids - 1)];
+      r.ok[i] = bid >= 0 && bid < num_blocks;
+      const int64_t slot = (static_cast<int64_t>(r.ok[i] ? bid : 0) << bs_shift) + (rel & bs_mask);
+#pragma unroll
+      for (int ks = 0; ks < KS; ks++) {
+        r.k[i][ks] = ld16_stream(kc + slot * kv_stride + ks * 32);
+        r.v[i][ks] = ld16_stream(vc + slot * kv_stride + ks * 32);
+      }
+    }
   }
 };
 
@@ -457,6 +492,7 @@ template <int HD> struct DecodeTile<float, HD> {
   static constexpr int V_STRIDE = HD * 4 + 16;   // bytes per key row of the V tile
   static constexpr int VT_BYTES = kKeys * V_STRIDE;
   static constexpr bool kPipe = HD == 64;
+  static constexpr bool kEarly = false;  // measured slower: more registers for no gain
   struct Regs {
     float4 k[kSub][kPieces], v[kSub][kPieces];
     bool ok[kSub];
@@ -464,9 +500,13 @@ template <int HD> struct DecodeTile<float, HD> {
   struct QOp { float q[kLaneDims]; };
   template <typename ACT>
   __device__ __forceinline__ static void load_q(QOp& q, const ACT* row, bool ok, int grp) {
-    const ACT* r = row + grp * kLaneDims;
+    const ACT* r = row + grp * kLaneDims;  // unconditional vector loads, as in the bf16 tile
+    constexpr int V = elem<ACT>::VEC;
+    float f[kLaneDims];
 #pragma unroll
-    for (int j = 0; j < kLaneDims; j++) q.q[j] = ok ? elem<ACT>::load1(r + j) : 0.f;
+    for (int j = 0; j < kLaneDims; j += V) elem<ACT>::widen(ld16(r + j), &f[j]);
+#pragma unroll
+    for (int j = 0; j < kLaneDims; j++) q.q[j] = ok ? f[j] : 0.f;
   }
   __device__ __forceinline__ static const float* lane_base(const void* cache, int kvh, int grp) {
     return static_cast<const float*>(cache) + kvh * HD + grp * kLaneDims;
@@ -482,6 +522,25 @@ template <int HD> struct DecodeTile<float, HD> {
       const int bid = tab[(key >> bs_shift) - tab_base];
       r.ok[i] = bid >= 0;
       const int64_t slot = (static_cast<int64_t>(r.ok[i] ? bid : 0) << bs_shift) + (key & bs_mask);
+#pragma unroll
+      for (int c = 0; c < kPieces; c++) {
+        const uint4 kk = ld16_stream(kc + slot * kv_stride + c * 4);
+        const uint4 vv = ld16_stream(vc + slot * kv_stride + c * 4);
+        r.k[i][c] = make_float4(__uint_as_float(kk.x), __uint_as_float(kk.y), __uint_as_float(kk.z), __uint_as_float(kk.w));
+        r.v[i][c] = make_float4(__uint_as_float(vv.x), __uint_as_float(vv.y), __uint_as_float(vv.z), __uint_as_float(vv.w));
+      }
+    }
+  }
+  __device__ __forceinline__ static void load_direct(Regs& r, const float* kc, const float* vc, int rel0,
+                                                     const int32_t* ids, int n_ids, int bs_shift, int kv_stride,
+                                                     int64_t num_blocks, int col) {
+    const int bs_mask = (1 << bs_shift) - 1;
+#pragma unroll
+    for (int i = 0; i < kSub; i++) {
+      const int rel = rel0 + i * 16 + col;
+      const int bid = ids[min(rel >> bs_shift, n_ids - 1)];
+      r.ok[i] = bid >= 0 && bid < num_blocks;
+      const int64_t slot = (static_cast<int64_t>(r.ok[i] ? bid : 0) << bs_shift) + (rel & bs_mask);
 #pragma unroll
       for (int c = 0; c < kPieces; c++) {
         const uint4 kk = ld16_stream(kc + slot * kv_stride + c * 4);
@@ -577,17 +636,26 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_kernel(DecodeParams p) {
 
   PROBE_TS(0);
   // With a plan, the item's block ids sit at a fixed stride: fetch them now,
-  // in the same memory round trip as the item itself.
+  // in the same memory round trip as the item itself, and issue each wave's
+  // first tile straight from them: its addresses need no field of the item.
   const bool item_ids = p.items != nullptr && p.item_ids != nullptr && p.ids_stride <= kTabCap;
+  const bool early = T::kEarly && item_ids;
   constexpr int kIdsPerThread = kTabCap / kMfmaThreads;
   int pre_ids[kIdsPerThread];
+  const int32_t* ids_row = p.item_ids + static_cast<int64_t>(blockIdx.x) * p.ids_stride;
+  typename T::Regs ra;
   if (item_ids) {
-    const int32_t* ids = p.item_ids + static_cast<int64_t>(blockIdx.x) * p.ids_stride;
 #pragma unroll
     for (int u = 0; u < kIdsPerThread; u++) {
       const int i = threadIdx.x + u * kMfmaThreads;
-      pre_ids[u] = i < p.ids_stride ? ids[i] : -1;
+      pre_ids[u] = i < p.ids_stride ? ids_row[i] : -1;
     }
+  }
+  if (early) {
+    T::load_direct(ra, T::lane_base(p.k_cache, blockIdx.y, threadIdx.x >> 4 & 3),
+                   T::lane_base(p.v_cache, blockIdx.y, threadIdx.x >> 4 & 3), (threadIdx.x >> 6) * T::kKeys,
+                   ids_row, p.ids_stride, __builtin_ctz(p.block_size), p.kv_heads * HD, p.num_cache_blocks,
+                   threadIdx.x & 15);
   }
   const Work w = resolve(p);
   if (!w.valid) return;
@@ -638,18 +706,20 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_kernel(DecodeParams p) {
 
   const int bs_shift = __builtin_ctz(bs);  // block sizes are powers of two
   const int stride = kMfmaWaves * T::kKeys;
-  // The partition in segments of at most kTabCap blocks: each segment's block
-  // ids are staged in LDS (invalid ids as -1), then streamed tile by tile.
+  // The partition in segments of at most kTabCap blocks: each segment's
+  // block ids are staged in LDS (invalid ids as -1), then streamed. With a
+  // plan there is one segment, its ids already in registers and each wave's
+  // first tile already in flight.
   for (int sb0 = w.b_begin; sb0 < w.b_end; sb0 += kTabCap) {
     const int sb1 = min(w.b_end, sb0 + kTabCap);
-    __syncthreads();  // the previous segment's table is no longer read
-    if (item_ids) {  // one segment: the whole item (ids_stride <= kTabCap)
+    if (item_ids) {
 #pragma unroll
       for (int u = 0; u < kIdsPerThread; u++) {
         const int bid = pre_ids[u];
         tab[tid + u * kMfmaThreads] = (bid >= 0 && bid < p.num_cache_blocks) ? bid : -1;
       }
     } else {
+      __syncthreads();  // the previous segment's table is no longer read
       for (int i = tid; i < sb1 - sb0; i += kMfmaThreads) {
         const int bid = gtab[sb0 + i];
         tab[i] = (bid >= 0 && bid < p.num_cache_blocks) ? bid : -1;
@@ -661,8 +731,10 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_kernel(DecodeParams p) {
     const int key_end = min(sb1 << bs_shift, w.pos + 1);
     int key0 = (sb0 << bs_shift) + wave * T::kKeys;
     if (key0 >= key_end) continue;
-    typename T::Regs ra;
-    T::load(ra, kc, vc, key0, key_end, kv_stride, bs_shift, tab, sb0, col);
+    // the early first tile stands unless this workgroup stored the new row
+    // after issuing it
+    if (!early || stores_new_row(p, w))
+      T::load(ra, kc, vc, key0, key_end, kv_stride, bs_shift, tab, sb0, col);
     if constexpr (kPipe) {
       // The next tile's loads are issued unconditionally (clamped to valid
       // addresses past the end) so every path reaches each compute with the
