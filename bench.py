@@ -107,20 +107,26 @@ def cpu_baseline(ctx, q_len, kv_bf16: bool, budget_s: float):
                      seed=21, kv_bf16=kv_bf16)
     threads = oracle.threads_default()
     attn_bytes, _ = algorithmic_bytes(ctx, q_len, 2 if kv_bf16 else 4, 4)
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        oracle.paged_attention(case.q, case.k_cache, case.v_cache, case.tables, case.table_offset,
-                               case.token_seq, case.token_pos, Q_HEADS, KV_HEADS, HEAD_DIM, BS,
-                               case.scale, threads=threads)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
-    return {"value": round(attn_bytes * reps / el / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port",
+
+    def rate(n_threads, budget):
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            oracle.paged_attention(case.q, case.k_cache, case.v_cache, case.tables, case.table_offset,
+                                   case.token_seq, case.token_pos, Q_HEADS, KV_HEADS, HEAD_DIM, BS,
+                                   case.scale, threads=n_threads)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget:
+                return attn_bytes * reps / el / 1e9, reps, el
+
+    value, reps, el = rate(threads, budget_s)
+    one, reps1, el1 = rate(1, budget_s / 4)  # the same loop on one thread
+    return {"value": round(value, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port", "value_1_thread": round(one, 3),
             "sample": f"{reps} layer(s) of the same batch (one layer's attention, "
                       f"{'bf16' if kv_bf16 else 'fp32'} K/V), {el:.1f} s, oracle.c "
-                      f"(token, head) loop on {threads} threads"}
+                      f"(token, head) loop on {threads} threads; then {reps1} layer(s) "
+                      f"in {el1:.1f} s on 1 thread (value_1_thread)"}
 
 
 def e2e_run(arch, prompts, out_lens, pool_blocks, max_seqs=64, budget=512, arrivals_s=None,
