@@ -373,9 +373,13 @@ __device__ __forceinline__ void compute_tile(WaveAcc<HD>& st, const TileRegs<HD 
   for (int i = 0; i < 4; i++)
 #pragma unroll
     for (int ks = 0; ks < KS; ks++) {
-      const bool vlive = key0 + i * 16 + col < key_end && r.ok[i];
+      // a mask, not a select: a select becomes a branch, and the loads it
+      // skips count as outstanding at every later join (the loop head then
+      // waits for the next tile's loads too)
+      const uint32_t m = 0u - static_cast<uint32_t>(key0 + i * 16 + col < key_end && r.ok[i]);
+      const uint4 v = r.v[i][ks];
       *reinterpret_cast<uint4*>(vt + (i * 16 + col) * V_STRIDE + (ks * 32 + grp * 8) * 2) =
-          vlive ? r.v[i][ks] : make_uint4(0, 0, 0, 0);
+          make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
     }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -596,11 +600,14 @@ template <int HD> struct DecodeTile<float, HD> {
     // V rows into this wave's LDS tile (row-major); a dead key's row is zeros.
 #pragma unroll
     for (int i = 0; i < kSub; i++) {
-      const bool vlive = key0 + i * 16 + col < key_end && r.ok[i];
+      const uint32_t m = 0u - static_cast<uint32_t>(key0 + i * 16 + col < key_end && r.ok[i]);  // as above
 #pragma unroll
-      for (int c = 0; c < kPieces; c++)
+      for (int c = 0; c < kPieces; c++) {
+        const float4 v = r.v[i][c];
         *reinterpret_cast<float4*>(vt + (i * 16 + col) * V_STRIDE + (grp * kLaneDims + c * 4) * 4) =
-            vlive ? r.v[i][c] : make_float4(0.f, 0.f, 0.f, 0.f);
+            make_float4(__uint_as_float(__float_as_uint(v.x) & m), __uint_as_float(__float_as_uint(v.y) & m),
+                        __uint_as_float(__float_as_uint(v.z) & m), __uint_as_float(__float_as_uint(v.w) & m));
+      }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
