@@ -397,92 +397,60 @@ __global__ __launch_bounds__(kThreads) void chunk_kernel(ChunkParams p) {
 #endif
 
   // Every other partition incremented the counter after its partials were
-  // performed, so the coherent loads below see all of them. Merge weights of
-  // (row, head, partition) go to LDS (the K/V stage is dead), then each
-  // output 4-vector sums the partials in partition order.
+  // performed, so the coherent loads below see all of them. Each thread owns
+  // kMG output 8-vectors (a row, a head, 8 dims) and merges their partials
+  // itself, kMJ partitions per round of loads: the partition's (m, l) for the
+  // row and head, and its normalised output, requested together, then folded
+  // in partition order into a running (max, sum) with rescaling. With at
+  // most kMJ partitions the whole merge is one memory round trip, with no
+  // LDS phase or barrier.
   const int J = it.part_stride;
   const int base = it.part0 - it.part;
-  // (m, l) of every (row, head, partition) into LDS in one round of loads,
-  // then each (row, head) turns them into merge weights (the K/V stage is
-  // dead: the region is reused).
-  float2* mls = reinterpret_cast<float2*>(lds);                                   // [nq][G][J]
-  float* wts = reinterpret_cast<float*>(lds + sizeof(float2) * kRowsMax * kMaxG * kMaxSplit);  // [nq][G][J]
-  {
-    // all of this thread's pairs in flight at once (at most kMlPer of them)
-    constexpr int kMlPer = kRowsMax * kMaxG * kMaxSplit / kThreads;
-    const int n_ml = nq * G * J;
-    float2 mlv[kMlPer];
-#pragma unroll
-    for (int u = 0; u < kMlPer; u++) {
-      const int idx = min(tid + u * kThreads, n_ml - 1);
-      const int rg = idx / J, j = idx - rg * J;
-      const int r = rg / G, g = rg - r * G;
-      const int64_t rec = static_cast<int64_t>(base + r * J + j) * p.q_heads + kvh * G + g;
-      mlv[u] = make_float2(ld_dev(ml + rec * 2), ld_dev(ml + rec * 2 + 1));
-    }
-#pragma unroll
-    for (int u = 0; u < kMlPer; u++)
-      if (tid + u * kThreads < n_ml) mls[tid + u * kThreads] = mlv[u];
-  }
-  __syncthreads();
-#ifdef LE_CHUNK_MERGE_TS
-  CHUNK_TS(1);
-#endif
-  for (int idx = tid; idx < nq * G; idx += kThreads) {
-    float M = -FLT_MAX;
-    for (int j = 0; j < J; j++) M = fmaxf(M, mls[idx * J + j].x);
-    float Lsum = 0.f;
-    for (int j = 0; j < J; j++) {
-      const float w = exp2f(mls[idx * J + j].x - M);
-      Lsum += mls[idx * J + j].y * w;
-      wts[idx * J + j] = w;
-    }
-    // the partials are normalised: partition j weighs exp2(m_j - M) * l_j / L
-    const float inv = 1.f / Lsum;
-    for (int j = 0; j < J; j++) wts[idx * J + j] *= mls[idx * J + j].y * inv;
-  }
-  __syncthreads();
-#ifdef LE_CHUNK_MERGE_TS
-  CHUNK_TS(7);
-#endif
-  constexpr int kMG = 4, kMJ = HD == 64 ? 8 : 4;  // output 8-vectors x partitions loaded per round
+  constexpr int kMG = 4, kMJ = HD == 64 ? 6 : 3;  // output 8-vectors x partitions per round
   const int per_row = G * (HD / 8);
   const int n_out = nq * per_row;
   for (int o0 = tid; o0 < n_out; o0 += kMG * kThreads) {
-    float sum[kMG][8];
     int64_t rec_base[kMG];
-    int widx[kMG], d8[kMG];
+    int d8[kMG];
+    float M[kMG], L[kMG], sum[kMG][8];
 #pragma unroll
     for (int gi = 0; gi < kMG; gi++) {
-#pragma unroll
-      for (int e = 0; e < 8; e++) sum[gi][e] = 0.f;
       const int o = min(o0 + gi * kThreads, n_out - 1);
       const int r = o / per_row, rem = o - r * per_row;
       const int g = rem / (HD / 8);
       d8[gi] = rem - g * (HD / 8);
       rec_base[gi] = static_cast<int64_t>(base + r * J) * p.q_heads + kvh * G + g;
-      widx[gi] = (r * G + g) * J;
+      M[gi] = -FLT_MAX;
+      L[gi] = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; e++) sum[gi][e] = 0.f;
     }
     for (int j0 = 0; j0 < J; j0 += kMJ) {
       uint4 x[kMG][kMJ];
+      float mj[kMG][kMJ], lj[kMG][kMJ];
 #pragma unroll
       for (int gi = 0; gi < kMG; gi++)
 #pragma unroll
         for (int jj = 0; jj < kMJ; jj++) {
-          const int j = min(j0 + jj, J - 1);
-          const int64_t rec = rec_base[gi] + static_cast<int64_t>(j) * p.q_heads;
+          const int64_t rec = rec_base[gi] + static_cast<int64_t>(min(j0 + jj, J - 1)) * p.q_heads;
           x[gi][jj] = ld_coherent16u(acc_rsrc, static_cast<uint32_t>((rec * HD + d8[gi] * 8) * 2));
+          mj[gi][jj] = ld_dev(ml + rec * 2);
+          lj[gi][jj] = ld_dev(ml + rec * 2 + 1);
         }
 #pragma unroll
       for (int gi = 0; gi < kMG; gi++)
 #pragma unroll
         for (int jj = 0; jj < kMJ; jj++)
           if (j0 + jj < J) {
-            const float w = wts[widx[gi] + j0 + jj];
+            // partition j holds o_j / l_j (fp16); fold in l_j * o_j at weight exp2(m_j - max)
+            const float m_new = fmaxf(M[gi], mj[gi][jj]);
+            const float a = exp2f(M[gi] - m_new), w = exp2f(mj[gi][jj] - m_new) * lj[gi][jj];
+            M[gi] = m_new;
+            L[gi] = L[gi] * a + w;
             float f[8];
             unpack_half8(x[gi][jj], f);
 #pragma unroll
-            for (int e = 0; e < 8; e++) sum[gi][e] += w * f[e];
+            for (int e = 0; e < 8; e++) sum[gi][e] = sum[gi][e] * a + w * f[e];
           }
     }
 #pragma unroll
@@ -491,9 +459,11 @@ __global__ __launch_bounds__(kThreads) void chunk_kernel(ChunkParams p) {
       if (o < n_out) {
         const int r = o / per_row, rem = o - r * per_row;
         const int g = rem / (HD / 8);
-        ACT* out = static_cast<ACT*>(p.out) + (static_cast<int64_t>(tok0 + r) * p.q_heads + kvh * G + g) * HD + d8[gi] * 8;
-        store4<ACT>(out, f32x4{sum[gi][0], sum[gi][1], sum[gi][2], sum[gi][3]});
-        store4<ACT>(out + 4, f32x4{sum[gi][4], sum[gi][5], sum[gi][6], sum[gi][7]});
+        ACT* out = static_cast<ACT*>(p.out) + (static_cast<int64_t>(tok0 + r) * p.q_heads + kvh * G + g) * HD +
+                   d8[gi] * 8;
+        const float inv = 1.f / L[gi];
+        store4<ACT>(out, f32x4{sum[gi][0], sum[gi][1], sum[gi][2], sum[gi][3]} * inv);
+        store4<ACT>(out + 4, f32x4{sum[gi][4], sum[gi][5], sum[gi][6], sum[gi][7]} * inv);
       }
     }
   }
