@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 
 #include "le_internal.h"
@@ -228,27 +229,33 @@ int ragged_attention(const void* q, le_dtype act_dtype, const void* k_new, const
       d.slots = arr(plan->off_slots); d.num_slots = num_slots;
     }
   }
+  if (plan->n_chunk_items == 0)
+    return hip_status(le::attention_decode(d, act_dtype == LE_BF16, kv_dtype == LE_BF16, stream));
+
+  if (kv_dtype != LE_BF16) return LE_EINVAL;  // chunk items exist only for bf16 caches
+  le::ChunkParams c{};
+  c.q = q; c.k_cache = k_cache; c.v_cache = v_cache;
+  c.tables = d.tables; c.table_offset = d.table_offset; c.token_pos = d.token_pos;
+  c.out = out; c.parts = parts;
+  c.items = reinterpret_cast<const le::ChunkItem*>(dev + plan->off_chunk_items);
+  // chunk items' block ids follow the decode items' at the same stride
+  c.item_ids = d.item_ids + static_cast<int64_t>(plan->n_decode_items) * plan->decode_ids_stride;
+  c.ids_stride = plan->decode_ids_stride;
+  c.n_items = plan->n_chunk_items;
+  c.q_heads = cfg.q_heads; c.kv_heads = cfg.kv_heads; c.head_dim = cfg.head_dim;
+  c.block_size = cfg.block_size; c.scale_log2 = scale_log2;
+  c.num_cache_blocks = num_cache_blocks;
+  // A mixed step is one launch (chunk and decode workgroups in one grid);
+  // LE_RAGGED_TWO_LAUNCHES=1 runs the two kernels one after the other instead.
+  static const bool two_launches = [] {
+    const char* v = std::getenv("LE_RAGGED_TWO_LAUNCHES");
+    return v && v[0] == '1';
+  }();
+  if (plan->n_decode_items > 0 && !two_launches)
+    return hip_status(le::attention_ragged(d, c, act_dtype == LE_BF16, stream));
   e = le::attention_decode(d, act_dtype == LE_BF16, kv_dtype == LE_BF16, stream);
   if (e != hipSuccess) return hip_status(e);
-
-  if (plan->n_chunk_items > 0) {
-    if (kv_dtype != LE_BF16) return LE_EINVAL;
-    le::ChunkParams c{};
-    c.q = q; c.k_cache = k_cache; c.v_cache = v_cache;
-    c.tables = d.tables; c.table_offset = d.table_offset; c.token_pos = d.token_pos;
-    c.out = out; c.parts = parts;
-    c.items = reinterpret_cast<const le::ChunkItem*>(dev + plan->off_chunk_items);
-    // chunk items' block ids follow the decode items' at the same stride
-    c.item_ids = d.item_ids + static_cast<int64_t>(plan->n_decode_items) * plan->decode_ids_stride;
-    c.ids_stride = plan->decode_ids_stride;
-    c.n_items = plan->n_chunk_items;
-    c.q_heads = cfg.q_heads; c.kv_heads = cfg.kv_heads; c.head_dim = cfg.head_dim;
-    c.block_size = cfg.block_size; c.scale_log2 = scale_log2;
-    c.num_cache_blocks = num_cache_blocks;
-    e = le::attention_chunk(c, act_dtype == LE_BF16, stream);
-    if (e != hipSuccess) return hip_status(e);
-  }
-
+  e = le::attention_chunk(c, act_dtype == LE_BF16, stream);
   return hip_status(e);
 }
 

@@ -1,0 +1,487 @@
+#pragma once
+// Chunked-prefill attention on MFMA (hot-path part 3, prefill-chunk rows).
+//
+// Computes the same function as the decode kernel (and the oracle
+// ref::paged_attention_head, ops.h:87-111) for the rows of a prefill chunk:
+// row t at position pos[t] attends over keys 0..pos[t] of its sequence,
+// i.e. causal inside the chunk and over the whole cached prefix before it
+// (cpu_model.cpp:144-158 writes every token's K/V before attention runs).
+// The reference has no prefill kernel (attention_prefill.cu:1 is a stub) and
+// runs chunk rows through the decode kernel, re-reading the history once per
+// row; here 32 consecutive rows share every K/V read.
+//
+// gfx950 design:
+//   * one 512-thread workgroup (8 waves) per (32-row tile, kv head, key
+//     partition); wave w computes query head kv_head*G + w for all 32 rows
+//     (two 16-row MFMA tiles), so one LDS copy of the keys serves the whole
+//     GQA group and both row tiles;
+//   * a partition's keys are staged 256 at a time: every thread issues its
+//     16-byte K and V loads at once (block ids come from the plan, fetched in
+//     the same round trip as the item), so a stage costs one memory latency;
+//     K and V rows land row-major in LDS;
+//   * S^T = K . Q^T on v_mfma_f32_16x16x32_bf16 (A = 16 keys x 32 dims from
+//     LDS, B = Q^T in registers); the accumulator puts one query row per lane
+//     column, so the online-softmax statistics of a row live in that lane and
+//     P^T is already the B operand of O^T = V^T . P^T, whose A operand comes
+//     from the row-major V tile through the transposing LDS read
+//     (ds_read_b64_tr_b16) and is shared by both row tiles;
+//   * the k order inside an MFMA is only required to agree between A and B,
+//     so P^T's keys {16i + 4g + j} feed the product without any shuffle;
+//   * causal mask by absolute position: key kp is live for row t iff
+//     kp <= pos[t]; masked scores are -inf and the running max starts at
+//     -FLT_MAX, so fully masked tiles add zero;
+//   * a tile whose keys were split stores each partition's normalised output
+//     (fp16, bounded by max |v|) and its fp32 (max, sum) with device-coherent
+//     stores; the last partition to arrive (atomic counter per tile and kv
+//     head, reset by it) merges them in partition order, inside the launch.
+// bf16 operands, fp32 accumulation; fp32 caches never come here (their chunk
+// rows run on the decode kernel for exact fp32 arithmetic).
+#include <float.h>
+
+#include "le_common.h"
+#include "le_internal.h"
+
+namespace le {
+namespace chk {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * kWave;
+constexpr int kTileKeys = 64;    // keys per MFMA tile
+constexpr int kStageKeys = 256;  // keys staged in LDS at once
+constexpr int kRowsMax = 32;     // query rows per item
+constexpr int kMaxG = 8;         // query heads per kv head
+constexpr int kMaxSplit = 16;    // partitions of one tile the merge stages in LDS
+
+template <int HD> struct ChunkLds {
+  static constexpr int ROW = HD * 2 + 16;  // bytes per key row of K and of V (padded)
+  static constexpr int K_BYTES = kStageKeys * ROW;
+  static constexpr int BYTES = 2 * K_BYTES;  // K rows, then V rows
+};
+
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// ds_read_b64_tr_b16: in each group of 16 lanes, lane i receives 16-bit
+// element (i % 4) of the 8-byte chunks addressed by lanes 4j + i/4, j = 0..3.
+__device__ __forceinline__ bf16x4 lds_read_tr(const char* p) {
+  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) i16x4*)(p));
+  return __builtin_bit_cast(bf16x4, v);
+}
+
+__device__ __forceinline__ void st_dev(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float* p) {
+  return __uint_as_float(__hip_atomic_load(reinterpret_cast<uint32_t*>(const_cast<float*>(p)),
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+#ifdef LE_PROBE_TIMING
+// Diagnostic build only: per-workgroup phase timestamps (100 MHz counter).
+__device__ uint64_t g_chunk_ts[8192][8];
+#define CHUNK_TS(k) do { if (threadIdx.x == 0 && kvh == 0 && item < 8192) \
+    g_chunk_ts[item][k] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define CHUNK_TS(k) do {} while (0)
+#endif
+
+// fp16 (round to nearest even) transport of normalised partial outputs.
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ uint2 pack_half4(f32x4 v) {
+  const f16x4 h = {static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1]), static_cast<_Float16>(v[2]),
+                   static_cast<_Float16>(v[3])};
+  return __builtin_bit_cast(uint2, h);
+}
+__device__ __forceinline__ void unpack_half8(uint4 r, float* o) {
+  const f16x8 h = __builtin_bit_cast(f16x8, r);
+#pragma unroll
+  for (int e = 0; e < 8; e++) o[e] = static_cast<float>(h[e]);
+}
+
+template <typename ACT> __device__ __forceinline__ void store4(ACT* p, f32x4 v);
+template <> __device__ __forceinline__ void store4<float>(float* p, f32x4 v) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
+template <> __device__ __forceinline__ void store4<bf16_t>(bf16_t* p, f32x4 v) {
+  *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+}
+
+// LDS of one chunk workgroup.
+template <int HD> struct ChunkSmem {
+  __attribute__((aligned(16))) char lds[ChunkLds<HD>::BYTES];
+  int last;
+};
+
+// One chunk workgroup (kThreads threads): chunk item `item`, kv head `kvh`.
+// Shared by the chunk kernel and the fused ragged kernel.
+template <typename ACT, int HD>
+__device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm, int item, int kvh) {
+  using L = ChunkLds<HD>;
+  constexpr int KS = HD / 32;  // MFMA k-steps over head dims
+  constexpr int DT = HD / 16;  // 16-dim output tiles
+  constexpr int CPR = HD / 8;  // 16-byte pieces per K/V row
+  constexpr int PIECES = 2 * kStageKeys * CPR;
+  constexpr int PER = PIECES / kThreads;  // 16-byte loads per thread per stage
+  static_assert(PER * kThreads == PIECES && PER % 2 == 0, "staging split");
+  static_assert(kRowsMax * kMaxG * kMaxSplit * (sizeof(float2) + sizeof(float)) <= L::BYTES,
+                "merge weights fit in the stage's LDS");
+
+  char* lds = sm.lds;
+  int& last = sm.last;
+
+  CHUNK_TS(0);
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid >> 6;
+  const int col = lane & 15;  // query row of this lane within a 16-row tile
+  const int grp = lane >> 4;  // k-group of this lane
+  const ChunkItem it = p.items[item];
+  const int G = p.q_heads / p.kv_heads;
+  const bool computes = wave < G;
+  const int head = kvh * G + (computes ? wave : 0);
+  const int bs_shift = __builtin_ctz(p.block_size);  // block sizes are powers of two
+  const int bs_mask = p.block_size - 1;
+  const int nq = it.n_q;
+  const int tok0 = it.tok_begin;
+  const int kv_stride = p.kv_heads * HD;
+  const int key_begin = it.blk_begin << bs_shift;
+  const int n_keys_blk = (it.blk_end - it.blk_begin) << bs_shift;  // load range: whole blocks
+  // The item's block ids sit at a fixed stride in the plan, padded with -1:
+  // each thread reads the ids of its own keys there directly, so the K/V
+  // loads wait for one round trip and no barrier.
+  const int32_t* ids = p.item_ids + static_cast<int64_t>(item) * p.ids_stride;
+  const char* kbase = static_cast<const char*>(p.k_cache);
+  const char* vbase = static_cast<const char*>(p.v_cache);
+
+  // Stage staging: thread pieces k cover key (tid + k*kThreads) / CPR, 16-byte
+  // piece c of that key's K row and of its V row. Keys past the item (or in
+  // an invalid block) read a valid address and are stored as zeros: their
+  // scores are masked, and a zero V row keeps p * v finite.
+  uint4 kv[2][PER / 2];
+  bool okp[PER / 2];
+  int dst[PER / 2];
+  auto issue = [&](int rel0) {
+#pragma unroll
+    for (int k = 0; k < PER / 2; k++) {
+      const int piece = tid + k * kThreads;
+      const int key_l = piece / CPR, c = piece - key_l * CPR;
+      const int rel = rel0 + key_l;
+      const int bid = ids[min(rel >> bs_shift, p.ids_stride - 1)];
+      okp[k] = rel < n_keys_blk && bid >= 0 && bid < p.num_cache_blocks;
+      const int64_t slot = (static_cast<int64_t>(okp[k] ? bid : 0) << bs_shift) + (rel & bs_mask);
+      const int64_t off = (slot * kv_stride + kvh * HD + c * 8) * 2;
+      kv[0][k] = ld16_stream(kbase + off);
+      kv[1][k] = ld16_stream(vbase + off);
+      dst[k] = key_l * L::ROW + c * 16;
+    }
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int k = 0; k < PER / 2; k++) {
+      *reinterpret_cast<uint4*>(lds + dst[k]) = okp[k] ? kv[0][k] : make_uint4(0, 0, 0, 0);
+      *reinterpret_cast<uint4*>(lds + L::K_BYTES + dst[k]) = okp[k] ? kv[1][k] : make_uint4(0, 0, 0, 0);
+    }
+  };
+  // Query rows first (they are needed last, and a wait for them must not
+  // cover the K/V loads issued after them), then the stage's K/V.
+  const int pos0 = p.token_pos[tok0];  // the tile's rows are consecutive positions
+  uint4 qraw[2][KS][sizeof(ACT) / 2];  // 8 elements per k-step: 16 bytes (bf16) or 32 (fp32)
+#pragma unroll
+  for (int rs = 0; rs < 2; rs++) {
+    const int r = rs * 16 + col;
+    const bool ok = computes && r < nq;
+    const ACT* q = static_cast<const ACT*>(p.q) +
+                   (static_cast<int64_t>(tok0 + (ok ? r : 0)) * p.q_heads + head) * HD + grp * 8;
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+      for (int h = 0; h < static_cast<int>(sizeof(ACT) / 2); h++) qraw[rs][ks][h] = ld16(q + ks * 32 + h * (16 / sizeof(ACT)));
+  }
+  issue(0);
+  CHUNK_TS(1);
+  // Q^T operands: this lane's 8 dims per k-step of rows col and 16 + col.
+  bf16x8 qb[2][KS];
+#pragma unroll
+  for (int rs = 0; rs < 2; rs++) {
+    const bool ok = computes && rs * 16 + col < nq;
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+      float f[8];
+      if constexpr (sizeof(ACT) == 2) {
+        elem<bf16_t>::widen(qraw[rs][ks][0], f);
+      } else {
+        elem<float>::widen(qraw[rs][ks][0], f);
+        elem<float>::widen(qraw[rs][ks][1], f + 4);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; e++) qb[rs][ks][e] = static_cast<__bf16>(ok ? f[e] : 0.f);
+    }
+  }
+  CHUNK_TS(7);
+
+  f32x4 acc[2][DT];
+#pragma unroll
+  for (int rs = 0; rs < 2; rs++)
+#pragma unroll
+    for (int d = 0; d < DT; d++) acc[rs][d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run[2] = {-FLT_MAX, -FLT_MAX}, l_run[2] = {0.f, 0.f};
+
+  for (int rel0 = 0;;) {
+    stash();
+    __syncthreads();
+    CHUNK_TS(2);
+    const int s0 = key_begin + rel0;
+#ifdef LE_CHUNK_PROBE_NOCOMPUTE
+    if (computes && s0 < 0) {
+#else
+    if (computes) {
+#endif
+      const int key_end = min(key_begin + n_keys_blk, pos0 + nq);  // past the last row's position: dead
+#pragma unroll 1
+      for (int kt = 0; kt < kStageKeys / kTileKeys; kt++) {
+        const int t0 = s0 + kt * kTileKeys;
+        if (t0 >= key_end) break;
+        const char* kt_lds = lds + kt * kTileKeys * L::ROW;
+        const char* vt_lds = lds + L::K_BYTES + kt * kTileKeys * L::ROW;
+        // ---- S^T: 64 keys x 32 rows ----
+        f32x4 s[2][4];
+#pragma unroll
+        for (int rs = 0; rs < 2; rs++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) s[rs][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+          for (int ks = 0; ks < KS; ks++) {
+            const bf16x8 a =
+                *reinterpret_cast<const bf16x8*>(kt_lds + (i * 16 + col) * L::ROW + (ks * 32 + grp * 8) * 2);
+#pragma unroll
+            for (int rs = 0; rs < 2; rs++) s[rs][i] = mfma16(a, qb[rs][ks], s[rs][i]);
+          }
+        // ---- causal mask, online softmax per row (log2 domain) ----
+        // A tile wholly below the diagonal and inside the range needs no
+        // mask: every row's position is at least pos0. The max runs on raw
+        // scores (the scale is positive) and the scale enters once, in
+        // exp2(s * scale - m). Arguments of exp2 are <= 0, so the raw
+        // hardware exp2 (whose results below 2^-126 flush to zero) suffices.
+        const bool full = t0 + kTileKeys - 1 <= pos0 && t0 + kTileKeys <= key_end;
+#pragma unroll
+        for (int rs = 0; rs < 2; rs++) {
+          if (!full) {
+            const int r = rs * 16 + col;
+            const int qpos = r < nq ? pos0 + r : -1;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+              for (int j = 0; j < 4; j++) {
+                const int kp = t0 + i * 16 + grp * 4 + j;
+                if (!(kp <= qpos && kp < key_end)) s[rs][i][j] = -INFINITY;
+              }
+          }
+          float mt = -INFINITY;
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            mt = fmaxf(fmaxf(mt, fmaxf(s[rs][i][0], s[rs][i][1])), fmaxf(s[rs][i][2], s[rs][i][3]));
+          mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+          mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+          const float m_new = fmaxf(m_run[rs], mt * p.scale_log2);
+          const float alpha = __builtin_amdgcn_exp2f(m_run[rs] - m_new);
+          m_run[rs] = m_new;
+          float ls = 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              const float e = __builtin_amdgcn_exp2f(fmaf(s[rs][i][j], p.scale_log2, -m_new));
+              s[rs][i][j] = e;
+              ls += e;
+            }
+          l_run[rs] = l_run[rs] * alpha + ls;  // this lane group's share; groups merge at the end
+#pragma unroll
+          for (int d = 0; d < DT; d++) acc[rs][d] *= alpha;
+        }
+        // ---- O^T += V^T . P^T over the tile's 64 keys (2 k-steps of 32) ----
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++) {
+          bf16x8 pb[2];
+#pragma unroll
+          for (int rs = 0; rs < 2; rs++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              pb[rs][j] = static_cast<__bf16>(s[rs][2 * kk][j]);
+              pb[rs][4 + j] = static_cast<__bf16>(s[rs][2 * kk + 1][j]);
+            }
+          // lane (col, grp) addresses key row kk*32 + 4*grp + col/4 (then +16)
+          // at dims 16*d + 4*(col%4), and receives dim 16*d + col of four
+          // keys: the keys P^T holds for that group.
+          const char* r_lo = vt_lds + (kk * 32 + grp * 4 + (col >> 2)) * L::ROW + (col & 3) * 8;
+          const char* r_hi = r_lo + 16 * L::ROW;
+#pragma unroll
+          for (int d = 0; d < DT; d++) {
+            const bf16x4 lo = lds_read_tr(r_lo + d * 32);
+            const bf16x4 hi = lds_read_tr(r_hi + d * 32);
+            const bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+            for (int rs = 0; rs < 2; rs++) acc[rs][d] = mfma16(a, pb[rs], acc[rs][d]);
+          }
+        }
+      }
+    }
+    rel0 += kStageKeys;
+    CHUNK_TS(3);
+    if (rel0 >= n_keys_blk) break;
+    __syncthreads();  // the stage is no longer read
+    issue(rel0);
+  }
+
+  // acc[rs][d][j] = O[row rs*16 + col][dim d*16 + grp*4 + j]
+  float l_tot[2];
+#pragma unroll
+  for (int rs = 0; rs < 2; rs++) {
+    l_tot[rs] = l_run[rs] + __shfl_xor(l_run[rs], 16, kWave);
+    l_tot[rs] += __shfl_xor(l_tot[rs], 32, kWave);
+  }
+  if (it.part0 < 0) {
+    if (computes) {
+#pragma unroll
+      for (int rs = 0; rs < 2; rs++) {
+        const int r = rs * 16 + col;
+        if (r < nq) {
+          ACT* out = static_cast<ACT*>(p.out) + (static_cast<int64_t>(tok0 + r) * p.q_heads + head) * HD;
+          const float inv = 1.f / l_tot[rs];
+#pragma unroll
+          for (int d = 0; d < DT; d++) store4<ACT>(out + d * 16 + grp * 4, acc[rs][d] * inv);
+        }
+      }
+    }
+    return;
+  }
+
+  // ---- split tile: store the partial, then the last partition merges ----
+  const __amdgpu_buffer_rsrc_t acc_rsrc = coherent_rsrc(p.parts.acc);
+  float* ml = reinterpret_cast<float*>(p.parts.ml);
+  if (computes) {
+#pragma unroll
+    for (int rs = 0; rs < 2; rs++) {
+      const int r = rs * 16 + col;
+      if (r < nq) {
+        const int64_t rec = static_cast<int64_t>(it.part0 + r * it.part_stride) * p.q_heads + head;
+        // the partition's normalised output in fp16 (|o| <= max |v|; a row
+        // with no live key in the partition stores zeros and l = 0), in the
+        // first half of the record's fp32-sized slot: partition indices are
+        // shared with the decode rows, whose fp32 partials may be live in the
+        // same launch (the fused ragged kernel)
+        const float inv = l_tot[rs] > 0.f ? 1.f / l_tot[rs] : 0.f;
+#pragma unroll
+        for (int d = 0; d < DT; d++) {
+          const f32x4 o = acc[rs][d] * inv;
+          st_coherent8(acc_rsrc, static_cast<uint32_t>(rec * HD * 4 + (d * 16 + grp * 4) * 2), pack_half4(o));
+        }
+        if (grp == 0) {
+          st_dev(ml + rec * 2, m_run[rs]);
+          st_dev(ml + rec * 2 + 1, l_tot[rs]);
+        }
+      }
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are performed
+  __syncthreads();                // ... and every other thread's
+  CHUNK_TS(4);
+  int32_t* counter = p.parts.counters + static_cast<int64_t>(tok0) * p.kv_heads + kvh;
+  if (tid == 0)
+    last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == it.part_stride - 1;
+  __syncthreads();
+  CHUNK_TS(5);
+  if (!last) return;
+#ifdef LE_CHUNK_PROBE_NOMERGE
+  if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return;
+#endif
+
+  // Every other partition incremented the counter after its partials were
+  // performed, so the coherent loads below see all of them. Each thread owns
+  // kMG output 8-vectors (a row, a head, 8 dims) and merges their partials
+  // itself, kMJ partitions per round of loads: the partition's (m, l) for the
+  // row and head, and its normalised output, requested together, then folded
+  // in partition order into a running (max, sum) with rescaling. With at
+  // most kMJ partitions the whole merge is one memory round trip, with no
+  // LDS phase or barrier.
+  const int J = it.part_stride;
+  const int base = it.part0 - it.part;
+  constexpr int kMG = 4, kMJ = HD == 64 ? 6 : 3;  // output 8-vectors x partitions per round
+  const int per_row = G * (HD / 8);
+  const int n_out = nq * per_row;
+  for (int o0 = tid; o0 < n_out; o0 += kMG * kThreads) {
+    int64_t rec_base[kMG];
+    int d8[kMG];
+    float M[kMG], L[kMG], sum[kMG][8];
+#pragma unroll
+    for (int gi = 0; gi < kMG; gi++) {
+      const int o = min(o0 + gi * kThreads, n_out - 1);
+      const int r = o / per_row, rem = o - r * per_row;
+      const int g = rem / (HD / 8);
+      d8[gi] = rem - g * (HD / 8);
+      rec_base[gi] = static_cast<int64_t>(base + r * J) * p.q_heads + kvh * G + g;
+      M[gi] = -FLT_MAX;
+      L[gi] = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; e++) sum[gi][e] = 0.f;
+    }
+    for (int j0 = 0; j0 < J; j0 += kMJ) {
+      uint4 x[kMG][kMJ];
+      float mj[kMG][kMJ], lj[kMG][kMJ];
+#pragma unroll
+      for (int gi = 0; gi < kMG; gi++)
+#pragma unroll
+        for (int jj = 0; jj < kMJ; jj++) {
+          const int64_t rec = rec_base[gi] + static_cast<int64_t>(min(j0 + jj, J - 1)) * p.q_heads;
+          x[gi][jj] = ld_coherent16u(acc_rsrc, static_cast<uint32_t>(rec * HD * 4 + d8[gi] * 16));
+          mj[gi][jj] = ld_dev(ml + rec * 2);
+          lj[gi][jj] = ld_dev(ml + rec * 2 + 1);
+        }
+#pragma unroll
+      for (int gi = 0; gi < kMG; gi++)
+#pragma unroll
+        for (int jj = 0; jj < kMJ; jj++)
+          if (j0 + jj < J) {
+            // partition j holds o_j / l_j (fp16); fold in l_j * o_j at weight exp2(m_j - max)
+            const float m_new = fmaxf(M[gi], mj[gi][jj]);
+            const float a = exp2f(M[gi] - m_new), w = exp2f(mj[gi][jj] - m_new) * lj[gi][jj];
+            M[gi] = m_new;
+            L[gi] = L[gi] * a + w;
+            float f[8];
+            unpack_half8(x[gi][jj], f);
+#pragma unroll
+            for (int e = 0; e < 8; e++) sum[gi][e] = sum[gi][e] * a + w * f[e];
+          }
+    }
+#pragma unroll
+    for (int gi = 0; gi < kMG; gi++) {
+      const int o = o0 + gi * kThreads;
+      if (o < n_out) {
+        const int r = o / per_row, rem = o - r * per_row;
+        const int g = rem / (HD / 8);
+        ACT* out = static_cast<ACT*>(p.out) + (static_cast<int64_t>(tok0 + r) * p.q_heads + kvh * G + g) * HD +
+                   d8[gi] * 8;
+        const float inv = 1.f / L[gi];
+        store4<ACT>(out, f32x4{sum[gi][0], sum[gi][1], sum[gi][2], sum[gi][3]} * inv);
+        store4<ACT>(out + 4, f32x4{sum[gi][4], sum[gi][5], sum[gi][6], sum[gi][7]} * inv);
+      }
+    }
+  }
+  CHUNK_TS(6);
+  if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+}  // namespace
+}  // namespace chk
+}  // namespace le

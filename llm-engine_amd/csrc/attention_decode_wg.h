@@ -1,0 +1,829 @@
+#pragma once
+// Paged decode attention with GQA-group sharing and split-K (hot-path parts 3, 4).
+//
+// Computes, for each query row t and query head h (kv head = h / group):
+//     out[t][h] = softmax_p( q[t][h] . K[slot(p)][kvh] * scale ) . V[slot(p)][kvh],
+//     p in 0..pos[t],  slot(p) = table[p / bs] * bs + p % bs
+// Reference: launch_attention_decode_gqa (attention_decode_gqa.cu:87-232) and
+// the oracle ref::paged_attention_head (ops.h:87-111).
+//
+// gfx950 design. The reference runs one block per (token, kv head), which at
+// 64 rows x 2 kv heads leaves most of the chip idle; here every row's context
+// is cut into partitions and each (row, kv head, partition) is a 256-thread
+// workgroup. Each K/V element of a kv head is read from HBM once and serves
+// the whole GQA group.
+//
+//   mfma_kernel, templated on the cache element type. The G query heads of
+//     the group are the N = 16 columns of the MFMA: S^T = K . Q^T takes K rows
+//     straight from HBM into A-operand registers, so the score of a key for
+//     all G heads costs no vector-ALU work; the softmax runs on the 16 x 16
+//     accumulator (one head per lane column); V is staged in a wave-private
+//     LDS tile and O^T = V^T . P^T reuses the accumulator of P^T directly as
+//     the B operand (an MFMA only needs A and B to agree on the order of k
+//     inside a lane group). Each wave runs its own online softmax over its
+//     tiles; the four waves merge at the end.
+//       bf16 cache: 64-key tiles on v_mfma_f32_16x16x32_bf16, V^T read with
+//       the transposing ds_read_b64_tr_b16.
+//       fp32 cache: 32-key tiles on v_mfma_f32_16x16x4_f32 (exact fp32
+//       products), V^T read as single floats of the row-major tile.
+//
+// Split rows are merged inside the same launch: each partition writes its
+// unnormalised partial (acc, running max, sum), and the last workgroup of the
+// row to arrive (an atomic counter per (row, kv head), reset by that
+// workgroup) merges them and writes the output. No second kernel, no extra
+// launch gap. Masked positions carry -inf scores and running maxima start at
+// -FLT_MAX, so no path computes inf - inf (the reference's sentinel rule,
+// attention_decode.cu:81).
+#include <float.h>
+
+#include "le_common.h"
+#include "le_internal.h"
+
+namespace le {
+namespace dec {
+namespace {
+
+constexpr int kTile = 64;     // bf16 tiles: keys per wave tile
+constexpr int kMaxG = 16;     // heads per kv head the MFMA columns can hold
+constexpr int kMergeBatch = 8;       // partial accumulators loaded per batch in the merge
+constexpr int kMaxMergeEntries = 1024;  // n_parts * G the merge stages in LDS
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+#ifdef LE_PROBE_TIMING
+// Diagnostic build only: per-workgroup phase timestamps (100 MHz counter).
+__device__ uint64_t g_probe_ts[16384][8];
+#define PROBE_TS(k) do { if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 16384) \
+    g_probe_ts[blockIdx.x][k] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define PROBE_TS(k) do {} while (0)
+#endif
+
+struct Work {
+  int token, pos, table_off, b_begin, b_end, part, part_begin, n_parts;
+  bool valid;
+};
+
+// This workgroup's item; valid is false if it has nothing to do (a split past
+// the end of a short context in the reference-shaped launch). Returned by
+// value so it stays in registers.
+__device__ __forceinline__ Work resolve(const DecodeParams& p, int bx, int bz) {
+  if (p.items) {
+    const DecodeItem it = p.items[bx];
+    return Work{it.token, it.pos, it.table_off, it.blk_begin, it.blk_end,
+                it.part, it.part_begin, it.n_parts, true};
+  }
+  const int token = bx;
+  const int pos = p.token_pos[token];
+  const int nb = pos / p.block_size + 1;
+  const int ns = min(p.nsplit, nb);
+  const int split = bz;
+  const int b0 = static_cast<int>(static_cast<int64_t>(split) * nb / ns);
+  const int b1 = static_cast<int>(static_cast<int64_t>(split + 1) * nb / ns);
+  const int pb = token * p.nsplit;
+  return Work{token, pos, p.table_offset[p.token_seq[token]], b0, b1,
+              ns == 1 ? -1 : pb + split, pb, ns, split < ns};
+}
+
+// The new K/V row of a decode row, for kv head kvh, stored by the workgroup
+// of the row's last partition (the only one whose keys reach the row's own
+// position) before it loads anything from the cache: the scatter of
+// le_kv_cache_write (store_kv.cu:20-36) folded into the attention launch.
+// One thread per 8-element piece; the caller waits for the stores and
+// synchronises the workgroup before any K/V load issued after it, so those
+// read the row back from the cache like every other key (no other workgroup
+// reads its lines in this launch). A first tile loaded before the store is
+// loaded again in that workgroup.
+__device__ __forceinline__ bool stores_new_row(const DecodeParams& p, const Work& w) {
+  return p.k_new != nullptr && (w.part < 0 || w.part == w.part_begin + w.n_parts - 1);
+}
+template <typename C>
+__device__ __forceinline__ void store_new_row(const DecodeParams& p, const Work& w, int kvh, int hd) {
+  if (!stores_new_row(p, w)) return;
+  const int pieces = hd / 8;
+  const int t = threadIdx.x;
+  if (t >= 2 * pieces) return;
+  const int64_t slot = p.slots[w.token];
+  if (slot < 0 || slot >= p.num_slots) return;
+  const int which = t >= pieces;  // 0 = K, 1 = V
+  const int c = t - which * pieces;
+  const int64_t src = (static_cast<int64_t>(w.token) * p.kv_heads + kvh) * hd + c * 8;
+  const int64_t dst = (slot * p.kv_heads + kvh) * hd + c * 8;
+  float v[8];
+  if (p.new_bf16) {
+    elem<bf16_t>::widen(ld16(static_cast<const bf16_t*>(which ? p.v_new : p.k_new) + src), v);
+  } else {
+    const float* f = static_cast<const float*>(which ? p.v_new : p.k_new) + src;
+    elem<float>::widen(ld16(f), v);
+    elem<float>::widen(ld16(f + 4), v + 4);
+  }
+  C* out = static_cast<C*>(const_cast<void*>(which ? p.v_cache : p.k_cache)) + dst;
+  if constexpr (sizeof(C) == 2) {
+    *reinterpret_cast<uint4*>(out) = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                                pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
+  } else {
+    reinterpret_cast<float4*>(out)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4*>(out)[1] = make_float4(v[4], v[5], v[6], v[7]);
+  }
+}
+
+// Partials cross workgroups (and XCDs, whose L2s are not coherent with each
+// other) through device-coherent accesses: relaxed atomic stores and loads at
+// agent scope, which the hardware performs at the coherence point. This avoids
+// agent-scope fences, which would write back the whole L2 of the XCD.
+__device__ __forceinline__ void st_dev(float* p, float v) {
+  __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float* p) {
+  return __uint_as_float(__hip_atomic_load(reinterpret_cast<uint32_t*>(const_cast<float*>(p)),
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+// Final stage shared by both kernels. fin_acc[g * HD + d] holds the
+// workgroup's unnormalised output for head g of the group, fin_ml[g] its
+// (max, sum). Writes the output (single partition) or the partial, and in the
+// latter case the last arriving workgroup of the row merges all partials.
+template <typename ACT, int HD, int NTHR>
+__device__ __forceinline__ void finish(const DecodeParams& p, const Work& w, int G, int kvh,
+                                       const float* fin_acc, const float2* fin_ml,
+                                       float2* merge_ml, float2* merge_w, int* flag) {
+  const int tid = threadIdx.x;
+  const int64_t head0 = static_cast<int64_t>(w.token) * p.q_heads + kvh * G;
+  if (w.part < 0) {
+    for (int i = tid; i < G * HD; i += NTHR) {
+      const int g = i / HD;
+      elem<ACT>::store1(static_cast<ACT*>(p.out) + head0 * HD + i, fin_acc[i] / fin_ml[g].y);
+    }
+    return;
+  }
+  const int64_t rec0 = static_cast<int64_t>(w.part) * p.q_heads + kvh * G;
+  float* ml = reinterpret_cast<float*>(p.parts.ml);
+  for (int i = tid; i < G * HD; i += NTHR) st_dev(p.parts.acc + rec0 * HD + i, fin_acc[i]);
+  if (tid < G) {
+    st_dev(ml + (rec0 + tid) * 2, fin_ml[tid].x);
+    st_dev(ml + (rec0 + tid) * 2 + 1, fin_ml[tid].y);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are performed
+  __syncthreads();                // ... and every other thread's
+  PROBE_TS(4);
+  int32_t* counter = p.parts.counters + static_cast<int64_t>(w.token) * p.kv_heads + kvh;
+  if (tid == 0)
+    *flag = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            w.n_parts - 1;
+  __syncthreads();
+  PROBE_TS(5);
+  if (!*flag) return;
+  // Every other partition incremented the counter after its partial was
+  // performed, so the coherent loads below see all of them. The loads are
+  // issued in batches (all (m, l) pairs at once, then the accumulators
+  // kMergeBatch partitions at a time) so the merge costs a few memory
+  // latencies, not one per partition.
+  const int np = w.n_parts;
+  const int64_t rbase = static_cast<int64_t>(w.part_begin) * p.q_heads + kvh * G;
+  // Every (m, l) pair and every accumulator value is requested before any is
+  // used: one memory round trip for the whole merge (np <= kMergeBatch per
+  // batch of accumulators; more partitions take more batches).
+  for (int i = tid; i < np * G; i += NTHR) {
+    const int j = i / G, g = i - j * G;
+    const float* r = ml + (rbase + static_cast<int64_t>(j) * p.q_heads + g) * 2;
+    merge_w[i] = make_float2(ld_dev(r), ld_dev(r + 1));  // (m, l) of partition j, head g
+  }
+  constexpr int kOutPerThread = (kMaxG * HD + NTHR - 1) / NTHR;
+  float o[kOutPerThread];
+  float v0[kOutPerThread][kMergeBatch];
+#pragma unroll
+  for (int u = 0; u < kOutPerThread; u++) {
+    o[u] = 0.f;
+    const int i = min(tid + u * NTHR, G * HD - 1);
+#pragma unroll
+    for (int b = 0; b < kMergeBatch; b++) {
+      const int j = min(b, np - 1);
+      v0[u][b] = ld_dev(p.parts.acc + (rbase + static_cast<int64_t>(j) * p.q_heads) * HD + i);
+    }
+  }
+  __syncthreads();
+  if (tid < G) {
+    float M = -FLT_MAX;
+    for (int j = 0; j < np; j++) M = fmaxf(M, merge_w[j * G + tid].x);
+    float L = 0.f;
+    for (int j = 0; j < np; j++) L += merge_w[j * G + tid].y * exp2f(merge_w[j * G + tid].x - M);
+    merge_ml[tid] = make_float2(M, 1.f / L);
+  }
+  __syncthreads();
+  for (int i = tid; i < np * G; i += NTHR) {  // weights exp2(m_j - M) / L
+    const int g = i % G;
+    merge_w[i].x = exp2f(merge_w[i].x - merge_ml[g].x) * merge_ml[g].y;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < kOutPerThread; u++) {
+    const int i = tid + u * NTHR;
+    if (i >= G * HD) continue;
+    const int g = i / HD;
+#pragma unroll
+    for (int b = 0; b < kMergeBatch; b++)
+      if (b < np) o[u] += v0[u][b] * merge_w[b * G + g].x;
+    for (int j0 = kMergeBatch; j0 < np; j0 += kMergeBatch) {
+      float v[kMergeBatch];
+#pragma unroll
+      for (int b = 0; b < kMergeBatch; b++)
+        v[b] = ld_dev(p.parts.acc + (rbase + static_cast<int64_t>(min(j0 + b, np - 1)) * p.q_heads) * HD + i);
+#pragma unroll
+      for (int b = 0; b < kMergeBatch; b++)
+        if (j0 + b < np) o[u] += v[b] * merge_w[(j0 + b) * G + g].x;
+    }
+    elem<ACT>::store1(static_cast<ACT*>(p.out) + head0 * HD + i, o[u]);
+  }
+  PROBE_TS(6);
+  if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
+// bf16 cache: MFMA kernel
+// ---------------------------------------------------------------------------
+template <int HD, int VT_BYTES, int NW> struct MfmaLds {
+  static constexpr int RED_STRIDE = HD + 4;              // floats per head in the merge area
+  static constexpr int RED_BYTES = NW * kMaxG * RED_STRIDE * 4;
+  static constexpr int BYTES = (NW * VT_BYTES > RED_BYTES ? NW * VT_BYTES : RED_BYTES);
+};
+// bytes per key row of a wave's V tile: the row plus 16 bytes against bank conflicts
+template <int HD> constexpr int kVStrideBf16 = HD * 2 + 16;
+
+constexpr int kTabCap = 1024;  // block ids of a partition staged in LDS
+
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+// ds_read_b64_tr_b16: in each group of 16 lanes, lane i receives 16-bit
+// element (i % 4) of the 8-byte chunks addressed by lanes 4j + i/4, j = 0..3.
+__device__ __forceinline__ bf16x4 lds_read_tr(const char* p) {
+  // C-style cast: the generic LDS pointer becomes an address-space-3 pointer.
+  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) i16x4*)(p));
+  return __builtin_bit_cast(bf16x4, v);
+}
+
+// One wave's K/V registers for a 64-key tile: this lane's key of each of the
+// four 16-key subtiles, KS 16-byte chunks (8 dims) each.
+template <int KS> struct TileRegs {
+  uint4 k[4][KS], v[4][KS];
+  bool ok[4];  // the lane's block id of subtile i was a valid cache block
+};
+
+// State the wave carries across tiles.
+template <int HD> struct WaveAcc {
+  f32x4 acc[HD / 16];
+  float m, l;
+};
+
+// Issues the tile's 8 * KS 16-byte loads without any branch: a lane whose key
+// is past the end (or whose block id is invalid) reads a valid address of the
+// cache and is masked afterwards. Branches around loads would make the
+// compiler wait for all outstanding loads at every join, serialising them.
+// Block ids come from the LDS copy of the table (`tab`, indexed from the
+// segment's first block), never through a generic pointer: a flat load would
+// count against the global-load counter and stall behind the K/V loads.
+template <int HD>
+__device__ __forceinline__ void load_tile(TileRegs<HD / 32>& r, const bf16_t* kc, const bf16_t* vc,
+                                          int key0, int key_end, int kv_stride, int bs_shift,
+                                          const int* tab, int tab_base, int col) {
+  constexpr int KS = HD / 32;
+  const int bs_mask = (1 << bs_shift) - 1;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int key = min(key0 + i * 16 + col, key_end - 1);
+    const int bid = tab[(key >> bs_shift) - tab_base];
+    r.ok[i] = bid >= 0;  // the staging step marks invalid ids as -1
+    const int64_t slot = (static_cast<int64_t>(r.ok[i] ? bid : 0) << bs_shift) + (key & bs_mask);
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+      r.k[i][ks] = ld16_stream(kc + slot * kv_stride + ks * 32);
+      r.v[i][ks] = ld16_stream(vc + slot * kv_stride + ks * 32);
+    }
+  }
+}
+
+template <int HD>
+__device__ __forceinline__ void compute_tile(WaveAcc<HD>& st, const TileRegs<HD / 32>& r,
+                                             const bf16x8* qb, int key0, int key_end,
+                                             float scale_log2, char* vt, int col, int grp) {
+  constexpr int V_STRIDE = kVStrideBf16<HD>;
+  constexpr int KS = HD / 32;
+  constexpr int DT = HD / 16;
+#ifdef LE_PROBE_NOCOMPUTE
+  // Measurement variant: consume the loads, skip the attention arithmetic.
+  uint32_t x = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) x ^= r.k[i][ks].x ^ r.k[i][ks].w ^ r.v[i][ks].y ^ r.v[i][ks].z;
+  st.acc[0][0] += __uint_as_float(x & 0x3fffffff) * 1e-30f;
+  st.l += 1.f;
+  return;
+#endif
+  // S^T = K . Q^T: lane holds head `col`, keys key0 + 16i + 4grp + j
+  f32x4 s[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    s[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++)
+      s[i] = mfma16(__builtin_bit_cast(bf16x8, r.k[i][ks]), qb[ks], s[i]);
+  }
+  float mt = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int key = key0 + i * 16 + grp * 4 + j;
+      const float v = key < key_end ? s[i][j] * scale_log2 : -INFINITY;
+      s[i][j] = v;
+      mt = fmaxf(mt, v);
+    }
+  mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+  mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+  const float m_new = fmaxf(st.m, mt);
+  const float alpha = exp2f(st.m - m_new);
+  st.m = m_new;
+  float ls = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float e = exp2f(s[i][j] - m_new);
+      s[i][j] = e;
+      ls += e;
+    }
+  st.l = st.l * alpha + ls;
+#pragma unroll
+  for (int d = 0; d < DT; d++) st.acc[d] *= alpha;
+
+  // V rows into this wave's LDS tile, row-major (key rows), with 16-byte
+  // stores. A dead key's row is replaced by zeros (its p is 0, but the row
+  // read may hold NaNs).
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+      // a mask, not a select: a select becomes a branch, and the loads it
+      // skips count as outstanding at every later join (the loop head then
+      // waits for the next tile's loads too)
+      const uint32_t m = 0u - static_cast<uint32_t>(key0 + i * 16 + col < key_end && r.ok[i]);
+      const uint4 v = r.v[i][ks];
+      *reinterpret_cast<uint4*>(vt + (i * 16 + col) * V_STRIDE + (ks * 32 + grp * 8) * 2) =
+          make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
+    }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+  // O^T += V^T . P^T over the tile (2 k-steps of 32 keys). The A operand
+  // (16 dims x 8 keys per lane group) comes from the row-major tile through
+  // the transposing LDS read: lane (col, grp) addresses key row
+  // kk*32 + 4*grp + col/4 (then +16) at dims 16*d + 4*(col%4) and receives
+  // dim 16*d + col of four keys, the same keys P^T holds for that group.
+#pragma unroll
+  for (int kk = 0; kk < 2; kk++) {
+    bf16x8 pb;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      pb[j] = static_cast<__bf16>(s[2 * kk][j]);
+      pb[4 + j] = static_cast<__bf16>(s[2 * kk + 1][j]);
+    }
+    const char* r_lo = vt + (kk * 32 + grp * 4 + (col >> 2)) * V_STRIDE + (col & 3) * 8;
+    const char* r_hi = r_lo + 16 * V_STRIDE;
+#pragma unroll
+    for (int d = 0; d < DT; d++) {
+      const bf16x4 lo = lds_read_tr(r_lo + d * 32);
+      const bf16x4 hi = lds_read_tr(r_hi + d * 32);
+      const bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      st.acc[d] = mfma16(a, pb, st.acc[d]);
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();  // the tile is read before the next one overwrites it
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Tile operations of the MFMA decode kernel, per cache element type. A tile is
+// one wave's kKeys consecutive keys; the kernel around it (item, block ids,
+// pipelining, cross-wave and cross-workgroup merge) is shared.
+template <typename KV, int HD> struct DecodeTile;
+
+// bf16 cache: 64-key tiles on v_mfma_f32_16x16x32_bf16 (load_tile,
+// compute_tile above).
+template <int HD> struct DecodeTile<bf16_t, HD> {
+  static constexpr int kKeys = kTile;
+  static constexpr int VT_BYTES = kKeys * kVStrideBf16<HD>;
+  static constexpr bool kPipe = HD == 64;  // double-buffered where the registers allow it
+  static constexpr bool kEarly = HD == 64;  // first tile issued before the item is read (HD 128: too many registers)
+  static constexpr int kLaneElems = 8;     // dims per lane group and k-step
+  using Regs = TileRegs<HD / 32>;
+  struct QOp { bf16x8 b[HD / 32]; };
+  template <typename ACT>
+  __device__ __forceinline__ static void load_q(QOp& q, const ACT* row, bool ok, int grp) {
+    // unconditional 16-byte loads (the row pointer is valid for every
+    // lane), selected afterwards: a load under a branch is waited for
+    // before the next one is issued
+    const ACT* r = row + grp * 8;
+    constexpr int V = elem<ACT>::VEC;
+    float f[HD / 32][8];
+#pragma unroll
+    for (int ks = 0; ks < HD / 32; ks++)
+#pragma unroll
+      for (int e = 0; e < 8; e += V) elem<ACT>::widen(ld16(r + ks * 32 + e), &f[ks][e]);
+#pragma unroll
+    for (int ks = 0; ks < HD / 32; ks++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) q.b[ks][e] = static_cast<__bf16>(ok ? f[ks][e] : 0.f);
+  }
+  __device__ __forceinline__ static const bf16_t* lane_base(const void* cache, int kvh, int grp) {
+    return static_cast<const bf16_t*>(cache) + kvh * HD + grp * 8;
+  }
+  __device__ __forceinline__ static void load(Regs& r, const bf16_t* kc, const bf16_t* vc, int key0, int key_end,
+                                              int kv_stride, int bs_shift, const int* tab, int tab_base, int col) {
+    load_tile<HD>(r, kc, vc, key0, key_end, kv_stride, bs_shift, tab, tab_base, col);
+  }
+  __device__ __forceinline__ static void compute(WaveAcc<HD>& st, const Regs& r, const QOp& q, int key0, int key_end,
+                                                 float scale_log2, char* vt, int col, int grp) {
+    compute_tile<HD>(st, r, q.b, key0, key_end, scale_log2, vt, col, grp);
+  }
+  // The first tile, addressed without the item: key rel0 + 16i + col of the
+  // item reads block ids[rel >> bs_shift] (the plan pads ids with -1 past
+  // the item, so those keys read block 0 and are masked by the caller).
+  __device__ __forceinline__ static void load_direct(Regs& r, const bf16_t* kc, const bf16_t* vc, int rel0,
+                                                     const int32_t* ids, int n_ids, int bs_shift, int kv_stride,
+                                                     int64_t num_blocks, int col) {
+    constexpr int KS = HD / 32;
+    const int bs_mask = (1 << bs_shift) - 1;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int rel = rel0 + i * 16 + col;
+      const int bid = ids[min(rel >> bs_shift, n_ids - 1)];
+      r.ok[i] = bid >= 0 && bid < num_blocks;
+      const int64_t slot = (static_cast<int64_t>(r.ok[i] ? bid : 0) << bs_shift) + (rel & bs_mask);
+#pragma unroll
+      for (int ks = 0; ks < KS; ks++) {
+        r.k[i][ks] = ld16_stream(kc + slot * kv_stride + ks * 32);
+        r.v[i][ks] = ld16_stream(vc + slot * kv_stride + ks * 32);
+      }
+    }
+  }
+};
+
+// fp32 cache: 32-key tiles on v_mfma_f32_16x16x4_f32, exact fp32 products.
+//   S^T = K . Q^T: lane (col, grp) holds key col of each 16-key subtile with
+//   its dims [grp*HD/4, (grp+1)*HD/4) (contiguous, 16-byte loads); k-step j
+//   takes dim grp*HD/4 + j from both K (A) and Q^T (B), so the sum over
+//   lane groups and steps covers every dim once.
+//   O^T += V^T . P^T: k-step j of the product covers keys
+//   16*(j/4) + 4*grp + j%4, which are exactly the scores the lane's S^T
+//   accumulators hold, so P^T needs no shuffle; the V^T operand reads
+//   single floats of the row-major V tile staged in LDS.
+template <int HD> struct DecodeTile<float, HD> {
+  static constexpr int kKeys = 32;
+  static constexpr int kSub = kKeys / 16;   // 16-key subtiles
+  static constexpr int kLaneDims = HD / 4;  // dims per lane per key
+  static constexpr int kPieces = kLaneDims / 4;  // 16-byte loads per lane per key
+  static constexpr int V_STRIDE = HD * 4 + 16;   // bytes per key row of the V tile
+  static constexpr int VT_BYTES = kKeys * V_STRIDE;
+  static constexpr bool kPipe = HD == 64;
+  static constexpr bool kEarly = false;  // measured slower: more registers for no gain
+  struct Regs {
+    float4 k[kSub][kPieces], v[kSub][kPieces];
+    bool ok[kSub];
+  };
+  struct QOp { float q[kLaneDims]; };
+  template <typename ACT>
+  __device__ __forceinline__ static void load_q(QOp& q, const ACT* row, bool ok, int grp) {
+    const ACT* r = row + grp * kLaneDims;  // unconditional vector loads, as in the bf16 tile
+    constexpr int V = elem<ACT>::VEC;
+    float f[kLaneDims];
+#pragma unroll
+    for (int j = 0; j < kLaneDims; j += V) elem<ACT>::widen(ld16(r + j), &f[j]);
+#pragma unroll
+    for (int j = 0; j < kLaneDims; j++) q.q[j] = ok ? f[j] : 0.f;
+  }
+  __device__ __forceinline__ static const float* lane_base(const void* cache, int kvh, int grp) {
+    return static_cast<const float*>(cache) + kvh * HD + grp * kLaneDims;
+  }
+  // Branch-free like the bf16 tile: a lane whose key is past the end (or in
+  // an invalid block) reads a valid address and is masked afterwards.
+  __device__ __forceinline__ static void load(Regs& r, const float* kc, const float* vc, int key0, int key_end,
+                                              int kv_stride, int bs_shift, const int* tab, int tab_base, int col) {
+    const int bs_mask = (1 << bs_shift) - 1;
+#pragma unroll
+    for (int i = 0; i < kSub; i++) {
+      const int key = min(key0 + i * 16 + col, key_end - 1);
+      const int bid = tab[(key >> bs_shift) - tab_base];
+      r.ok[i] = bid >= 0;
+      const int64_t slot = (static_cast<int64_t>(r.ok[i] ? bid : 0) << bs_shift) + (key & bs_mask);
+#pragma unroll
+      for (int c = 0; c < kPieces; c++) {
+        const uint4 kk = ld16_stream(kc + slot * kv_stride + c * 4);
+        const uint4 vv = ld16_stream(vc + slot * kv_stride + c * 4);
+        r.k[i][c] = make_float4(__uint_as_float(kk.x), __uint_as_float(kk.y), __uint_as_float(kk.z), __uint_as_float(kk.w));
+        r.v[i][c] = make_float4(__uint_as_float(vv.x), __uint_as_float(vv.y), __uint_as_float(vv.z), __uint_as_float(vv.w));
+      }
+    }
+  }
+  __device__ __forceinline__ static void load_direct(Regs& r, const float* kc, const float* vc, int rel0,
+                                                     const int32_t* ids, int n_ids, int bs_shift, int kv_stride,
+                                                     int64_t num_blocks, int col) {
+    const int bs_mask = (1 << bs_shift) - 1;
+#pragma unroll
+    for (int i = 0; i < kSub; i++) {
+      const int rel = rel0 + i * 16 + col;
+      const int bid = ids[min(rel >> bs_shift, n_ids - 1)];
+      r.ok[i] = bid >= 0 && bid < num_blocks;
+      const int64_t slot = (static_cast<int64_t>(r.ok[i] ? bid : 0) << bs_shift) + (rel & bs_mask);
+#pragma unroll
+      for (int c = 0; c < kPieces; c++) {
+        const uint4 kk = ld16_stream(kc + slot * kv_stride + c * 4);
+        const uint4 vv = ld16_stream(vc + slot * kv_stride + c * 4);
+        r.k[i][c] = make_float4(__uint_as_float(kk.x), __uint_as_float(kk.y), __uint_as_float(kk.z), __uint_as_float(kk.w));
+        r.v[i][c] = make_float4(__uint_as_float(vv.x), __uint_as_float(vv.y), __uint_as_float(vv.z), __uint_as_float(vv.w));
+      }
+    }
+  }
+  __device__ __forceinline__ static void compute(WaveAcc<HD>& st, const Regs& r, const QOp& q, int key0, int key_end,
+                                                 float scale_log2, char* vt, int col, int grp) {
+    constexpr int DT = HD / 16;
+    // ---- S^T: kSub subtiles of 16 keys x 16 heads ----
+    f32x4 s[kSub];
+#pragma unroll
+    for (int i = 0; i < kSub; i++) {
+      s[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < kPieces; c++) {
+        const float kv4[4] = {r.k[i][c].x, r.k[i][c].y, r.k[i][c].z, r.k[i][c].w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) s[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv4[e], q.q[c * 4 + e], s[i], 0, 0, 0);
+      }
+    }
+    float mt = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kSub; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int key = key0 + i * 16 + grp * 4 + j;
+        const float v = key < key_end ? s[i][j] * scale_log2 : -INFINITY;
+        s[i][j] = v;
+        mt = fmaxf(mt, v);
+      }
+    mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+    mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+    const float m_new = fmaxf(st.m, mt);
+    const float alpha = exp2f(st.m - m_new);
+    st.m = m_new;
+    float ls = 0.f;
+#pragma unroll
+    for (int i = 0; i < kSub; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float e = exp2f(s[i][j] - m_new);
+        s[i][j] = e;
+        ls += e;
+      }
+    st.l = st.l * alpha + ls;
+#pragma unroll
+    for (int d = 0; d < DT; d++) st.acc[d] *= alpha;
+
+    // V rows into this wave's LDS tile (row-major); a dead key's row is zeros.
+#pragma unroll
+    for (int i = 0; i < kSub; i++) {
+      const uint32_t m = 0u - static_cast<uint32_t>(key0 + i * 16 + col < key_end && r.ok[i]);  // as above
+#pragma unroll
+      for (int c = 0; c < kPieces; c++) {
+        const float4 v = r.v[i][c];
+        *reinterpret_cast<float4*>(vt + (i * 16 + col) * V_STRIDE + (grp * kLaneDims + c * 4) * 4) =
+            make_float4(__uint_as_float(__float_as_uint(v.x) & m), __uint_as_float(__float_as_uint(v.y) & m),
+                        __uint_as_float(__float_as_uint(v.z) & m), __uint_as_float(__float_as_uint(v.w) & m));
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- O^T += V^T . P^T: k-step j covers keys 16*(j/4) + 4*grp + j%4 ----
+#pragma unroll
+    for (int j = 0; j < kSub * 4; j++) {
+      const float pb = s[j >> 2][j & 3];
+      const float* vrow = reinterpret_cast<const float*>(vt + (16 * (j >> 2) + 4 * grp + (j & 3)) * V_STRIDE);
+#pragma unroll
+      for (int d = 0; d < DT; d++) st.acc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vrow[d * 16 + col], pb, st.acc[d], 0, 0, 0);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();  // the tile is read before the next one overwrites it
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+};
+
+// LDS of one decode workgroup of NW waves.
+template <typename KV, int HD, int NW> struct DecodeSmem {
+  using L = MfmaLds<HD, DecodeTile<KV, HD>::VT_BYTES, NW>;
+  __attribute__((aligned(16))) char lds[L::BYTES];
+  float fin_acc[kMaxG * HD];
+  float2 fin_ml[kMaxG];
+  float2 merge_ml[kMaxG];
+  float2 merge_w[kMaxMergeEntries];
+  int tab[kTabCap];
+  int flag;
+};
+
+// One decode workgroup of NW waves: item (or row) bx, kv head by, split bz
+// (the reference-shaped launch without a plan). Shared by the decode kernel
+// and the fused ragged kernel.
+template <typename ACT, typename KV, int HD, int NW>
+__device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, HD, NW>& sm, int bx, int by, int bz) {
+  using T = DecodeTile<KV, HD>;
+  using L = MfmaLds<HD, T::VT_BYTES, NW>;
+  constexpr int kMfmaWaves = NW;
+  constexpr int kMfmaThreads = NW * kWave;
+  constexpr int DT = HD / 16;  // 16-dim output tiles
+  constexpr bool kPipe = T::kPipe;
+  char* lds = sm.lds;
+  float* fin_acc = sm.fin_acc;
+  float2* fin_ml = sm.fin_ml;
+  float2* merge_ml = sm.merge_ml;
+  float2* merge_w = sm.merge_w;
+  int* tab = sm.tab;
+
+  PROBE_TS(0);
+  // With a plan, the item's block ids sit at a fixed stride: fetch them now,
+  // in the same memory round trip as the item itself, and issue each wave's
+  // first tile straight from them: its addresses need no field of the item.
+  const bool item_ids = p.items != nullptr && p.item_ids != nullptr && p.ids_stride <= kTabCap;
+  const bool early = T::kEarly && item_ids;
+  constexpr int kIdsPerThread = kTabCap / kMfmaThreads;
+  int pre_ids[kIdsPerThread];
+  const int32_t* ids_row = p.item_ids + static_cast<int64_t>(bx) * p.ids_stride;
+  typename T::Regs ra;
+  if (item_ids) {
+#pragma unroll
+    for (int u = 0; u < kIdsPerThread; u++) {
+      const int i = threadIdx.x + u * kMfmaThreads;
+      pre_ids[u] = i < p.ids_stride ? ids_row[i] : -1;
+    }
+  }
+  if (early) {
+    T::load_direct(ra, T::lane_base(p.k_cache, by, threadIdx.x >> 4 & 3),
+                   T::lane_base(p.v_cache, by, threadIdx.x >> 4 & 3), (threadIdx.x >> 6) * T::kKeys,
+                   ids_row, p.ids_stride, __builtin_ctz(p.block_size), p.kv_heads * HD, p.num_cache_blocks,
+                   threadIdx.x & 15);
+  }
+  const Work w = resolve(p, bx, bz);
+  if (!w.valid) return;
+#ifdef LE_PROBE_TIMING
+  if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 16384) {
+    g_probe_ts[blockIdx.x][4] = __builtin_amdgcn_s_memrealtime() + (w.token & 0) ;
+  }
+#endif
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid >> 6;
+  const int col = lane & 15;   // head of the group (B/C column); key row for A loads
+  const int grp = lane >> 4;   // k-group
+  const int kvh = by;
+  const int G = p.q_heads / p.kv_heads;
+  const int bs = p.block_size;
+  const int32_t* gtab = p.tables + w.table_off;
+  const int kv_stride = p.kv_heads * HD;
+  const KV* kc = T::lane_base(p.k_cache, kvh, grp);
+  const KV* vc = T::lane_base(p.v_cache, kvh, grp);
+  char* vt = lds + wave * T::VT_BYTES;
+  store_new_row<KV>(p, w, kvh, HD);
+
+  // Q^T (B operand): column `col` = head kvh*G + col.
+  typename T::QOp qb;
+  {
+    const bool ok = col < G;
+    T::template load_q<ACT>(qb, static_cast<const ACT*>(p.q) +
+                                    (static_cast<int64_t>(w.token) * p.q_heads + kvh * G + (ok ? col : 0)) * HD,
+                            ok, grp);
+  }
+
+  WaveAcc<HD> st;
+#pragma unroll
+  for (int d = 0; d < DT; d++) st.acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  st.m = -FLT_MAX;
+  st.l = 0.f;
+#ifdef LE_PROBE_TIMING
+  {
+    float qs = 0.f;
+    qs += static_cast<float>(reinterpret_cast<const float*>(&qb)[0]);
+    if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 16384)
+      g_probe_ts[blockIdx.x][5] = __builtin_amdgcn_s_memrealtime() + (qs == 12345.f);
+    if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 16384)
+      g_probe_ts[blockIdx.x][6] = __builtin_amdgcn_s_memrealtime() + (pre_ids[0] == 12345);
+  }
+#endif
+
+  const int bs_shift = __builtin_ctz(bs);  // block sizes are powers of two
+  const int stride = kMfmaWaves * T::kKeys;
+  // The partition in segments of at most kTabCap blocks: each segment's
+  // block ids are staged in LDS (invalid ids as -1), then streamed. With a
+  // plan there is one segment, its ids already in registers and each wave's
+  // first tile already in flight.
+  for (int sb0 = w.b_begin; sb0 < w.b_end; sb0 += kTabCap) {
+    const int sb1 = min(w.b_end, sb0 + kTabCap);
+    if (item_ids) {
+#pragma unroll
+      for (int u = 0; u < kIdsPerThread; u++) {
+        const int bid = pre_ids[u];
+        tab[tid + u * kMfmaThreads] = (bid >= 0 && bid < p.num_cache_blocks) ? bid : -1;
+      }
+    } else {
+      __syncthreads();  // the previous segment's table is no longer read
+      for (int i = tid; i < sb1 - sb0; i += kMfmaThreads) {
+        const int bid = gtab[sb0 + i];
+        tab[i] = (bid >= 0 && bid < p.num_cache_blocks) ? bid : -1;
+      }
+    }
+    if (p.k_new != nullptr) __builtin_amdgcn_s_waitcnt(0);  // the new row is stored
+    __syncthreads();
+    PROBE_TS(1);
+    const int key_end = min(sb1 << bs_shift, w.pos + 1);
+    int key0 = (sb0 << bs_shift) + wave * T::kKeys;
+    if (key0 >= key_end) continue;
+    // the early first tile stands unless this workgroup stored the new row
+    // after issuing it
+    if (!early || stores_new_row(p, w))
+      T::load(ra, kc, vc, key0, key_end, kv_stride, bs_shift, tab, sb0, col);
+    if constexpr (kPipe) {
+      // The next tile's loads are issued unconditionally (clamped to valid
+      // addresses past the end) so every path reaches each compute with the
+      // same loads outstanding and the wait before it covers only the tile
+      // being computed.
+      typename T::Regs rb;
+      while (true) {
+        T::load(rb, kc, vc, key0 + stride, key_end, kv_stride, bs_shift, tab, sb0, col);
+        T::compute(st, ra, qb, key0, key_end, p.scale_log2, vt, col, grp);
+        if (key0 + stride >= key_end) break;
+        T::load(ra, kc, vc, key0 + 2 * stride, key_end, kv_stride, bs_shift, tab, sb0, col);
+        T::compute(st, rb, qb, key0 + stride, key_end, p.scale_log2, vt, col, grp);
+        if (key0 + 2 * stride >= key_end) break;
+        key0 += 2 * stride;
+      }
+    } else {
+      while (true) {
+        T::compute(st, ra, qb, key0, key_end, p.scale_log2, vt, col, grp);
+        key0 += stride;
+        if (key0 >= key_end) break;
+        T::load(ra, kc, vc, key0, key_end, kv_stride, bs_shift, tab, sb0, col);
+      }
+    }
+  }
+
+  PROBE_TS(2);
+  // ---- merge the four waves ----
+  float l_tot = st.l + __shfl_xor(st.l, 16, kWave);
+  l_tot += __shfl_xor(l_tot, 32, kWave);
+  __syncthreads();  // V^T tiles are dead; reuse the LDS for the merge
+  float* red = reinterpret_cast<float*>(lds);  // [wave][head][HD + 4]: acc..., m, l
+  if (col < G) {
+    float* r = red + (wave * kMaxG + col) * L::RED_STRIDE;
+#pragma unroll
+    for (int d = 0; d < DT; d++)
+      *reinterpret_cast<float4*>(r + d * 16 + grp * 4) =
+          make_float4(st.acc[d][0], st.acc[d][1], st.acc[d][2], st.acc[d][3]);
+    if (grp == 0) { r[HD] = st.m; r[HD + 1] = l_tot; }
+  }
+  __syncthreads();
+  if (tid < G) {
+    float M = -FLT_MAX;
+#pragma unroll
+    for (int v = 0; v < kMfmaWaves; v++) M = fmaxf(M, red[(v * kMaxG + tid) * L::RED_STRIDE + HD]);
+    float Ls = 0.f;
+#pragma unroll
+    for (int v = 0; v < kMfmaWaves; v++) {
+      const float* r = red + (v * kMaxG + tid) * L::RED_STRIDE;
+      Ls += r[HD + 1] * exp2f(r[HD] - M);
+    }
+    fin_ml[tid] = make_float2(M, Ls);
+  }
+  __syncthreads();
+  for (int i = tid; i < G * HD; i += kMfmaThreads) {
+    const int g = i / HD, d = i - g * HD;
+    const float M = fin_ml[g].x;
+    float o = 0.f;
+#pragma unroll
+    for (int v = 0; v < kMfmaWaves; v++) {
+      const float* r = red + (v * kMaxG + g) * L::RED_STRIDE;
+      o += r[d] * exp2f(r[HD] - M);
+    }
+    fin_acc[i] = o;
+  }
+  __syncthreads();
+  PROBE_TS(3);
+  finish<ACT, HD, kMfmaThreads>(p, w, G, kvh, fin_acc, fin_ml, merge_ml, merge_w, &sm.flag);
+  PROBE_TS(7);
+}
+}  // namespace
+}  // namespace dec
+}  // namespace le

@@ -1,0 +1,63 @@
+// Ragged paged attention of a mixed step in one launch (hot-path part 3):
+// the step's prefill-chunk rows (chunk_wg, attention_chunk_wg.h) and decode
+// rows (decode_wg, attention_decode_wg.h) as workgroups of one grid.
+//
+// With two launches the chunk rows' latency-bound phases (stage, compute,
+// partial store, merge) and the decode rows' HBM streaming run one after the
+// other, with a launch gap between them. In one grid the decode workgroups
+// stream on the CUs the chunk workgroups leave free, and start on the others
+// as chunk workgroups retire. Chunk workgroups come first in the grid: theirs
+// is the longer dependent chain (a split tile's merge waits for its last
+// partition).
+//
+// Both kinds keep their own merges inside the launch: partition indices and
+// arrival counters are disjoint between them (the plan numbers partitions
+// across both lists; counters are indexed by a row's or tile's first token).
+// Workgroups are 512 threads (the chunk workgroup's eight waves); the decode
+// workgroups run as eight waves as well. The LDS is the larger of the two.
+#include "attention_chunk_wg.h"
+#include "attention_decode_wg.h"
+
+namespace le {
+namespace {
+
+constexpr int kRaggedThreads = chk::kThreads;
+constexpr int kDecodeWaves = kRaggedThreads / kWave;
+
+template <int HD> union RaggedSmem {
+  chk::ChunkSmem<HD> c;
+  dec::DecodeSmem<bf16_t, HD, kDecodeWaves> d;
+};
+
+template <typename ACT, int HD>
+__global__ __launch_bounds__(kRaggedThreads) void ragged_kernel(DecodeParams dp, ChunkParams cp) {
+  __shared__ RaggedSmem<HD> sm;
+  const int n_chunk_wg = cp.n_items * cp.kv_heads;
+  const int b = blockIdx.x;
+  if (b < n_chunk_wg) {
+    chk::chunk_wg<ACT, HD>(cp, sm.c, b / cp.kv_heads, b % cp.kv_heads);
+  } else {
+    const int d = b - n_chunk_wg;
+    dec::decode_wg<ACT, bf16_t, HD, kDecodeWaves>(dp, sm.d, d / dp.kv_heads, d % dp.kv_heads, 0);
+  }
+}
+
+}  // namespace
+
+hipError_t attention_ragged(const DecodeParams& d, const ChunkParams& c, int act_bf16, hipStream_t s) {
+  const int64_t n = static_cast<int64_t>(c.n_items + d.n_rows) * c.kv_heads;
+  if (n <= 0) return hipSuccess;
+  if (n > 0x7fffffff || d.kv_heads != c.kv_heads || d.head_dim != c.head_dim || !d.items)
+    return hipErrorInvalidValue;
+  const dim3 grid(static_cast<unsigned>(n));
+  if (c.head_dim == 64) {
+    if (act_bf16) ragged_kernel<bf16_t, 64><<<grid, kRaggedThreads, 0, s>>>(d, c);
+    else ragged_kernel<float, 64><<<grid, kRaggedThreads, 0, s>>>(d, c);
+  } else {
+    if (act_bf16) ragged_kernel<bf16_t, 128><<<grid, kRaggedThreads, 0, s>>>(d, c);
+    else ragged_kernel<float, 128><<<grid, kRaggedThreads, 0, s>>>(d, c);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace le

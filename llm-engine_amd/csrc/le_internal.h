@@ -98,6 +98,10 @@ struct ChunkParams {
 
 hipError_t attention_chunk(const ChunkParams& p, int act_bf16, hipStream_t stream);
 
+// A mixed step's chunk rows and decode rows (bf16 cache, plan items) in one
+// launch: chunk workgroups first, then decode workgroups.
+hipError_t attention_ragged(const DecodeParams& d, const ChunkParams& c, int act_bf16, hipStream_t stream);
+
 // Split count for the reference-shaped entry point, where the host does not
 // know the context lengths: enough workgroups to cover the chip several times.
 int decode_nsplit(int n_tokens, int kv_heads);
