@@ -330,9 +330,10 @@ def main():
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": measured_traffic(args.workload, args.kv) if args.partition == 0 else None,
-                "kernel": "le_ragged_paged_attention (decode_kernel"
-                          + (" + chunk_kernel" if P.n_chunk_items else "")
-                          + (" + combine_kernel" if P.n_combine_items else "") + ")",
+                "kernel": "le_ragged_paged_attention ("
+                          + ("ragged_kernel: chunk and decode workgroups in one launch"
+                             if P.n_chunk_items and P.n_decode_items else
+                             "chunk_kernel" if P.n_chunk_items else "decode mfma_kernel") + ")",
                 "bytes_per_launch": attn_b, "us_per_launch": round(attn_us, 3)}
     if args.workload == "config3":
         fl = chunk_flops(ctx, q_len)
