@@ -781,6 +781,11 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
   }
 
   PROBE_TS(2);
+#ifdef LE_PROBE_NOFINISH
+  // Measurement variant: stream the tiles, skip the merges (output unwritten).
+  if (st.l == 12345.f) static_cast<float*>(p.out)[0] = st.acc[0][0];
+  return;
+#endif
   // ---- merge the four waves ----
   float l_tot = st.l + __shfl_xor(st.l, 16, kWave);
   l_tot += __shfl_xor(l_tot, 32, kWave);

@@ -34,7 +34,7 @@ namespace {
 constexpr int kDefaultPartition = 640;       // decode rows: smallest automatic partition
 constexpr int kMaxAutoPartition = 4096;      // decode rows: largest automatic partition
 constexpr int kPartitionQuantum = 128;       // 4 waves x 32-key fp32 tiles
-constexpr int64_t kTargetItems = 256;        // workgroups per step the sizing aims for
+constexpr int64_t kTargetItems = 512;        // workgroups per step the sizing aims for (two per CU)
 constexpr int kMaxMergeEntries = 1024;       // partitions x group the decode merge can stage
 constexpr int kDefaultChunkTile = 32;        // query rows per chunk item (two MFMA row tiles)
 constexpr int kDefaultChunkPartition = 256;  // keys per chunk item: one LDS stage
