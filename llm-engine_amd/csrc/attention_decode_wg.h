@@ -800,29 +800,23 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
     if (grp == 0) { r[HD] = st.m; r[HD + 1] = l_tot; }
   }
   __syncthreads();
-  if (tid < G) {
-    float M = -FLT_MAX;
-#pragma unroll
-    for (int v = 0; v < kMfmaWaves; v++) M = fmaxf(M, red[(v * kMaxG + tid) * L::RED_STRIDE + HD]);
-    float Ls = 0.f;
-#pragma unroll
-    for (int v = 0; v < kMfmaWaves; v++) {
-      const float* r = red + (v * kMaxG + tid) * L::RED_STRIDE;
-      Ls += r[HD + 1] * exp2f(r[HD] - M);
-    }
-    fin_ml[tid] = make_float2(M, Ls);
-  }
-  __syncthreads();
+  // each output element folds the waves' (m, l) itself: no separate phase
+  // (and barrier) for the per-head statistics
   for (int i = tid; i < G * HD; i += kMfmaThreads) {
     const int g = i / HD, d = i - g * HD;
-    const float M = fin_ml[g].x;
-    float o = 0.f;
+    float M = -FLT_MAX;
+#pragma unroll
+    for (int v = 0; v < kMfmaWaves; v++) M = fmaxf(M, red[(v * kMaxG + g) * L::RED_STRIDE + HD]);
+    float o = 0.f, Ls = 0.f;
 #pragma unroll
     for (int v = 0; v < kMfmaWaves; v++) {
       const float* r = red + (v * kMaxG + g) * L::RED_STRIDE;
-      o += r[d] * exp2f(r[HD] - M);
+      const float e = exp2f(r[HD] - M);
+      o += r[d] * e;
+      Ls += r[HD + 1] * e;
     }
     fin_acc[i] = o;
+    if (d == 0) fin_ml[g] = make_float2(M, Ls);
   }
   __syncthreads();
   PROBE_TS(3);
