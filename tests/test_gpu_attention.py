@@ -204,14 +204,17 @@ def test_chunk_rows_other_shapes(gpu, q_heads, kv_heads, head_dim):
 
 @pytest.mark.parametrize("block_size", [8, 32, 64])
 def test_chunk_rows_block_sizes(gpu, block_size):
-    ctx = [600, 129, 64]
-    q_len = [100, 129, 3]
-    case = make_case(ctx, q_len=q_len, block_size=block_size, num_blocks=256, seed=43, kv_bf16=True)
-    got, qh, plan = run_ragged(case, torch.bfloat16, gpu)
+    """Chunk rows and decode rows (one long enough to be split) in one step, so
+    in one launch, at block sizes other than 16."""
+    ctx = [600, 129, 64, 2000, 37]
+    q_len = [100, 129, 3, 1, 1]
+    case = make_case(ctx, q_len=q_len, block_size=block_size, num_blocks=512, seed=43, kv_bf16=True)
+    got, qh, plan = run_ragged(case, torch.bfloat16, gpu, partition_tokens=512)
     want = oracle_out(case, qh)
     err = max_abs(got, want)
-    print(f"chunk block {block_size}: items {plan.plan.n_chunk_items} max|err| {err:.3e}")
-    assert plan.plan.n_chunk_items > 0
+    print(f"chunk block {block_size}: items chunk {plan.plan.n_chunk_items} decode {plan.plan.n_decode_items} "
+          f"max|err| {err:.3e}")
+    assert plan.plan.n_chunk_items > 0 and plan.plan.n_decode_items > 2
     assert err < TOL_BF16_OUT
 
 
