@@ -247,10 +247,8 @@ int ragged_attention(const void* q, le_dtype act_dtype, const void* k_new, const
   c.num_cache_blocks = num_cache_blocks;
   // A mixed step is one launch (chunk and decode workgroups in one grid);
   // LE_RAGGED_TWO_LAUNCHES=1 runs the two kernels one after the other instead.
-  static const bool two_launches = [] {
-    const char* v = std::getenv("LE_RAGGED_TWO_LAUNCHES");
-    return v && v[0] == '1';
-  }();
+  const char* two = std::getenv("LE_RAGGED_TWO_LAUNCHES");  // read per call: tests switch it
+  const bool two_launches = two && two[0] == '1';
   if (plan->n_decode_items > 0 && !two_launches)
     return hip_status(le::attention_ragged(d, c, act_dtype == LE_BF16, stream));
   e = le::attention_decode(d, act_dtype == LE_BF16, kv_dtype == LE_BF16, stream);

@@ -154,6 +154,26 @@ def test_mixed_step_config3(gpu, act):
     assert err < tol_for(True, act)
 
 
+def test_mixed_step_two_launches(gpu, monkeypatch):
+    """A mixed step runs as one launch by default; LE_RAGGED_TWO_LAUNCHES=1
+    runs the chunk and decode kernels one after the other. Both against the
+    oracle, on a step with split decode rows and split chunk tiles."""
+    ctx = [900, 40, 2500, 1700, 300]
+    q_len = [300, 40, 1, 1, 1]
+    case = make_case(ctx, q_len=q_len, num_blocks=1024, seed=61, kv_bf16=True)
+    want = None
+    for two in ("0", "1"):
+        monkeypatch.setenv("LE_RAGGED_TWO_LAUNCHES", two)
+        got, qh, plan = run_ragged(case, torch.float32, gpu, partition_tokens=640)
+        if want is None:
+            want = oracle_out(case, qh)
+        err = max_abs(got, want)
+        print(f"two_launches={two}: chunk {plan.plan.n_chunk_items} decode {plan.plan.n_decode_items} "
+              f"parts {plan.plan.n_parts} max|err| {err:.3e}")
+        assert plan.plan.n_chunk_items > 0 and plan.plan.n_decode_items > 3
+        assert err < TOL_BF16
+
+
 def test_workspace_reused_across_plans(gpu):
     """One workspace serves steps of different shapes (as the engine uses it):
     a step with few rows and many split partials, then a larger mixed step
