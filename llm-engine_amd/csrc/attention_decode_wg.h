@@ -9,11 +9,12 @@
 //
 // gfx950 design. The reference runs one block per (token, kv head), which at
 // 64 rows x 2 kv heads leaves most of the chip idle; here every row's context
-// is cut into partitions and each (row, kv head, partition) is a 256-thread
-// workgroup. Each K/V element of a kv head is read from HBM once and serves
-// the whole GQA group.
+// is cut into partitions and each (row, kv head, partition) is a workgroup of
+// NW waves (decode_wg below: four in the decode kernel, attention_decode.hip;
+// eight in the fused ragged kernel, attention_ragged.hip). Each K/V element of
+// a kv head is read from HBM once and serves the whole GQA group.
 //
-//   mfma_kernel, templated on the cache element type. The G query heads of
+//   decode_wg, templated on the cache element type. The G query heads of
 //     the group are the N = 16 columns of the MFMA: S^T = K . Q^T takes K rows
 //     straight from HBM into A-operand registers, so the score of a key for
 //     all G heads costs no vector-ALU work; the softmax runs on the 16 x 16
