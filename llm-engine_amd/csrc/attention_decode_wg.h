@@ -22,7 +22,7 @@
 //     LDS tile and O^T = V^T . P^T reuses the accumulator of P^T directly as
 //     the B operand (an MFMA only needs A and B to agree on the order of k
 //     inside a lane group). Each wave runs its own online softmax over its
-//     tiles; the four waves merge at the end.
+//     tiles; the waves merge at the end.
 //       bf16 cache: 64-key tiles on v_mfma_f32_16x16x32_bf16, V^T read with
 //       the transposing ds_read_b64_tr_b16.
 //       fp32 cache: 32-key tiles on v_mfma_f32_16x16x4_f32 (exact fp32
