@@ -167,7 +167,9 @@ __device__ __forceinline__ void finish(const DecodeParams& p, const Work& w, int
     st_dev(ml + (rec0 + tid) * 2, fin_ml[tid].x);
     st_dev(ml + (rec0 + tid) * 2 + 1, fin_ml[tid].y);
   }
+#ifndef LE_PROBE_NOSTOREWAIT  // measurement variant: results may be stale
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are performed
+#endif
   __syncthreads();                // ... and every other thread's
   PROBE_TS(4);
   int32_t* counter = p.parts.counters + static_cast<int64_t>(w.token) * p.kv_heads + kvh;
@@ -821,6 +823,10 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
   }
   __syncthreads();
   PROBE_TS(3);
+#ifdef LE_PROBE_NOCROSS  // measurement variant: the four-wave merge only
+  if (fin_acc[tid] == 12345.f) static_cast<float*>(p.out)[0] = 0.f;
+  return;
+#endif
   finish<ACT, HD, kMfmaThreads>(p, w, G, kvh, fin_acc, fin_ml, merge_ml, merge_w, &sm.flag);
   PROBE_TS(7);
 }
