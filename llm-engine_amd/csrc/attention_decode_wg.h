@@ -47,7 +47,6 @@ namespace {
 constexpr int kTile = 64;     // bf16 tiles: keys per wave tile
 constexpr int kMaxG = 16;     // heads per kv head the MFMA columns can hold
 constexpr int kMergeBatch = 8;       // partial accumulators loaded per batch in the merge
-constexpr int kMaxMergeEntries = 1024;  // n_parts * G the merge stages in LDS
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
@@ -149,8 +148,7 @@ __device__ __forceinline__ float ld_dev(const float* p) {
 // latter case the last arriving workgroup of the row merges all partials.
 template <typename ACT, int HD, int NTHR>
 __device__ __forceinline__ void finish(const DecodeParams& p, const Work& w, int G, int kvh,
-                                       const float* fin_acc, const float2* fin_ml,
-                                       float2* merge_ml, float2* merge_w, int* flag) {
+                                       const float* fin_acc, const float2* fin_ml, int* flag) {
   const int tid = threadIdx.x;
   const int64_t head0 = static_cast<int64_t>(w.token) * p.q_heads + kvh * G;
   if (w.part < 0) {
@@ -160,9 +158,17 @@ __device__ __forceinline__ void finish(const DecodeParams& p, const Work& w, int
     }
     return;
   }
+  // The partial: the group's G records (head g of partition part is record
+  // part * q_heads + kvh * G + g) of HD fp32 accumulators, contiguous, written
+  // in 16-byte pieces; its (m, l) pairs beside.
+  const int n4 = G * HD / 4;
   const int64_t rec0 = static_cast<int64_t>(w.part) * p.q_heads + kvh * G;
   float* ml = reinterpret_cast<float*>(p.parts.ml);
-  for (int i = tid; i < G * HD; i += NTHR) st_dev(p.parts.acc + rec0 * HD + i, fin_acc[i]);
+  {
+    const __amdgpu_buffer_rsrc_t r = coherent_rsrc(p.parts.acc + rec0 * HD);
+    for (int c = tid; c < n4; c += NTHR)
+      st_coherent16(r, static_cast<uint32_t>(c * 16), *reinterpret_cast<const f32x4*>(fin_acc + c * 4));
+  }
   if (tid < G) {
     st_dev(ml + (rec0 + tid) * 2, fin_ml[tid].x);
     st_dev(ml + (rec0 + tid) * 2 + 1, fin_ml[tid].y);
@@ -180,65 +186,44 @@ __device__ __forceinline__ void finish(const DecodeParams& p, const Work& w, int
   PROBE_TS(5);
   if (!*flag) return;
   // Every other partition incremented the counter after its partial was
-  // performed, so the coherent loads below see all of them. The loads are
-  // issued in batches (all (m, l) pairs at once, then the accumulators
-  // kMergeBatch partitions at a time) so the merge costs a few memory
-  // latencies, not one per partition.
+  // performed, so the coherent loads below see all of them. Each thread owns
+  // one 16-byte piece of the output (4 dims of one head) and merges it
+  // itself: for kMergeBatch partitions at a time it requests the piece and
+  // the head's (m, l) together, then folds them in partition order into a
+  // running (max, sum) with rescaling. Up to kMergeBatch partitions the merge
+  // is one memory round trip, with no LDS phase or barrier.
   const int np = w.n_parts;
   const int64_t rbase = static_cast<int64_t>(w.part_begin) * p.q_heads + kvh * G;
-  // Every (m, l) pair and every accumulator value is requested before any is
-  // used: one memory round trip for the whole merge (np <= kMergeBatch per
-  // batch of accumulators; more partitions take more batches).
-  for (int i = tid; i < np * G; i += NTHR) {
-    const int j = i / G, g = i - j * G;
-    const float* r = ml + (rbase + static_cast<int64_t>(j) * p.q_heads + g) * 2;
-    merge_w[i] = make_float2(ld_dev(r), ld_dev(r + 1));  // (m, l) of partition j, head g
-  }
-  constexpr int kOutPerThread = (kMaxG * HD + NTHR - 1) / NTHR;
-  float o[kOutPerThread];
-  float v0[kOutPerThread][kMergeBatch];
+  const __amdgpu_buffer_rsrc_t r = coherent_rsrc(p.parts.acc + rbase * HD);
+  for (int c = tid; c < n4; c += NTHR) {
+    const int g = c * 4 / HD;
+    float M = -FLT_MAX, L = 0.f;
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+    for (int j0 = 0; j0 < np; j0 += kMergeBatch) {
+      f32x4 x[kMergeBatch];
+      float mj[kMergeBatch], lj[kMergeBatch];
 #pragma unroll
-  for (int u = 0; u < kOutPerThread; u++) {
-    o[u] = 0.f;
-    const int i = min(tid + u * NTHR, G * HD - 1);
-#pragma unroll
-    for (int b = 0; b < kMergeBatch; b++) {
-      const int j = min(b, np - 1);
-      v0[u][b] = ld_dev(p.parts.acc + (rbase + static_cast<int64_t>(j) * p.q_heads) * HD + i);
-    }
-  }
-  __syncthreads();
-  if (tid < G) {
-    float M = -FLT_MAX;
-    for (int j = 0; j < np; j++) M = fmaxf(M, merge_w[j * G + tid].x);
-    float L = 0.f;
-    for (int j = 0; j < np; j++) L += merge_w[j * G + tid].y * exp2f(merge_w[j * G + tid].x - M);
-    merge_ml[tid] = make_float2(M, 1.f / L);
-  }
-  __syncthreads();
-  for (int i = tid; i < np * G; i += NTHR) {  // weights exp2(m_j - M) / L
-    const int g = i % G;
-    merge_w[i].x = exp2f(merge_w[i].x - merge_ml[g].x) * merge_ml[g].y;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int u = 0; u < kOutPerThread; u++) {
-    const int i = tid + u * NTHR;
-    if (i >= G * HD) continue;
-    const int g = i / HD;
-#pragma unroll
-    for (int b = 0; b < kMergeBatch; b++)
-      if (b < np) o[u] += v0[u][b] * merge_w[b * G + g].x;
-    for (int j0 = kMergeBatch; j0 < np; j0 += kMergeBatch) {
-      float v[kMergeBatch];
+      for (int b = 0; b < kMergeBatch; b++) {
+        const int64_t jr = static_cast<int64_t>(min(j0 + b, np - 1)) * p.q_heads;
+        x[b] = ld_coherent16(r, static_cast<uint32_t>((jr * HD + c * 4) * 4));
+        mj[b] = ld_dev(ml + (rbase + jr + g) * 2);
+        lj[b] = ld_dev(ml + (rbase + jr + g) * 2 + 1);
+      }
 #pragma unroll
       for (int b = 0; b < kMergeBatch; b++)
-        v[b] = ld_dev(p.parts.acc + (rbase + static_cast<int64_t>(min(j0 + b, np - 1)) * p.q_heads) * HD + i);
-#pragma unroll
-      for (int b = 0; b < kMergeBatch; b++)
-        if (j0 + b < np) o[u] += v[b] * merge_w[(j0 + b) * G + g].x;
+        if (j0 + b < np) {
+          // partition j holds sum_p exp2(s_p - m_j) v_p and l_j = sum_p exp2(s_p - m_j)
+          const float m_new = fmaxf(M, mj[b]);
+          const float a = exp2f(M - m_new), e = exp2f(mj[b] - m_new);
+          M = m_new;
+          L = L * a + lj[b] * e;
+          o = o * a + x[b] * e;
+        }
     }
-    elem<ACT>::store1(static_cast<ACT*>(p.out) + head0 * HD + i, o[u]);
+    const float inv = 1.f / L;
+    ACT* out = static_cast<ACT*>(p.out) + head0 * HD + c * 4;
+#pragma unroll
+    for (int e = 0; e < 4; e++) elem<ACT>::store1(out + e, o[e] * inv);
   }
   PROBE_TS(6);
   if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -633,8 +618,6 @@ template <typename KV, int HD, int NW> struct DecodeSmem {
   __attribute__((aligned(16))) char lds[L::BYTES];
   float fin_acc[kMaxG * HD];
   float2 fin_ml[kMaxG];
-  float2 merge_ml[kMaxG];
-  float2 merge_w[kMaxMergeEntries];
   int tab[kTabCap];
   int flag;
 };
@@ -653,8 +636,6 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
   char* lds = sm.lds;
   float* fin_acc = sm.fin_acc;
   float2* fin_ml = sm.fin_ml;
-  float2* merge_ml = sm.merge_ml;
-  float2* merge_w = sm.merge_w;
   int* tab = sm.tab;
 
   PROBE_TS(0);
@@ -827,7 +808,7 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
   if (fin_acc[tid] == 12345.f) static_cast<float*>(p.out)[0] = 0.f;
   return;
 #endif
-  finish<ACT, HD, kMfmaThreads>(p, w, G, kvh, fin_acc, fin_ml, merge_ml, merge_w, &sm.flag);
+  finish<ACT, HD, kMfmaThreads>(p, w, G, kvh, fin_acc, fin_ml, &sm.flag);
   PROBE_TS(7);
 }
 }  // namespace

@@ -35,7 +35,7 @@ constexpr int kDefaultPartition = 640;       // decode rows: smallest automatic 
 constexpr int kMaxAutoPartition = 4096;      // decode rows: largest automatic partition
 constexpr int kPartitionQuantum = 128;       // 4 waves x 32-key fp32 tiles
 constexpr int64_t kTargetItems = 512;        // workgroups per step the sizing aims for (two per CU)
-constexpr int kMaxMergeEntries = 1024;       // partitions x group the decode merge can stage
+constexpr int kMaxMergeEntries = 1024;       // partitions x group of one decode row (bounds the merge's loads)
 constexpr int kDefaultChunkTile = 32;        // query rows per chunk item (two MFMA row tiles)
 constexpr int kDefaultChunkPartition = 256;  // keys per chunk item: one LDS stage
 constexpr int kMaxChunkParts = 16;           // partitions of a chunk tile the in-kernel merge stages
@@ -159,7 +159,7 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
         for (int r = 0; r < s.len; r++) {
           const int pos = s.start + r;
           const int nb = pos / bs + 1;
-          // The in-kernel merge stages n_parts * group (m, l) pairs in LDS.
+          // Partitions per row are capped (the merging workgroup loads them all).
           const int J = std::min((nb + dec_pb - 1) / dec_pb, max_decode_parts);
           // Split rows are merged inside the decode launch by the last
           // partition to finish, so they need no combine item.
