@@ -382,10 +382,13 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
         // shared with the decode rows, whose fp32 partials may be live in the
         // same launch (the fused ragged kernel)
         const float inv = l_tot[rs] > 0.f ? 1.f / l_tot[rs] : 0.f;
+        // 16-byte piece c = (d / 2) * 4 + grp holds the lane's 4 dims of
+        // output tiles d and d + 1: dims d*16 + grp*4 .. +4, then +16
 #pragma unroll
-        for (int d = 0; d < DT; d++) {
-          const f32x4 o = acc[rs][d] * inv;
-          st_coherent8(acc_rsrc, static_cast<uint32_t>(rec * HD * 4 + (d * 16 + grp * 4) * 2), pack_half4(o));
+        for (int d = 0; d < DT; d += 2) {
+          const uint2 lo = pack_half4(acc[rs][d] * inv), hi = pack_half4(acc[rs][d + 1] * inv);
+          st_coherent16(acc_rsrc, static_cast<uint32_t>(rec * HD * 4 + ((d / 2) * 4 + grp) * 16),
+                        __builtin_bit_cast(f32x4v, make_uint4(lo.x, lo.y, hi.x, hi.y)));
         }
         if (grp == 0) {
           st_dev(ml + rec * 2, m_run[rs]);
@@ -471,11 +474,12 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
       if (o < n_out) {
         const int r = o / per_row, rem = o - r * per_row;
         const int g = rem / (HD / 8);
+        // piece d8 = (d / 2) * 4 + g4: dims (d8 / 4) * 32 + (d8 % 4) * 4 .. +4, then +16
         ACT* out = static_cast<ACT*>(p.out) + (static_cast<int64_t>(tok0 + r) * p.q_heads + kvh * G + g) * HD +
-                   d8[gi] * 8;
+                   (d8[gi] >> 2) * 32 + (d8[gi] & 3) * 4;
         const float inv = 1.f / L[gi];
         store4<ACT>(out, f32x4{sum[gi][0], sum[gi][1], sum[gi][2], sum[gi][3]} * inv);
-        store4<ACT>(out + 4, f32x4{sum[gi][4], sum[gi][5], sum[gi][6], sum[gi][7]} * inv);
+        store4<ACT>(out + 16, f32x4{sum[gi][4], sum[gi][5], sum[gi][6], sum[gi][7]} * inv);
       }
     }
   }
