@@ -101,6 +101,23 @@ def test_decode_block_sizes(gpu, block_size):
     assert max_abs(got2, oracle_out(case, qh)) < TOL_F32
 
 
+@pytest.mark.parametrize("kv_bf16", [False, True])
+def test_decode_partition_over_table_segments(gpu, kv_bf16):
+    """Partitions longer than the 1024 block ids a workgroup stages in LDS at
+    once (here 2400 and 1900 blocks in one partition): the table is staged in
+    segments. Also the reference-shaped launch over the same rows."""
+    ctx = [38400, 30000, 700]
+    case = make_case(ctx, num_blocks=4500, seed=71, kv_bf16=kv_bf16)
+    got, qh, plan = run_ragged(case, torch.float32, gpu, partition_tokens=40000)
+    want = oracle_out(case, qh)
+    err = max_abs(got, want)
+    print(f"segments kv_bf16={kv_bf16}: items {plan.plan.n_decode_items} max|err| {err:.3e}")
+    assert plan.plan.n_decode_items == 3
+    assert err < tol_for(kv_bf16, torch.float32)
+    ref_shaped, _ = run_decode(case, torch.float32, gpu)
+    assert max_abs(ref_shaped, want) < tol_for(kv_bf16, torch.float32)
+
+
 def test_decode_edges(gpu):
     """pos 0 (one key), exact block multiples, one row past a boundary, and a
     long 8192 context (several 512-position LDS chunks in one workgroup)."""
