@@ -368,7 +368,11 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
   }
 
   // ---- split tile: store the partial, then the last partition merges ----
-  const __amdgpu_buffer_rsrc_t acc_rsrc = coherent_rsrc(p.parts.acc);
+  // The tile's partial records start at record (part0 - part) * q_heads:
+  // offsets from there stay far below the buffer descriptor's 2 GB range
+  // however large the workspace is.
+  const int64_t rec_tile = static_cast<int64_t>(it.part0 - it.part) * p.q_heads;
+  const __amdgpu_buffer_rsrc_t acc_rsrc = coherent_rsrc(p.parts.acc + rec_tile * HD);
   float* ml = reinterpret_cast<float*>(p.parts.ml);
   if (computes) {
 #pragma unroll
@@ -387,7 +391,7 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
 #pragma unroll
         for (int d = 0; d < DT; d += 2) {
           const uint2 lo = pack_half4(acc[rs][d] * inv), hi = pack_half4(acc[rs][d + 1] * inv);
-          st_coherent16(acc_rsrc, static_cast<uint32_t>(rec * HD * 4 + ((d / 2) * 4 + grp) * 16),
+          st_coherent16(acc_rsrc, static_cast<uint32_t>((rec - rec_tile) * HD * 4 + ((d / 2) * 4 + grp) * 16),
                         __builtin_bit_cast(f32x4v, make_uint4(lo.x, lo.y, hi.x, hi.y)));
         }
         if (grp == 0) {
@@ -448,7 +452,7 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
 #pragma unroll
         for (int jj = 0; jj < kMJ; jj++) {
           const int64_t rec = rec_base[gi] + static_cast<int64_t>(min(j0 + jj, J - 1)) * p.q_heads;
-          x[gi][jj] = ld_coherent16u(acc_rsrc, static_cast<uint32_t>(rec * HD * 4 + d8[gi] * 16));
+          x[gi][jj] = ld_coherent16u(acc_rsrc, static_cast<uint32_t>((rec - rec_tile) * HD * 4 + d8[gi] * 16));
           mj[gi][jj] = ld_dev(ml + rec * 2);
           lj[gi][jj] = ld_dev(ml + rec * 2 + 1);
         }
