@@ -314,3 +314,37 @@ def test_store_then_attend(gpu, kv_bf16, new_bf16, mixed):
     print(f"store+attend kv_bf16={kv_bf16} new_bf16={new_bf16} mixed={mixed}: parts {plan.plan.n_parts} "
           f"max|err| {err:.3e}")
     assert err < tol_for(kv_bf16, torch.float32)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_ragged_steps(gpu, seed):
+    """Randomised mixed steps against the oracle: the number of sequences,
+    their contexts and rows (decode rows, chunks at cached offsets, whole
+    prompts), the GQA shape, head dim, block size, cache and activation
+    dtypes, and the decode partition size all drawn from a seeded generator.
+    Every launch shape the planner produces for such steps (one launch or
+    decode only, split and unsplit rows and tiles) is reached across the
+    seeds."""
+    rng = np.random.default_rng(1000 + seed)
+    q_heads, kv_heads = [(14, 2), (32, 4), (8, 8), (16, 2), (4, 1), (28, 4)][rng.integers(6)]
+    head_dim = int(rng.choice([64, 128]))
+    block_size = int(rng.choice([8, 16, 32]))
+    kv_bf16 = bool(rng.integers(2))
+    act = torch.bfloat16 if rng.integers(2) else torch.float32
+    n = int(rng.integers(1, 12))
+    ctx = np.exp(rng.uniform(np.log(1), np.log(3000), size=n)).astype(np.int64) + 1
+    q_len = np.ones(n, dtype=np.int64)
+    for s in range(n):
+        if rng.uniform() < 0.35:
+            q_len[s] = int(rng.integers(1, ctx[s] + 1))
+    need = int(((ctx + block_size - 1) // block_size).sum())
+    case = make_case(ctx, q_len=q_len, q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim,
+                     block_size=block_size, num_blocks=need + 64, seed=seed, kv_bf16=kv_bf16)
+    part = int(rng.choice([0, 256, 640, 2048]))
+    got, qh, plan = run_ragged(case, act, gpu, partition_tokens=part)
+    want = oracle_out(case, qh)
+    err = max_abs(got, want)
+    print(f"seed {seed}: {q_heads}/{kv_heads}x{head_dim} bs {block_size} kv_bf16 {kv_bf16} act {act} "
+          f"rows {plan.plan.n_tokens} dec {plan.plan.n_decode_items} chunk {plan.plan.n_chunk_items} "
+          f"parts {plan.plan.n_parts}: max|err| {err:.3e}")
+    assert err < tol_for(kv_bf16, act)
