@@ -221,6 +221,28 @@ int le_ragged_paged_attention_store(const void* q, le_dtype act_dtype, const voi
                                     const le_step_plan* plan, float scale, void* out,
                                     void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* ------------------------------------------------------------------------
+ * (2)+(3) A layer's attention from its stacked QKV projection rows.
+ * Equals le_rope_kv_cache_write(qkv, act_dtype, qkv_row_stride, bias,
+ * <plan positions>, <plan slots>, cos_table, sin_table, max_positions, ...,
+ * q_scratch, k_cache, v_cache, kv_dtype, num_cache_blocks*block_size)
+ * followed by le_ragged_paged_attention(q_scratch, ...) on the same plan,
+ * bit for bit (the reference's add_bias + rope + store_kv + attention
+ * launches, cuda_model.cu:358-377). When every sequence has one row in the
+ * step (decode rows only), bias, RoPE and the K/V store happen inside the
+ * attention launch and q_scratch is not touched (it may be null then).
+ * qkv: [n_tokens][qkv_row_stride] in act_dtype, q | k | v of each row at
+ * element 0, q_heads*head_dim and (q_heads+kv_heads)*head_dim; bias: fp32
+ * [(q_heads+2*kv_heads)*head_dim] or null; q_scratch: [n_tokens][q_heads *
+ * head_dim] in act_dtype. qkv_row_stride a multiple of 8.
+ * ------------------------------------------------------------------------ */
+int le_ragged_paged_attention_qkv(const void* qkv, le_dtype act_dtype, int64_t qkv_row_stride,
+                                  const float* bias, const float* cos_table, const float* sin_table,
+                                  int max_positions, void* k_cache, void* v_cache, le_dtype kv_dtype,
+                                  int64_t num_cache_blocks, const le_step_plan* plan, float scale,
+                                  void* out, void* q_scratch, void* workspace, size_t workspace_bytes,
+                                  hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

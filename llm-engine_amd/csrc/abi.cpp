@@ -173,13 +173,24 @@ size_t le_ragged_workspace_size(const le_step_plan* plan) {
 
 namespace {
 
+// A decode step's q and new K/V rows taken straight from the stacked QKV
+// projection (bias and RoPE applied inside the attention launch).
+struct RopeRows {
+  int64_t row_stride;
+  const float* bias;
+  const float* cos_t;
+  const float* sin_t;
+  int max_pos;
+};
+
 // Ragged attention over a packed step; with k_new, the step's new K/V rows are
 // stored at the plan's slots first (inside the decode launch on a pure decode
 // step, by a scatter launch otherwise).
 int ragged_attention(const void* q, le_dtype act_dtype, const void* k_new, const void* v_new,
                      le_dtype new_dtype, const void* k_cache, const void* v_cache, le_dtype kv_dtype,
                      int64_t num_cache_blocks, const le_step_plan* plan, float scale, void* out,
-                     void* workspace, size_t workspace_bytes, hipStream_t stream) {
+                     void* workspace, size_t workspace_bytes, hipStream_t stream,
+                     const RopeRows* rope = nullptr) {
   if (!plan || !valid_dtype(act_dtype) || !valid_dtype(kv_dtype)) return LE_EINVAL;
   if (plan->n_tokens == 0) return LE_OK;
   const le_plan_config& cfg = plan->cfg;
@@ -227,8 +238,13 @@ int ragged_attention(const void* q, le_dtype act_dtype, const void* k_new, const
     } else {
       d.k_new = k_new; d.v_new = v_new; d.new_bf16 = new_dtype == LE_BF16;
       d.slots = arr(plan->off_slots); d.num_slots = num_slots;
+      if (rope) {
+        d.rope_row_stride = rope->row_stride; d.rope_bias = rope->bias;
+        d.rope_cos = rope->cos_t; d.rope_sin = rope->sin_t; d.rope_max_pos = rope->max_pos;
+      }
     }
   }
+  if (rope && !d.k_new) return LE_EINVAL;  // q rows in QKV form need the in-launch path
   if (plan->n_chunk_items == 0)
     return hip_status(le::attention_decode(d, act_dtype == LE_BF16, kv_dtype == LE_BF16, stream));
 
@@ -278,6 +294,47 @@ int le_ragged_paged_attention_store(const void* q, le_dtype act_dtype, const voi
   if (plan && plan->cfg.head_dim % 8 != 0) return LE_EUNSUPPORTED;
   return ragged_attention(q, act_dtype, k_new, v_new, new_dtype, k_cache, v_cache, kv_dtype,
                           num_cache_blocks, plan, scale, out, workspace, workspace_bytes, stream);
+}
+
+
+int le_ragged_paged_attention_qkv(const void* qkv, le_dtype act_dtype, int64_t qkv_row_stride,
+                                  const float* bias, const float* cos_table, const float* sin_table,
+                                  int max_positions, void* k_cache, void* v_cache, le_dtype kv_dtype,
+                                  int64_t num_cache_blocks, const le_step_plan* plan, float scale,
+                                  void* out, void* q_scratch, void* workspace, size_t workspace_bytes,
+                                  hipStream_t stream) {
+  if (!plan || !valid_dtype(act_dtype) || !valid_dtype(kv_dtype) || max_positions <= 0)
+    return LE_EINVAL;
+  if (plan->n_tokens == 0) return LE_OK;
+  const le_plan_config& cfg = plan->cfg;
+  const int shape = check_attention_shape(cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.block_size);
+  if (shape != LE_OK) return shape;
+  if (cfg.head_dim % 16 != 0) return LE_EUNSUPPORTED;  // both halves of a head in 8-element pieces
+  const int qd = cfg.q_heads * cfg.head_dim, kvd = cfg.kv_heads * cfg.head_dim;
+  if (qkv_row_stride < static_cast<int64_t>(qd) + 2 * kvd) return LE_EINVAL;
+  if (qkv_row_stride % 8 != 0) return LE_EUNSUPPORTED;  // 16-byte vector rows
+  if (!qkv || !cos_table || !sin_table || !plan->dev) return LE_EINVAL;
+  const size_t esz = act_dtype == LE_BF16 ? 2 : 4;
+  const char* row0 = static_cast<const char*>(qkv);
+  const void* k_new = row0 + qd * esz;
+  const void* v_new = row0 + (static_cast<int64_t>(qd) + kvd) * esz;
+  if (plan->n_tokens == plan->n_seqs && plan->n_chunk_items == 0 && plan->n_decode_items > 0) {
+    // decode rows only: bias, RoPE and the store inside the attention launch
+    RopeRows r{qkv_row_stride, bias, cos_table, sin_table, max_positions};
+    return ragged_attention(qkv, act_dtype, k_new, v_new, act_dtype, k_cache, v_cache, kv_dtype,
+                            num_cache_blocks, plan, scale, out, workspace, workspace_bytes, stream, &r);
+  }
+  if (!q_scratch || !k_cache || !v_cache) return LE_EINVAL;
+  const char* dev = static_cast<const char*>(plan->dev);
+  const int32_t* positions = reinterpret_cast<const int32_t*>(dev + plan->off_positions);
+  const int32_t* slots = reinterpret_cast<const int32_t*>(dev + plan->off_slots);
+  const hipError_t e = le::rope_kv_cache_write(
+      qkv, act_dtype == LE_BF16, qkv_row_stride, bias, positions, slots, cos_table, sin_table,
+      max_positions, plan->n_tokens, cfg.q_heads, cfg.kv_heads, cfg.head_dim, q_scratch, k_cache,
+      v_cache, kv_dtype == LE_BF16, num_cache_blocks * cfg.block_size, stream);
+  if (e != hipSuccess) return hip_status(e);
+  return ragged_attention(q_scratch, act_dtype, nullptr, nullptr, LE_F32, k_cache, v_cache, kv_dtype,
+                          num_cache_blocks, plan, scale, out, workspace, workspace_bytes, stream, nullptr);
 }
 
 }  // extern "C"

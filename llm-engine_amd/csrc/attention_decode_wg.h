@@ -87,6 +87,76 @@ __device__ __forceinline__ Work resolve(const DecodeParams& p, int bx, int bz) {
               ns == 1 ? -1 : pb + split, pb, ns, split < ns};
 }
 
+// ---- Rows straight from the stacked QKV projection ----
+// Eight consecutive elements of a row as fp32.
+template <typename ACT>
+__device__ __forceinline__ void load8(const ACT* p, float* o) {
+  if constexpr (sizeof(ACT) == 2) {
+    elem<bf16_t>::widen(ld16(p), o);
+  } else {
+    elem<float>::widen(ld16(p), o);
+    elem<float>::widen(ld16(p + 4), o + 4);
+  }
+}
+template <typename ACT>
+__device__ __forceinline__ float round_act(float x) {
+  if constexpr (sizeof(ACT) == 2) return __uint_as_float(f32_to_bf16_bits(x) << 16);
+  return x;
+}
+
+// Dims [d0, d0 + 8) of one head after bias and rotate_half RoPE (rope.cu:53,
+// ops.h:55-66): head is the head's first element in the row, hb its bias (or
+// null), cs/sn the position's cos/sin rows. The operations and their order
+// are those of rope_kv_write_kernel (bias added and rounded to the activation
+// type; a*c - b*s and b*c + a*s without contraction), so q and k are
+// bit-identical to that kernel's. d0 is a multiple of 8 and half of head_dim
+// a multiple of 8, so the eight dims sit on one side of the rotation.
+template <typename ACT>
+__device__ __forceinline__ void rope8(const ACT* head, const float* hb, int d0, int half, const float* cs,
+                                      const float* sn, float* o) {
+#pragma clang fp contract(off)
+  const bool lo = d0 < half;
+  const int dp = lo ? d0 + half : d0 - half;  // the partner dims
+  float own[8], oth[8], c[8], s[8];
+  load8<ACT>(head + d0, own);
+  load8<ACT>(head + dp, oth);
+  load8<float>(cs + (lo ? d0 : dp), c);
+  load8<float>(sn + (lo ? d0 : dp), s);
+  if (hb) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      own[e] = round_act<ACT>(own[e] + hb[d0 + e]);
+      oth[e] = round_act<ACT>(oth[e] + hb[dp + e]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const float x = own[e] * c[e];
+    const float y = oth[e] * s[e];
+    o[e] = lo ? x - y : x + y;
+  }
+}
+
+// Where load_q reads the query: a q row as attention takes it, or the q part
+// of a stacked QKV row, biased and rotated on the way in.
+template <typename ACT> struct QRow {
+  const ACT* row;
+  __device__ __forceinline__ void piece8(int d0, float* o) const { load8<ACT>(row + d0, o); }
+};
+template <typename ACT> struct QRope {
+  const ACT* head;
+  const float* hb;
+  const float* cs;
+  const float* sn;
+  int half;
+  // rounded to the activation type, as the separately rotated q is stored
+  __device__ __forceinline__ void piece8(int d0, float* o) const {
+    rope8<ACT>(head, hb, d0, half, cs, sn, o);
+#pragma unroll
+    for (int e = 0; e < 8; e++) o[e] = round_act<ACT>(o[e]);
+  }
+};
+
 // The new K/V row of a decode row, for kv head kvh, stored by the workgroup
 // of the row's last partition (the only one whose keys reach the row's own
 // position) before it loads anything from the cache: the scatter of
@@ -112,7 +182,36 @@ __device__ __forceinline__ void store_new_row(const DecodeParams& p, const Work&
   const int64_t src = (static_cast<int64_t>(w.token) * p.kv_heads + kvh) * hd + c * 8;
   const int64_t dst = (slot * p.kv_heads + kvh) * hd + c * 8;
   float v[8];
-  if (p.new_bf16) {
+  if (p.rope_max_pos > 0) {
+    // k biased and rotated, v biased, as rope_kv_write_kernel stores them; a
+    // position outside the tables stores nothing
+    if (w.pos < 0 || w.pos >= p.rope_max_pos) return;
+    const int half = hd / 2;
+    const int64_t tab = static_cast<int64_t>(w.pos) * half;
+    const int64_t row = static_cast<int64_t>(w.token) * p.rope_row_stride + kvh * hd;
+    const float* hb = p.rope_bias ? p.rope_bias + (p.q_heads + which * p.kv_heads + kvh) * hd : nullptr;
+    if (p.new_bf16) {
+      const bf16_t* h = static_cast<const bf16_t*>(which ? p.v_new : p.k_new) + row;
+      if (!which) {
+        rope8<bf16_t>(h, hb, c * 8, half, p.rope_cos + tab, p.rope_sin + tab, v);
+      } else {
+        load8<bf16_t>(h + c * 8, v);
+        if (hb)
+#pragma unroll
+          for (int e = 0; e < 8; e++) v[e] = round_act<bf16_t>(v[e] + hb[c * 8 + e]);
+      }
+    } else {
+      const float* h = static_cast<const float*>(which ? p.v_new : p.k_new) + row;
+      if (!which) {
+        rope8<float>(h, hb, c * 8, half, p.rope_cos + tab, p.rope_sin + tab, v);
+      } else {
+        load8<float>(h + c * 8, v);
+        if (hb)
+#pragma unroll
+          for (int e = 0; e < 8; e++) v[e] = v[e] + hb[c * 8 + e];
+      }
+    }
+  } else if (p.new_bf16) {
     elem<bf16_t>::widen(ld16(static_cast<const bf16_t*>(which ? p.v_new : p.k_new) + src), v);
   } else {
     const float* f = static_cast<const float*>(which ? p.v_new : p.k_new) + src;
@@ -413,18 +512,14 @@ template <int HD> struct DecodeTile<bf16_t, HD> {
   static constexpr int kLaneElems = 8;     // dims per lane group and k-step
   using Regs = TileRegs<HD / 32>;
   struct QOp { bf16x8 b[HD / 32]; };
-  template <typename ACT>
-  __device__ __forceinline__ static void load_q(QOp& q, const ACT* row, bool ok, int grp) {
+  template <typename Src>
+  __device__ __forceinline__ static void load_q(QOp& q, const Src& src, bool ok, int grp) {
     // unconditional 16-byte loads (the row pointer is valid for every
     // lane), selected afterwards: a load under a branch is waited for
     // before the next one is issued
-    const ACT* r = row + grp * 8;
-    constexpr int V = elem<ACT>::VEC;
     float f[HD / 32][8];
 #pragma unroll
-    for (int ks = 0; ks < HD / 32; ks++)
-#pragma unroll
-      for (int e = 0; e < 8; e += V) elem<ACT>::widen(ld16(r + ks * 32 + e), &f[ks][e]);
+    for (int ks = 0; ks < HD / 32; ks++) src.piece8(grp * 8 + ks * 32, f[ks]);
 #pragma unroll
     for (int ks = 0; ks < HD / 32; ks++)
 #pragma unroll
@@ -487,13 +582,11 @@ template <int HD> struct DecodeTile<float, HD> {
     bool ok[kSub];
   };
   struct QOp { float q[kLaneDims]; };
-  template <typename ACT>
-  __device__ __forceinline__ static void load_q(QOp& q, const ACT* row, bool ok, int grp) {
-    const ACT* r = row + grp * kLaneDims;  // unconditional vector loads, as in the bf16 tile
-    constexpr int V = elem<ACT>::VEC;
-    float f[kLaneDims];
+  template <typename Src>
+  __device__ __forceinline__ static void load_q(QOp& q, const Src& src, bool ok, int grp) {
+    float f[kLaneDims];  // unconditional vector loads, as in the bf16 tile
 #pragma unroll
-    for (int j = 0; j < kLaneDims; j += V) elem<ACT>::widen(ld16(r + j), &f[j]);
+    for (int j = 0; j < kLaneDims; j += 8) src.piece8(grp * kLaneDims + j, &f[j]);
 #pragma unroll
     for (int j = 0; j < kLaneDims; j++) q.q[j] = ok ? f[j] : 0.f;
   }
@@ -687,9 +780,17 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
   typename T::QOp qb;
   {
     const bool ok = col < G;
-    T::template load_q<ACT>(qb, static_cast<const ACT*>(p.q) +
-                                    (static_cast<int64_t>(w.token) * p.q_heads + kvh * G + (ok ? col : 0)) * HD,
-                            ok, grp);
+    const int h = kvh * G + (ok ? col : 0);
+    if (p.rope_max_pos > 0) {
+      const bool pos_ok = w.pos >= 0 && w.pos < p.rope_max_pos;  // else q = 0, as rope_kv_write_kernel
+      const int64_t tab = static_cast<int64_t>(pos_ok ? w.pos : 0) * (HD / 2);
+      const QRope<ACT> src{static_cast<const ACT*>(p.q) + static_cast<int64_t>(w.token) * p.rope_row_stride + h * HD,
+                           p.rope_bias ? p.rope_bias + h * HD : nullptr, p.rope_cos + tab, p.rope_sin + tab, HD / 2};
+      T::load_q(qb, src, ok && pos_ok, grp);
+    } else {
+      const QRow<ACT> src{static_cast<const ACT*>(p.q) + (static_cast<int64_t>(w.token) * p.q_heads + h) * HD};
+      T::load_q(qb, src, ok, grp);
+    }
   }
 
   WaveAcc<HD> st;

@@ -256,8 +256,6 @@ void Model::forward(const le_step_slice* slices, int n_slices, int32_t* tokens_o
   const int N = plan.n_tokens, R = plan.n_logits;
   if (N == 0) return;
   const int32_t* d_ids = le_plan_dev_array(&plan, plan.off_token_ids);
-  const int32_t* d_pos = le_plan_dev_array(&plan, plan.off_positions);
-  const int32_t* d_slots = le_plan_dev_array(&plan, plan.off_slots);
   const int32_t* d_rows = le_plan_dev_array(&plan, plan.off_logit_rows);
   const size_t n = static_cast<size_t>(N);
   const int QKV = QD_ + 2 * KVD_;
@@ -273,26 +271,24 @@ void Model::forward(const le_step_slice* slices, int n_slices, int32_t* tokens_o
   void* ws = ws_bytes ? ws_.get(ws_bytes, /*zero=*/true, stream_) : nullptr;
   const float scale = 1.0f / std::sqrt(static_cast<float>(hd_));
   const le_dtype act_dt = bf16_ ? LE_BF16 : LE_F32, kv_dt = kv_bf16_ ? LE_BF16 : LE_F32;
-  const int64_t num_slots = static_cast<int64_t>(num_blocks_) * bs_;
   const int L_n = static_cast<int>(layers_.size());
 
-  // Per layer: norm (fused with the previous residual add), one QKV GEMM, one
-  // bias+RoPE+cache-write launch, attention, O GEMM, residual+norm, one
-  // gate|up GEMM, SiLU product, down GEMM.
+  // Per layer: norm (fused with the previous residual add), one QKV GEMM,
+  // attention with bias+RoPE+cache-write (inside its launch on a decode
+  // step), O GEMM, residual+norm, one gate|up GEMM, SiLU product, down GEMM.
   hip_ok(gather_rows(embed_, d_ids, x, N, H_, bf16_, stream_), "embedding");
   hip_ok(residual_rmsnorm(x, nullptr, nullptr, layers_[0].in_norm, h, N, H_, d_.eps, false, bf16_, stream_),
          "rmsnorm");
   for (int l = 0; l < L_n; l++) {
     const Layer& L = layers_[l];
     gemm(h, L.wqkv, qkv, N, QKV, H_);
-    // Every token's K/V is rotated and written before attention runs, so
-    // tokens of one step (a prefill chunk) attend to each other.
-    le_ok(le_rope_kv_cache_write(qkv, act_dt, QKV, L.bqkv, d_pos, d_slots, cos_, sin_, d_.max_pos, N,
-                                 nh_, nkv_, hd_, q, kc_[l], vc_[l], kv_dt, num_slots, stream_),
-          "le_rope_kv_cache_write");
-    le_ok(le_ragged_paged_attention(q, act_dt, kc_[l], vc_[l], kv_dt, num_blocks_, &plan, scale, attn, ws,
-                                    ws_bytes, stream_),
-          "le_ragged_paged_attention");
+    // Bias, RoPE, the K/V store and attention from the QKV rows: one launch
+    // on a decode step; otherwise every token's K/V is rotated and written
+    // before attention runs, so tokens of one step (a prefill chunk) attend
+    // to each other.
+    le_ok(le_ragged_paged_attention_qkv(qkv, act_dt, QKV, L.bqkv, cos_, sin_, d_.max_pos, kc_[l], vc_[l],
+                                        kv_dt, num_blocks_, &plan, scale, attn, q, ws, ws_bytes, stream_),
+          "le_ragged_paged_attention_qkv");
     gemm(attn, L.wo, o, N, H_, QD_);
     hip_ok(residual_rmsnorm(x, o, nullptr, L.post_norm, h, N, H_, d_.eps, true, bf16_, stream_), "residual");
     gemm(h, L.wgate_up, gate_up, N, 2 * I_, H_);

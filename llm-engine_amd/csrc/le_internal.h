@@ -66,6 +66,19 @@ struct DecodeParams {
   const int32_t* slots;
   int new_bf16;
   int64_t num_slots;
+  // Rows straight from the stacked QKV projection (rope_max_pos > 0): q and
+  // the new K/V rows are read at rope_row_stride elements per token (q, k_new
+  // and v_new point at row 0's q, k and v parts, all in the activation type);
+  // the bias (fp32 [q | k | v], may be null) is added and rounded to the
+  // activation type, then q and k rotate by the row's position (tables
+  // [rope_max_pos][head_dim / 2]) exactly as rope_kv_cache_write computes
+  // them. A row whose position is outside the tables attends with q = 0 and
+  // stores nothing (as rope_kv_cache_write writes zeros and skips the store).
+  int64_t rope_row_stride;
+  const float* rope_bias;
+  const float* rope_cos;
+  const float* rope_sin;
+  int rope_max_pos;
   const DecodeItem* items;  // null: one item per (token, split) with `nsplit` splits
   const int32_t* item_ids;  // with items: block ids of item i at item_ids[i * ids_stride + j]
   int ids_stride;

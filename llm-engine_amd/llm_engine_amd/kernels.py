@@ -250,3 +250,45 @@ def ragged_paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
         float(scale), _p(out), _p(workspace), workspace.numel() * workspace.element_size(),
         _stream(stream)))
     return out
+
+
+def ragged_paged_attention_qkv(qkv: torch.Tensor, bias: torch.Tensor | None, cos_t: torch.Tensor,
+                               sin_t: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                               plan: Plan, scale: float, out: torch.Tensor | None = None,
+                               workspace: torch.Tensor | None = None, q_scratch: torch.Tensor | None = None,
+                               stream=None) -> torch.Tensor:
+    """A layer's attention from its stacked QKV rows (cuda_model.cu:358-377:
+    bias, RoPE, the K/V store and attention). Equals rope_kv_cache_write on the
+    plan's positions and slots followed by ragged_paged_attention, bit for bit;
+    on a decode-only step all of it runs in the attention launch
+    (le_ragged_paged_attention_qkv). qkv: [N, >= (q_heads + 2*kv_heads)*head_dim]
+    laid out [q | k | v]; cos_t/sin_t: fp32 [max_pos, head_dim/2]."""
+    P = plan.plan
+    cfg = P.cfg
+    n = P.n_tokens
+    _req(plan.device_buf is not None, "plan not uploaded")
+    hd, qd, kv_dim = cfg.head_dim, cfg.q_heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+    _req(qkv.dim() == 2 and qkv.stride(1) == 1 and qkv.shape[0] == n and qkv.shape[1] >= qd + 2 * kv_dim,
+         "qkv: [N, >= q_dim + 2*kv_dim] with unit column stride")
+    _req(cos_t.dtype == torch.float32 and cos_t.shape == sin_t.shape and cos_t.is_contiguous()
+         and sin_t.is_contiguous() and cos_t.shape[1] == hd // 2, "cos/sin: fp32 [max_pos, head_dim/2]")
+    if bias is not None:
+        _req(bias.dtype == torch.float32 and bias.is_contiguous() and bias.numel() == qd + 2 * kv_dim,
+             "bias: fp32 [q_dim + 2*kv_dim]")
+    _req(k_cache.shape == v_cache.shape and k_cache.dtype == v_cache.dtype, "k/v caches must match")
+    num_blocks = k_cache.numel() // (cfg.block_size * kv_dim)
+    if out is None:
+        out = torch.empty(n, qd, dtype=qkv.dtype, device=qkv.device)
+    if q_scratch is None:
+        q_scratch = torch.empty(n, qd, dtype=qkv.dtype, device=qkv.device)
+    _req(q_scratch.is_contiguous() and q_scratch.numel() >= n * qd and q_scratch.dtype == qkv.dtype,
+         "q_scratch: [N, q_dim] in the activation dtype")
+    need = plan.workspace_size()
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.zeros(max(need, 1), dtype=torch.uint8, device=qkv.device)
+    check("le_ragged_paged_attention_qkv", _lib.load().le_ragged_paged_attention_qkv(
+        _p(qkv), _dt(qkv), qkv.stride(0), None if bias is None else _p(bias), _p(cos_t), _p(sin_t),
+        cos_t.shape[0], _p(k_cache), _p(v_cache), _dt(k_cache), num_blocks, ctypes.byref(P), float(scale),
+        _p(out), _p(q_scratch), _p(workspace), workspace.numel() * workspace.element_size(),
+        _stream(stream)))
+    return out
