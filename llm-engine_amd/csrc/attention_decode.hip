@@ -4,6 +4,8 @@
 // the fused ragged kernel (attention_ragged.hip) shares.
 #include "attention_decode_wg.h"
 
+#include <atomic>
+
 namespace le {
 namespace {
 
@@ -44,6 +46,52 @@ extern "C" int le_probe_timing_clear(void) {
   return hipMemcpyToSymbol(HIP_SYMBOL(dec::g_probe_ts), zeros, sizeof(zeros)) == hipSuccess ? 0 : 1;
 }
 #endif
+
+namespace {
+__global__ void xcd_probe_kernel(int* out) {
+  if (threadIdx.x == 0) {
+    unsigned v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    out[blockIdx.x + blockIdx.y * gridDim.x] = static_cast<int>(v & 0xf);
+  }
+}
+
+constexpr int kProbeW = 1000, kProbeH = 2;
+__device__ int g_xcd_probe[kProbeW * kProbeH];  // static: the check allocates nothing
+
+// 1-D and 2-D grids of the sizes decode launches use, wider than the chip.
+int probe_placement(hipStream_t stream) {
+  int* d = nullptr;
+  if (hipGetSymbolAddress(reinterpret_cast<void**>(&d), HIP_SYMBOL(g_xcd_probe)) != hipSuccess) return 0;
+  static int h[kProbeW * kProbeH];
+  bool ok = true;
+  for (int shape = 0; shape < 2 && ok; shape++) {
+    const dim3 grid = shape == 0 ? dim3(kProbeW * kProbeH) : dim3(kProbeW, kProbeH);
+    xcd_probe_kernel<<<grid, 64, 0, stream>>>(d);
+    ok = hipGetLastError() == hipSuccess &&
+         hipMemcpyAsync(h, d, sizeof(h), hipMemcpyDeviceToHost, stream) == hipSuccess &&
+         hipStreamSynchronize(stream) == hipSuccess;
+    for (int i = 0; ok && i < kProbeW * kProbeH; i++) ok = h[i] == i % 8;
+  }
+  return ok ? 1 : 0;
+}
+}  // namespace
+
+bool xcd_placement_holds(hipStream_t stream) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> state[kMaxDevices];  // 0 unknown, 1 holds, 2 does not
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+  int st = state[dev].load();
+  if (st == 0) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+      return false;  // no probe inside a capture; the coherent stores are correct anywhere
+    st = probe_placement(stream) ? 1 : 2;
+    state[dev].store(st);
+  }
+  return st == 1;
+}
 
 int decode_nsplit(int n_tokens, int kv_heads) {
   const int rows = n_tokens * kv_heads;

@@ -37,8 +37,11 @@ __global__ __launch_bounds__(kRaggedThreads) void ragged_kernel(DecodeParams dp,
   if (b < n_chunk_wg) {
     chk::chunk_wg<ACT, HD>(cp, sm.c, b / cp.kv_heads, b % cp.kv_heads);
   } else {
+    // item-major within each kv head, as the decode kernel's 2-D grid: the
+    // plan places a split row's partitions at item indices equal modulo 8,
+    // so they share an XCD in either launch
     const int d = b - n_chunk_wg;
-    dec::decode_wg<ACT, bf16_t, HD, kDecodeWaves>(dp, sm.d, d / dp.kv_heads, d % dp.kv_heads, 0);
+    dec::decode_wg<ACT, bf16_t, HD, kDecodeWaves>(dp, sm.d, d % dp.n_rows, d / dp.n_rows, 0);
   }
 }
 

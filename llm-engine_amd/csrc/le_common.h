@@ -153,6 +153,11 @@ __device__ __forceinline__ f32x4v ld_coherent16(__amdgpu_buffer_rsrc_t r, uint32
 __device__ __forceinline__ void st_coherent16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, f32x4v v) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4raw, v), r, byte_off, 0, kCachePolicySc1);
 }
+// A plain 16-byte store (write-back into the XCD's L2), for data that only
+// workgroups on the same XCD read back.
+__device__ __forceinline__ void st_l2_16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, f32x4v v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4raw, v), r, byte_off, 0, 0);
+}
 typedef uint32_t u32x2raw __attribute__((vector_size(8)));
 __device__ __forceinline__ void st_coherent8(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, uint2 v) {
   __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2raw, v), r, byte_off, 0, kCachePolicySc1);

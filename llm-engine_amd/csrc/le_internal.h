@@ -87,7 +87,16 @@ struct DecodeParams {
   int q_heads, kv_heads, head_dim, block_size;
   float scale_log2;         // softmax scale * log2(e)
   int64_t num_cache_blocks;
+  // With items: every partition of a split row runs on one XCD (the plan's
+  // placement, confirmed on this device by xcd_placement_holds), so partials
+  // go through that XCD's L2 with plain stores.
+  int l2_local;
 };
+
+// True when this device sends workgroup i of a launch to XCD i % 8 (checked
+// once per device with a probe launch, then cached). False while the stream
+// is being captured and the device is not checked yet, or on any error.
+bool xcd_placement_holds(hipStream_t stream);
 
 hipError_t attention_decode(const DecodeParams& p, int act_bf16, int kv_bf16, hipStream_t stream);
 

@@ -39,13 +39,62 @@ constexpr int kMaxMergeEntries = 1024;       // partitions x group of one decode
 constexpr int kDefaultChunkTile = 32;        // query rows per chunk item (two MFMA row tiles)
 constexpr int kDefaultChunkPartition = 256;  // keys per chunk item: one LDS stage
 constexpr int kMaxChunkParts = 16;           // partitions of a chunk tile the in-kernel merge stages
-constexpr int kMaxChunkItemBlocks = 1024;    // block ids of one chunk item the kernel stages
+constexpr int kMaxChunkItemBlocks = 1024;
+constexpr int kXcds = 8;                     // MI355X: XCDs, each with its own L2
+constexpr int kItemOverheadBlocks = 8;       // a decode item's fixed cost, in streamed blocks    // block ids of one chunk item the kernel stages
 
 int64_t align256(int64_t x) { return (x + 255) & ~static_cast<int64_t>(255); }
 
 int round_to_blocks(int tokens, int bs) {
   const int b = (tokens + bs - 1) / bs;
   return b < 1 ? 1 : b;
+}
+
+// The dispatcher sends workgroup i of a launch (linear id) to XCD i % 8, and
+// each XCD has its own L2. A split row's partitions exchange partials and an
+// arrival counter at the end of the launch; with all of them on one XCD that
+// exchange stays in one L2. So the rows (each row's partitions as a unit) are
+// dealt longest-first into kXcds bins, each to the bin with the least work so
+// far, and item k of bin b goes to index k * kXcds + b. Bins are padded to
+// one length with empty items (n_parts 0), so the item count is a multiple of
+// kXcds and the kv head's offset in the grid (a multiple of the item count)
+// keeps every row on its bin's XCD.
+std::vector<le::DecodeItem> place_on_xcds(const std::vector<le::DecodeItem>& dec) {
+  struct Row { size_t first, n; int64_t longest, work; };
+  std::vector<Row> rows;
+  for (size_t i = 0; i < dec.size();) {
+    size_t j = i;
+    Row r{i, 0, 0, 0};
+    while (j < dec.size() && dec[j].token == dec[i].token && dec[j].part_begin == dec[i].part_begin) {
+      const int64_t nb = dec[j].blk_end - dec[j].blk_begin;
+      r.longest = std::max(r.longest, nb);
+      r.work += nb + kItemOverheadBlocks;
+      j++;
+    }
+    r.n = j - i;
+    rows.push_back(r);
+    i = j;
+  }
+  std::stable_sort(rows.begin(), rows.end(), [](const Row& a, const Row& b) { return a.longest > b.longest; });
+  std::vector<std::vector<le::DecodeItem>> bins(kXcds);
+  int64_t load[kXcds] = {};
+  for (const Row& r : rows) {
+    int b = 0;
+    for (int k = 1; k < kXcds; k++)
+      if (load[k] < load[b]) b = k;
+    load[b] += r.work;
+    for (size_t k = 0; k < r.n; k++) bins[b].push_back(dec[r.first + k]);
+  }
+  size_t len = 0;
+  for (const auto& b : bins) len = std::max(len, b.size());
+  le::DecodeItem pad{};
+  pad.token = -1;
+  pad.part = -1;
+  pad.n_parts = 0;  // resolved as "no work"
+  std::vector<le::DecodeItem> out(len * kXcds, pad);
+  for (int b = 0; b < kXcds; b++)
+    for (size_t k = 0; k < bins[b].size(); k++) out[k * kXcds + b] = bins[b][k];
+  return out;
 }
 
 }  // namespace
@@ -185,9 +234,13 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
   // Longest work first: workgroups start over a couple of microseconds in
   // launch order, so the items on the critical path (most keys) go first.
   // Merges do not depend on the order (partials are addressed by index).
-  std::stable_sort(dec.begin(), dec.end(), [](const le::DecodeItem& a, const le::DecodeItem& b) {
-    return a.blk_end - a.blk_begin > b.blk_end - b.blk_begin;
-  });
+  if (parts > 0) {
+    dec = place_on_xcds(dec);
+  } else {
+    std::stable_sort(dec.begin(), dec.end(), [](const le::DecodeItem& a, const le::DecodeItem& b) {
+      return a.blk_end - a.blk_begin > b.blk_end - b.blk_begin;
+    });
+  }
   std::stable_sort(chk.begin(), chk.end(), [](const le::ChunkItem& a, const le::ChunkItem& b) {
     return a.blk_end - a.blk_begin > b.blk_end - b.blk_begin;
   });

@@ -75,11 +75,19 @@ def check_work_lists(plan, slices, bs=16):
     toff = plan.host_array("table_offset")
     tseq = plan.host_array("token_seq")
     # decode items: per row, [blk_begin, blk_end) ranges tile [0, pos/bs] exactly once
-    rows = {}
-    for it in dec:
+    rows, bins = {}, {}
+    for k, it in enumerate(dec):
         token, p, to, b0, b1, part, pb, npart = (int(x) for x in it)
+        if npart == 0:  # padding that keeps split rows on one XCD
+            assert token == -1 and b0 == b1 and P.n_parts > 0
+            continue
         assert p == pos[token] and to == toff[tseq[token]]
         rows.setdefault(token, []).append((b0, b1, part, pb, npart))
+        if npart > 1:  # a split row's partitions sit at indices equal modulo 8 (one XCD)
+            bins.setdefault(token, set()).add(k % 8)
+    assert all(len(b) == 1 for b in bins.values())
+    if P.n_parts > 0:
+        assert len(dec) % 8 == 0
     for token, items in rows.items():
         items.sort()
         assert items[0][0] == 0 and items[-1][1] == pos[token] // bs + 1
