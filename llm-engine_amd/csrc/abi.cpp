@@ -224,7 +224,10 @@ int ragged_attention(const void* q, le_dtype act_dtype, const void* k_new, const
   d.n_rows = plan->n_decode_items; d.nsplit = 1;
   d.q_heads = cfg.q_heads; d.kv_heads = cfg.kv_heads; d.head_dim = cfg.head_dim;
   d.block_size = cfg.block_size; d.scale_log2 = scale_log2; d.num_cache_blocks = num_cache_blocks;
-  d.l2_local = plan->n_parts > 0 && le::xcd_placement_holds(stream);
+  // LE_DECODE_COHERENT=1 keeps the write-through partials (read per call:
+  // tests run both paths)
+  const char* coh = std::getenv("LE_DECODE_COHERENT");
+  d.l2_local = plan->n_parts > 0 && !(coh && coh[0] == '1') && le::xcd_placement_holds(stream);
   const int64_t num_slots = num_cache_blocks * cfg.block_size;
   hipError_t e = hipSuccess;
   if (k_new) {

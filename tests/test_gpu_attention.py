@@ -348,3 +348,27 @@ def test_random_ragged_steps(gpu, seed):
           f"rows {plan.plan.n_tokens} dec {plan.plan.n_decode_items} chunk {plan.plan.n_chunk_items} "
           f"parts {plan.plan.n_parts}: max|err| {err:.3e}")
     assert err < tol_for(kv_bf16, act)
+
+
+@pytest.mark.parametrize("kv_bf16", [False, True])
+def test_split_rows_both_partial_paths(gpu, monkeypatch, kv_bf16):
+    """Split decode rows of a plan launch merge through the XCD's L2 (the plan
+    places a row's partitions on one XCD) unless LE_DECODE_COHERENT=1 keeps
+    the write-through partials. Both paths against the oracle, on rows split
+    into 2..7 partitions, with a mixed step (chunk rows in the same launch)
+    as well."""
+    rng = np.random.default_rng(77)
+    ctx = loguniform_ctx(rng, 24, 700, 4096)
+    for q_len in (None, [1] * 23 + [64]):
+        case = make_case(ctx, q_len=q_len, num_blocks=8192, seed=78, kv_bf16=kv_bf16)
+        want = None
+        for coherent in ("0", "1"):
+            monkeypatch.setenv("LE_DECODE_COHERENT", coherent)
+            got, qh, plan = run_ragged(case, torch.float32, gpu, partition_tokens=640)
+            if want is None:
+                want = oracle_out(case, qh)
+            err = max_abs(got, want)
+            print(f"coherent={coherent} mixed={q_len is not None}: parts {plan.plan.n_parts} "
+                  f"decode items {plan.plan.n_decode_items} max|err| {err:.3e}")
+            assert plan.plan.n_parts > 0 and plan.plan.n_decode_items % 8 == 0
+            assert err < tol_for(kv_bf16, torch.float32)
