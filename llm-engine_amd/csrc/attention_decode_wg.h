@@ -386,6 +386,33 @@ template <int HD> struct WaveAcc {
 // Block ids come from the LDS copy of the table (`tab`, indexed from the
 // segment's first block), never through a generic pointer: a flat load would
 // count against the global-load counter and stall behind the K/V loads.
+// Online softmax of one tile (log2 domain). s holds the tile's scaled scores
+// (-inf for dead keys) in a lane's column, mt their maximum over the column.
+// The arguments of exp2 are <= 0, so the raw hardware exp2 (whose results
+// below 2^-126 flush to zero) suffices; exp2f wraps a denormal-safe scaling
+// around it on every score. The rescale is unconditional: a wave-uniform
+// branch around it splits the loop body, and the next tile's loads then no
+// longer interleave with this tile's arithmetic (28.6 -> 29.7 us on 64 rows
+// x 4096 keys).
+template <int NS, int HD>
+__device__ __forceinline__ void softmax_tile(WaveAcc<HD>& st, f32x4 (&s)[NS], float mt) {
+  const float m_new = fmaxf(st.m, mt);
+  const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
+  st.m = m_new;
+  float ls = 0.f;
+#pragma unroll
+  for (int i = 0; i < NS; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const float e = __builtin_amdgcn_exp2f(s[i][j] - m_new);
+      s[i][j] = e;
+      ls += e;
+    }
+  st.l = st.l * alpha + ls;
+#pragma unroll
+  for (int d = 0; d < HD / 16; d++) st.acc[d] *= alpha;
+}
+
 template <int HD>
 __device__ __forceinline__ void load_tile(TileRegs<HD / 32>& r, const bf16_t* kc, const bf16_t* vc,
                                           int key0, int key_end, int kv_stride, int bs_shift,
@@ -445,21 +472,7 @@ __device__ __forceinline__ void compute_tile(WaveAcc<HD>& st, const TileRegs<HD 
     }
   mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
   mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-  const float m_new = fmaxf(st.m, mt);
-  const float alpha = exp2f(st.m - m_new);
-  st.m = m_new;
-  float ls = 0.f;
-#pragma unroll
-  for (int i = 0; i < 4; i++)
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const float e = exp2f(s[i][j] - m_new);
-      s[i][j] = e;
-      ls += e;
-    }
-  st.l = st.l * alpha + ls;
-#pragma unroll
-  for (int d = 0; d < DT; d++) st.acc[d] *= alpha;
+  softmax_tile<4>(st, s, mt);
 
   // V rows into this wave's LDS tile, row-major (key rows), with 16-byte
   // stores. A dead key's row is replaced by zeros (its p is 0, but the row
@@ -670,21 +683,7 @@ template <int HD> struct DecodeTile<float, HD> {
       }
     mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
     mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-    const float m_new = fmaxf(st.m, mt);
-    const float alpha = exp2f(st.m - m_new);
-    st.m = m_new;
-    float ls = 0.f;
-#pragma unroll
-    for (int i = 0; i < kSub; i++)
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const float e = exp2f(s[i][j] - m_new);
-        s[i][j] = e;
-        ls += e;
-      }
-    st.l = st.l * alpha + ls;
-#pragma unroll
-    for (int d = 0; d < DT; d++) st.acc[d] *= alpha;
+    softmax_tile<kSub>(st, s, mt);
 
     // V rows into this wave's LDS tile (row-major); a dead key's row is zeros.
 #pragma unroll
