@@ -492,7 +492,7 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
           if (j0 + jj < J) {
             // partition j holds o_j / l_j (fp16); fold in l_j * o_j at weight exp2(m_j - max)
             const float m_new = fmaxf(M[gi], mj[gi][jj]);
-            const float a = exp2f(M[gi] - m_new), w = exp2f(mj[gi][jj] - m_new) * lj[gi][jj];
+            const float a = __builtin_amdgcn_exp2f(M[gi] - m_new), w = __builtin_amdgcn_exp2f(mj[gi][jj] - m_new) * lj[gi][jj];
             M[gi] = m_new;
             L[gi] = L[gi] * a + w;
             float f[8];

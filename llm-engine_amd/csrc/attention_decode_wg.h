@@ -324,7 +324,7 @@ __device__ __forceinline__ void finish(const DecodeParams& p, const Work& w, int
         if (j0 + b < np) {
           // partition j holds sum_p exp2(s_p - m_j) v_p and l_j = sum_p exp2(s_p - m_j)
           const float m_new = fmaxf(M, mj[b]);
-          const float a = exp2f(M - m_new), e = exp2f(mj[b] - m_new);
+          const float a = __builtin_amdgcn_exp2f(M - m_new), e = __builtin_amdgcn_exp2f(mj[b] - m_new);
           M = m_new;
           L = L * a + lj[b] * e;
           o = o * a + x[b] * e;
@@ -906,7 +906,7 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
 #pragma unroll
     for (int v = 0; v < kMfmaWaves; v++) {
       const float* r = red + (v * kMaxG + g) * L::RED_STRIDE;
-      const float e = exp2f(r[HD] - M);
+      const float e = __builtin_amdgcn_exp2f(r[HD] - M);
       o += r[d] * e;
       Ls += r[HD + 1] * e;
     }
