@@ -242,9 +242,50 @@ __device__ __forceinline__ void st_dev(float* p, float v) {
   __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float ld_dev(const float* p) {
-  return __uint_as_float(__hip_atomic_load(reinterpret_cast<uint32_t*>(const_cast<float*>(p)),
-                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+__device__ __forceinline__ float2 ld_dev2(const float* p) {  // 8 bytes, 8-byte aligned
+  const uint64_t v = __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<float*>(p)), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float(static_cast<uint32_t>(v)), __uint_as_float(static_cast<uint32_t>(v >> 32)));
+}
+
+// The last arriver's merge of a split row: each thread owns one 16-byte
+// piece of the output (4 dims of one head) and, for B partitions at a time,
+// requests that piece of each partial together with the head's (m, l) (one
+// 8-byte load), then folds them in partition order into a running (max,
+// sum) with rescaling. Up to B partitions the merge is one memory round
+// trip, with no LDS phase or barrier.
+template <typename ACT, int HD, int NTHR, int B>
+__device__ __forceinline__ void merge_parts(const DecodeParams& p, __amdgpu_buffer_rsrc_t r, const float* ml,
+                                            int64_t rbase, int np, int n4, int64_t head0) {
+  for (int c = threadIdx.x; c < n4; c += NTHR) {
+    const int g = c * 4 / HD;
+    float M = -FLT_MAX, L = 0.f;
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+    for (int j0 = 0; j0 < np; j0 += B) {
+      f32x4 x[B];
+      float2 mlj[B];
+#pragma unroll
+      for (int b = 0; b < B; b++) {
+        const int64_t jr = static_cast<int64_t>(min(j0 + b, np - 1)) * p.q_heads;
+        x[b] = ld_coherent16(r, static_cast<uint32_t>((jr * HD + c * 4) * 4));
+        mlj[b] = ld_dev2(ml + (rbase + jr + g) * 2);
+      }
+#pragma unroll
+      for (int b = 0; b < B; b++)
+        if (j0 + b < np) {
+          // partition j holds sum_p exp2(s_p - m_j) v_p and l_j = sum_p exp2(s_p - m_j)
+          const float m_new = fmaxf(M, mlj[b].x);
+          const float a = __builtin_amdgcn_exp2f(M - m_new), e = __builtin_amdgcn_exp2f(mlj[b].x - m_new);
+          M = m_new;
+          L = L * a + mlj[b].y * e;
+          o = o * a + x[b] * e;
+        }
+    }
+    const float inv = 1.f / L;
+    ACT* out = static_cast<ACT*>(p.out) + head0 * HD + c * 4;
+#pragma unroll
+    for (int e = 0; e < 4; e++) elem<ACT>::store1(out + e, o[e] * inv);
+  }
 }
 
 // Final stage shared by both kernels. fin_acc[g * HD + d] holds the
@@ -296,45 +337,16 @@ __device__ __forceinline__ void finish(const DecodeParams& p, const Work& w, int
   PROBE_TS(5);
   if (!*flag) return;
   // Every other partition incremented the counter after its partial was
-  // performed, so the coherent loads below see all of them. Each thread owns
-  // one 16-byte piece of the output (4 dims of one head) and merges it
-  // itself: for kMergeBatch partitions at a time it requests the piece and
-  // the head's (m, l) together, then folds them in partition order into a
-  // running (max, sum) with rescaling. Up to kMergeBatch partitions the merge
-  // is one memory round trip, with no LDS phase or barrier.
+  // performed, so the coherent loads of the merge see all of them.
   const int np = w.n_parts;
   const int64_t rbase = static_cast<int64_t>(w.part_begin) * p.q_heads + kvh * G;
   const __amdgpu_buffer_rsrc_t r = coherent_rsrc(p.parts.acc + rbase * HD);
-  for (int c = tid; c < n4; c += NTHR) {
-    const int g = c * 4 / HD;
-    float M = -FLT_MAX, L = 0.f;
-    f32x4 o = {0.f, 0.f, 0.f, 0.f};
-    for (int j0 = 0; j0 < np; j0 += kMergeBatch) {
-      f32x4 x[kMergeBatch];
-      float mj[kMergeBatch], lj[kMergeBatch];
-#pragma unroll
-      for (int b = 0; b < kMergeBatch; b++) {
-        const int64_t jr = static_cast<int64_t>(min(j0 + b, np - 1)) * p.q_heads;
-        x[b] = ld_coherent16(r, static_cast<uint32_t>((jr * HD + c * 4) * 4));
-        mj[b] = ld_dev(ml + (rbase + jr + g) * 2);
-        lj[b] = ld_dev(ml + (rbase + jr + g) * 2 + 1);
-      }
-#pragma unroll
-      for (int b = 0; b < kMergeBatch; b++)
-        if (j0 + b < np) {
-          // partition j holds sum_p exp2(s_p - m_j) v_p and l_j = sum_p exp2(s_p - m_j)
-          const float m_new = fmaxf(M, mj[b]);
-          const float a = __builtin_amdgcn_exp2f(M - m_new), e = __builtin_amdgcn_exp2f(mj[b] - m_new);
-          M = m_new;
-          L = L * a + lj[b] * e;
-          o = o * a + x[b] * e;
-        }
-    }
-    const float inv = 1.f / L;
-    ACT* out = static_cast<ACT*>(p.out) + head0 * HD + c * 4;
-#pragma unroll
-    for (int e = 0; e < 4; e++) elem<ACT>::store1(out + e, o[e] * inv);
-  }
+  // Batches as wide as the row's partition count (up to kMergeBatch), so no
+  // load is issued twice.
+  if (np <= kMergeBatch / 2)
+    merge_parts<ACT, HD, NTHR, kMergeBatch / 2>(p, r, ml, rbase, np, n4, head0);
+  else
+    merge_parts<ACT, HD, NTHR, kMergeBatch>(p, r, ml, rbase, np, n4, head0);
   PROBE_TS(6);
   if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
