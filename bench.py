@@ -207,6 +207,8 @@ def main():
     ap.add_argument("--e2e-layers", type=int, default=None, help="model layers (default: all)")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--partition", type=int, default=0, help="decode partition tokens (0 = planner's choice)")
+    ap.add_argument("--chunk-partition", type=int, default=0,
+                    help="chunk-row key partition tokens (0 = planner's choice)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
@@ -250,7 +252,7 @@ def main():
 
     t0 = time.perf_counter()
     plan = kernels.Plan(slices_of(case), Q_HEADS, KV_HEADS, HEAD_DIM, BS, kv_dt,
-                        partition_tokens=args.partition)
+                        partition_tokens=args.partition, chunk_partition_tokens=args.chunk_partition)
     pack_us = (time.perf_counter() - t0) * 1e6
     plan.upload()
     torch.cuda.synchronize()
@@ -329,7 +331,7 @@ def main():
     P = plan.plan
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "traffic": measured_traffic(args.workload, args.kv) if args.partition == 0 else None,
+                "traffic": measured_traffic(args.workload, args.kv) if args.partition == 0 and args.chunk_partition == 0 else None,
                 "kernel": "le_ragged_paged_attention ("
                           + ("ragged_kernel: chunk and decode workgroups in one launch"
                              if P.n_chunk_items and P.n_decode_items else

@@ -265,6 +265,7 @@ int ragged_attention(const void* q, le_dtype act_dtype, const void* k_new, const
   c.q_heads = cfg.q_heads; c.kv_heads = cfg.kv_heads; c.head_dim = cfg.head_dim;
   c.block_size = cfg.block_size; c.scale_log2 = scale_log2;
   c.num_cache_blocks = num_cache_blocks;
+  c.l2_local = d.l2_local;
   // A mixed step is one launch (chunk and decode workgroups in one grid);
   // LE_RAGGED_TWO_LAUNCHES=1 runs the two kernels one after the other instead.
   const char* two = std::getenv("LE_RAGGED_TWO_LAUNCHES");  // read per call: tests switch it

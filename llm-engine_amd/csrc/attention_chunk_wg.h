@@ -159,6 +159,7 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
   const int col = lane & 15;  // query row of this lane within a 16-row tile
   const int grp = lane >> 4;  // k-group of this lane
   const ChunkItem it = p.items[item];
+  if (it.n_q <= 0) return;  // padding that keeps split tiles on one XCD
   const int G = p.q_heads / p.kv_heads;
   const bool computes = wave < G;
   const int head = kvh * G + (computes ? wave : 0);
@@ -420,12 +421,18 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
 #pragma unroll
         for (int d = 0; d < DT; d += 2) {
           const uint2 lo = pack_half4(acc[rs][d] * inv), hi = pack_half4(acc[rs][d + 1] * inv);
-          st_coherent16(acc_rsrc, static_cast<uint32_t>((rec - rec_tile) * HD * 4 + ((d / 2) * 4 + grp) * 16),
-                        __builtin_bit_cast(f32x4v, make_uint4(lo.x, lo.y, hi.x, hi.y)));
+          const uint32_t off = static_cast<uint32_t>((rec - rec_tile) * HD * 4 + ((d / 2) * 4 + grp) * 16);
+          const f32x4v v = __builtin_bit_cast(f32x4v, make_uint4(lo.x, lo.y, hi.x, hi.y));
+          if (p.l2_local) st_l2_16(acc_rsrc, off, v);
+          else st_coherent16(acc_rsrc, off, v);
         }
         if (grp == 0) {
-          st_dev(ml + rec * 2, m_run[rs]);
-          st_dev(ml + rec * 2 + 1, l_tot[rs]);
+          if (p.l2_local) {
+            reinterpret_cast<float2*>(ml)[rec] = make_float2(m_run[rs], l_tot[rs]);
+          } else {
+            st_dev(ml + rec * 2, m_run[rs]);
+            st_dev(ml + rec * 2 + 1, l_tot[rs]);
+          }
         }
       }
     }

@@ -35,7 +35,9 @@ __global__ __launch_bounds__(kRaggedThreads) void ragged_kernel(DecodeParams dp,
   const int n_chunk_wg = cp.n_items * cp.kv_heads;
   const int b = blockIdx.x;
   if (b < n_chunk_wg) {
-    chk::chunk_wg<ACT, HD>(cp, sm.c, b / cp.kv_heads, b % cp.kv_heads);
+    // item-major within each kv head, as the chunk kernel's 2-D grid (the
+    // plan places a split tile's partitions at item indices equal modulo 8)
+    chk::chunk_wg<ACT, HD>(cp, sm.c, b % cp.n_items, b / cp.n_items);
   } else {
     // item-major within each kv head, as the decode kernel's 2-D grid: the
     // plan places a split row's partitions at item indices equal modulo 8,

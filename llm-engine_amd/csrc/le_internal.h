@@ -116,6 +116,9 @@ struct ChunkParams {
   int q_heads, kv_heads, head_dim, block_size;
   float scale_log2;
   int64_t num_cache_blocks;
+  // every partition of a split tile runs on one XCD (the plan's placement,
+  // confirmed by xcd_placement_holds): partials go through its L2
+  int l2_local;
 };
 
 hipError_t attention_chunk(const ChunkParams& p, int act_bf16, hipStream_t stream);

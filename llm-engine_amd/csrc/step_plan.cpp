@@ -37,7 +37,11 @@ constexpr int kPartitionQuantum = 128;       // 4 waves x 32-key fp32 tiles
 constexpr int64_t kTargetItems = 512;        // workgroups per step the sizing aims for (two per CU)
 constexpr int kMaxMergeEntries = 1024;       // partitions x group of one decode row (bounds the merge's loads)
 constexpr int kDefaultChunkTile = 32;        // query rows per chunk item (two MFMA row tiles)
-constexpr int kDefaultChunkPartition = 256;  // keys per chunk item: one LDS stage
+// Keys per chunk item: one and a half LDS stages. In the one-launch mixed
+// step, fewer chunk workgroups leave CUs to the decode rows from the start,
+// and fewer partials shorten the tiles' merges (config 3: 256 keys 24.1 us,
+// 320 25.1, 384 22.7, 448 23.4, 512 25.0, 768 31.1).
+constexpr int kDefaultChunkPartition = 384;
 constexpr int kMaxChunkParts = 16;           // partitions of a chunk tile the in-kernel merge stages
 constexpr int kMaxChunkItemBlocks = 1024;
 constexpr int kXcds = 8;                     // MI355X: XCDs, each with its own L2
@@ -51,50 +55,66 @@ int round_to_blocks(int tokens, int bs) {
 }
 
 // The dispatcher sends workgroup i of a launch (linear id) to XCD i % 8, and
-// each XCD has its own L2. A split row's partitions exchange partials and an
-// arrival counter at the end of the launch; with all of them on one XCD that
-// exchange stays in one L2. So the rows (each row's partitions as a unit) are
-// dealt longest-first into kXcds bins, each to the bin with the least work so
-// far, and item k of bin b goes to index k * kXcds + b. Bins are padded to
-// one length with empty items (n_parts 0), so the item count is a multiple of
-// kXcds and the kv head's offset in the grid (a multiple of the item count)
-// keeps every row on its bin's XCD.
-std::vector<le::DecodeItem> place_on_xcds(const std::vector<le::DecodeItem>& dec) {
-  struct Row { size_t first, n; int64_t longest, work; };
-  std::vector<Row> rows;
-  for (size_t i = 0; i < dec.size();) {
+// each XCD has its own L2. The partitions of a split row (decode) or tile
+// (chunk) exchange partials and an arrival counter at the end of the launch;
+// with all of them on one XCD that exchange stays in one L2. So the groups
+// (one row's or tile's partitions) are dealt longest-first into kXcds bins,
+// each to the bin with the least work so far, and item k of bin b goes to
+// index k * kXcds + b. Bins are padded to one length with empty items, so the
+// item count is a multiple of kXcds and the kv head's offset in the grid (a
+// multiple of the item count) keeps every group on its bin's XCD.
+template <typename Item, typename Same, typename Blocks>
+std::vector<Item> place_on_xcds(const std::vector<Item>& items, Same same_group, Blocks blocks, const Item& pad) {
+  struct Group { size_t first, n; int64_t longest, work; };
+  std::vector<Group> groups;
+  for (size_t i = 0; i < items.size();) {
     size_t j = i;
-    Row r{i, 0, 0, 0};
-    while (j < dec.size() && dec[j].token == dec[i].token && dec[j].part_begin == dec[i].part_begin) {
-      const int64_t nb = dec[j].blk_end - dec[j].blk_begin;
-      r.longest = std::max(r.longest, nb);
-      r.work += nb + kItemOverheadBlocks;
+    Group g{i, 0, 0, 0};
+    while (j < items.size() && same_group(items[j], items[i])) {
+      const int64_t nb = blocks(items[j]);
+      g.longest = std::max(g.longest, nb);
+      g.work += nb + kItemOverheadBlocks;
       j++;
     }
-    r.n = j - i;
-    rows.push_back(r);
+    g.n = j - i;
+    groups.push_back(g);
     i = j;
   }
-  std::stable_sort(rows.begin(), rows.end(), [](const Row& a, const Row& b) { return a.longest > b.longest; });
-  std::vector<std::vector<le::DecodeItem>> bins(kXcds);
+  std::stable_sort(groups.begin(), groups.end(), [](const Group& a, const Group& b) { return a.longest > b.longest; });
+  std::vector<std::vector<Item>> bins(kXcds);
   int64_t load[kXcds] = {};
-  for (const Row& r : rows) {
+  for (const Group& g : groups) {
     int b = 0;
     for (int k = 1; k < kXcds; k++)
       if (load[k] < load[b]) b = k;
-    load[b] += r.work;
-    for (size_t k = 0; k < r.n; k++) bins[b].push_back(dec[r.first + k]);
+    load[b] += g.work;
+    for (size_t k = 0; k < g.n; k++) bins[b].push_back(items[g.first + k]);
   }
   size_t len = 0;
   for (const auto& b : bins) len = std::max(len, b.size());
+  std::vector<Item> out(len * kXcds, pad);
+  for (int b = 0; b < kXcds; b++)
+    for (size_t k = 0; k < bins[b].size(); k++) out[k * kXcds + b] = bins[b][k];
+  return out;
+}
+
+std::vector<le::DecodeItem> place_decode_items(const std::vector<le::DecodeItem>& dec) {
   le::DecodeItem pad{};
   pad.token = -1;
   pad.part = -1;
   pad.n_parts = 0;  // resolved as "no work"
-  std::vector<le::DecodeItem> out(len * kXcds, pad);
-  for (int b = 0; b < kXcds; b++)
-    for (size_t k = 0; k < bins[b].size(); k++) out[k * kXcds + b] = bins[b][k];
-  return out;
+  return place_on_xcds(
+      dec, [](const le::DecodeItem& a, const le::DecodeItem& b) { return a.token == b.token && a.part_begin == b.part_begin; },
+      [](const le::DecodeItem& d) { return static_cast<int64_t>(d.blk_end - d.blk_begin); }, pad);
+}
+
+std::vector<le::ChunkItem> place_chunk_items(const std::vector<le::ChunkItem>& chk) {
+  le::ChunkItem pad{};
+  pad.n_q = 0;  // no rows: the workgroup returns at once
+  pad.part0 = -1;
+  return place_on_xcds(
+      chk, [](const le::ChunkItem& a, const le::ChunkItem& b) { return a.tok_begin == b.tok_begin; },
+      [](const le::ChunkItem& c) { return static_cast<int64_t>(c.blk_end - c.blk_begin); }, pad);
 }
 
 }  // namespace
@@ -235,15 +255,21 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
   // launch order, so the items on the critical path (most keys) go first.
   // Merges do not depend on the order (partials are addressed by index).
   if (parts > 0) {
-    dec = place_on_xcds(dec);
+    dec = place_decode_items(dec);
   } else {
     std::stable_sort(dec.begin(), dec.end(), [](const le::DecodeItem& a, const le::DecodeItem& b) {
       return a.blk_end - a.blk_begin > b.blk_end - b.blk_begin;
     });
   }
-  std::stable_sort(chk.begin(), chk.end(), [](const le::ChunkItem& a, const le::ChunkItem& b) {
-    return a.blk_end - a.blk_begin > b.blk_end - b.blk_begin;
-  });
+  bool chunk_split = false;
+  for (const auto& c : chk) chunk_split |= c.part0 >= 0;
+  if (chunk_split) {
+    chk = place_chunk_items(chk);
+  } else {
+    std::stable_sort(chk.begin(), chk.end(), [](const le::ChunkItem& a, const le::ChunkItem& b) {
+      return a.blk_end - a.blk_begin > b.blk_end - b.blk_begin;
+    });
+  }
 
   // ---- layout: every array 256-byte aligned in one buffer ----
   le_step_plan P{};

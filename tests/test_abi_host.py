@@ -101,11 +101,19 @@ def check_work_lists(plan, slices, bs=16):
             assert sorted(i[2] for i in items) == list(range(items[0][3], items[0][3] + npart))
     # chunk items: each tile's partitions tile the keys up to its last row,
     # numbered 0..J-1 in key order, with part0 = base + j
-    tiles = {}
-    for it in chk:
+    tiles, tile_bins = {}, {}
+    for k, it in enumerate(chk):
         tb, nq, b0, b1, p0, stride, seq, part = (int(x) for x in it)
+        if nq == 0:  # padding that keeps split tiles on one XCD
+            assert b0 == b1 and p0 == -1
+            continue
         assert 1 <= nq <= 32 and all(pos[tb + r] == pos[tb] + r for r in range(nq))
         tiles.setdefault(tb, []).append((b0, b1, p0, stride, nq, part))
+        if p0 >= 0:  # a split tile's partitions sit at indices equal modulo 8 (one XCD)
+            tile_bins.setdefault(tb, set()).add(k % 8)
+    assert all(len(b) == 1 for b in tile_bins.values())
+    if tile_bins:
+        assert len(chk) % 8 == 0
     for tb, items in tiles.items():
         items.sort()
         nq, J = items[0][4], items[0][3]
