@@ -135,6 +135,82 @@ template <int HD> struct ChunkSmem {
   int last;
 };
 
+// The last partition's merge of a split tile. Each thread owns kMG output
+// 8-vectors (a row, a head, 8 dims) and merges their partials itself, kMJ
+// partitions per round of loads: the partition's (m, l) for the row and head,
+// and its normalised output, requested together, then folded in partition
+// order into a running (max, sum) with rescaling. With at most kMJ
+// partitions the whole merge is one memory round trip, with no LDS phase or
+// barrier.
+template <typename ACT, int HD, int kMJ>
+__device__ __forceinline__ void merge_tile(const ChunkParams& p, const ChunkItem& it, __amdgpu_buffer_rsrc_t acc_rsrc,
+                                           float* ml, int64_t rec_tile, int base, int J, int G, int kvh, int nq,
+                                           int tok0) {
+  constexpr int kMG = 4;  // output 8-vectors per thread and round
+  const int tid = threadIdx.x;
+  const int per_row = G * (HD / 8);
+  const int n_out = nq * per_row;
+  for (int o0 = tid; o0 < n_out; o0 += kMG * kThreads) {
+    int64_t rec_base[kMG];
+    int d8[kMG];
+    float M[kMG], L[kMG], sum[kMG][8];
+#pragma unroll
+    for (int gi = 0; gi < kMG; gi++) {
+      const int o = min(o0 + gi * kThreads, n_out - 1);
+      const int r = o / per_row, rem = o - r * per_row;
+      const int g = rem / (HD / 8);
+      d8[gi] = rem - g * (HD / 8);
+      rec_base[gi] = static_cast<int64_t>(base + r * J) * p.q_heads + kvh * G + g;
+      M[gi] = -FLT_MAX;
+      L[gi] = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; e++) sum[gi][e] = 0.f;
+    }
+    for (int j0 = 0; j0 < J; j0 += kMJ) {
+      uint4 x[kMG][kMJ];
+      float mj[kMG][kMJ], lj[kMG][kMJ];
+#pragma unroll
+      for (int gi = 0; gi < kMG; gi++)
+#pragma unroll
+        for (int jj = 0; jj < kMJ; jj++) {
+          const int64_t rec = rec_base[gi] + static_cast<int64_t>(min(j0 + jj, J - 1)) * p.q_heads;
+          x[gi][jj] = ld_coherent16u(acc_rsrc, static_cast<uint32_t>((rec - rec_tile) * HD * 4 + d8[gi] * 16));
+          mj[gi][jj] = ld_dev(ml + rec * 2);
+          lj[gi][jj] = ld_dev(ml + rec * 2 + 1);
+        }
+#pragma unroll
+      for (int gi = 0; gi < kMG; gi++)
+#pragma unroll
+        for (int jj = 0; jj < kMJ; jj++)
+          if (j0 + jj < J) {
+            // partition j holds o_j / l_j (fp16); fold in l_j * o_j at weight exp2(m_j - max)
+            const float m_new = fmaxf(M[gi], mj[gi][jj]);
+            const float a = __builtin_amdgcn_exp2f(M[gi] - m_new), w = __builtin_amdgcn_exp2f(mj[gi][jj] - m_new) * lj[gi][jj];
+            M[gi] = m_new;
+            L[gi] = L[gi] * a + w;
+            float f[8];
+            unpack_half8(x[gi][jj], f);
+#pragma unroll
+            for (int e = 0; e < 8; e++) sum[gi][e] = sum[gi][e] * a + w * f[e];
+          }
+    }
+#pragma unroll
+    for (int gi = 0; gi < kMG; gi++) {
+      const int o = o0 + gi * kThreads;
+      if (o < n_out) {
+        const int r = o / per_row, rem = o - r * per_row;
+        const int g = rem / (HD / 8);
+        // piece d8 = (d / 2) * 4 + g4: dims (d8 / 4) * 32 + (d8 % 4) * 4 .. +4, then +16
+        ACT* out = static_cast<ACT*>(p.out) + (static_cast<int64_t>(tok0 + r) * p.q_heads + kvh * G + g) * HD +
+                   (d8[gi] >> 2) * 32 + (d8[gi] & 3) * 4;
+        const float inv = 1.f / L[gi];
+        store4<ACT>(out, f32x4{sum[gi][0], sum[gi][1], sum[gi][2], sum[gi][3]} * inv);
+        store4<ACT>(out + 16, f32x4{sum[gi][4], sum[gi][5], sum[gi][6], sum[gi][7]} * inv);
+      }
+    }
+  }
+}
+
 // One chunk workgroup (kThreads threads): chunk item `item`, kv head `kvh`.
 // Shared by the chunk kernel and the fused ragged kernel.
 template <typename ACT, int HD>
@@ -452,76 +528,16 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
 #endif
 
   // Every other partition incremented the counter after its partials were
-  // performed, so the coherent loads below see all of them. Each thread owns
-  // kMG output 8-vectors (a row, a head, 8 dims) and merges their partials
-  // itself, kMJ partitions per round of loads: the partition's (m, l) for the
-  // row and head, and its normalised output, requested together, then folded
-  // in partition order into a running (max, sum) with rescaling. With at
-  // most kMJ partitions the whole merge is one memory round trip, with no
-  // LDS phase or barrier.
+  // performed, so the coherent loads of the merge see all of them.
   const int J = it.part_stride;
   const int base = it.part0 - it.part;
-  constexpr int kMG = 4, kMJ = HD == 64 ? 6 : 3;  // output 8-vectors x partitions per round
-  const int per_row = G * (HD / 8);
-  const int n_out = nq * per_row;
-  for (int o0 = tid; o0 < n_out; o0 += kMG * kThreads) {
-    int64_t rec_base[kMG];
-    int d8[kMG];
-    float M[kMG], L[kMG], sum[kMG][8];
-#pragma unroll
-    for (int gi = 0; gi < kMG; gi++) {
-      const int o = min(o0 + gi * kThreads, n_out - 1);
-      const int r = o / per_row, rem = o - r * per_row;
-      const int g = rem / (HD / 8);
-      d8[gi] = rem - g * (HD / 8);
-      rec_base[gi] = static_cast<int64_t>(base + r * J) * p.q_heads + kvh * G + g;
-      M[gi] = -FLT_MAX;
-      L[gi] = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; e++) sum[gi][e] = 0.f;
-    }
-    for (int j0 = 0; j0 < J; j0 += kMJ) {
-      uint4 x[kMG][kMJ];
-      float mj[kMG][kMJ], lj[kMG][kMJ];
-#pragma unroll
-      for (int gi = 0; gi < kMG; gi++)
-#pragma unroll
-        for (int jj = 0; jj < kMJ; jj++) {
-          const int64_t rec = rec_base[gi] + static_cast<int64_t>(min(j0 + jj, J - 1)) * p.q_heads;
-          x[gi][jj] = ld_coherent16u(acc_rsrc, static_cast<uint32_t>((rec - rec_tile) * HD * 4 + d8[gi] * 16));
-          mj[gi][jj] = ld_dev(ml + rec * 2);
-          lj[gi][jj] = ld_dev(ml + rec * 2 + 1);
-        }
-#pragma unroll
-      for (int gi = 0; gi < kMG; gi++)
-#pragma unroll
-        for (int jj = 0; jj < kMJ; jj++)
-          if (j0 + jj < J) {
-            // partition j holds o_j / l_j (fp16); fold in l_j * o_j at weight exp2(m_j - max)
-            const float m_new = fmaxf(M[gi], mj[gi][jj]);
-            const float a = __builtin_amdgcn_exp2f(M[gi] - m_new), w = __builtin_amdgcn_exp2f(mj[gi][jj] - m_new) * lj[gi][jj];
-            M[gi] = m_new;
-            L[gi] = L[gi] * a + w;
-            float f[8];
-            unpack_half8(x[gi][jj], f);
-#pragma unroll
-            for (int e = 0; e < 8; e++) sum[gi][e] = sum[gi][e] * a + w * f[e];
-          }
-    }
-#pragma unroll
-    for (int gi = 0; gi < kMG; gi++) {
-      const int o = o0 + gi * kThreads;
-      if (o < n_out) {
-        const int r = o / per_row, rem = o - r * per_row;
-        const int g = rem / (HD / 8);
-        // piece d8 = (d / 2) * 4 + g4: dims (d8 / 4) * 32 + (d8 % 4) * 4 .. +4, then +16
-        ACT* out = static_cast<ACT*>(p.out) + (static_cast<int64_t>(tok0 + r) * p.q_heads + kvh * G + g) * HD +
-                   (d8[gi] >> 2) * 32 + (d8[gi] & 3) * 4;
-        const float inv = 1.f / L[gi];
-        store4<ACT>(out, f32x4{sum[gi][0], sum[gi][1], sum[gi][2], sum[gi][3]} * inv);
-        store4<ACT>(out + 16, f32x4{sum[gi][4], sum[gi][5], sum[gi][6], sum[gi][7]} * inv);
-      }
-    }
+  // Rounds of loads as wide as the tile's partition count (up to 6 for hd
+  // 64), so no load is issued twice.
+  if constexpr (HD == 64) {
+    if (J <= 4) merge_tile<ACT, HD, 4>(p, it, acc_rsrc, ml, rec_tile, base, J, G, kvh, nq, tok0);
+    else merge_tile<ACT, HD, 6>(p, it, acc_rsrc, ml, rec_tile, base, J, G, kvh, nq, tok0);
+  } else {
+    merge_tile<ACT, HD, 3>(p, it, acc_rsrc, ml, rec_tile, base, J, G, kvh, nq, tok0);
   }
   CHUNK_TS(6);
   if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
