@@ -59,7 +59,10 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * kWave;
 constexpr int kTileKeys = 64;    // keys per MFMA tile
-constexpr int kStageKeys = 256;  // keys staged in LDS at once
+// Keys staged in LDS at once: 384 for head_dim 64 (110 KB of K and V rows,
+// so a default 384-key partition is one memory round trip), 256 for
+// head_dim 128 (139 KB).
+template <int HD> constexpr int kStageKeys = HD == 64 ? 384 : 256;
 constexpr int kRowsMax = 32;     // query rows per item
 constexpr int kMaxG = 8;         // query heads per kv head
 constexpr int kMaxSplit = 16;    // partitions of one tile the merge stages in LDS
@@ -73,7 +76,7 @@ __device__ __forceinline__ float vmax3(float a, float b, float c) {
 
 template <int HD> struct ChunkLds {
   static constexpr int ROW = HD * 2 + 16;  // bytes per key row of K and of V (padded)
-  static constexpr int K_BYTES = kStageKeys * ROW;
+  static constexpr int K_BYTES = kStageKeys<HD> * ROW;
   static constexpr int BYTES = 2 * K_BYTES;  // K rows, then V rows
 };
 
@@ -219,7 +222,7 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
   constexpr int KS = HD / 32;  // MFMA k-steps over head dims
   constexpr int DT = HD / 16;  // 16-dim output tiles
   constexpr int CPR = HD / 8;  // 16-byte pieces per K/V row
-  constexpr int PIECES = 2 * kStageKeys * CPR;
+  constexpr int PIECES = 2 * kStageKeys<HD> * CPR;
   constexpr int PER = PIECES / kThreads;  // 16-byte loads per thread per stage
   static_assert(PER * kThreads == PIECES && PER % 2 == 0, "staging split");
   static_assert(kRowsMax * kMaxG * kMaxSplit * (sizeof(float2) + sizeof(float)) <= L::BYTES,
@@ -259,27 +262,33 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
   // scores are masked, and a zero V row keeps p * v finite.
   uint4 kv[2][PER / 2];
   bool okp[PER / 2];
-  int dst[PER / 2];
   auto issue = [&](int rel0) {
 #pragma unroll
     for (int k = 0; k < PER / 2; k++) {
       const int piece = tid + k * kThreads;
       const int key_l = piece / CPR, c = piece - key_l * CPR;
+      // a piece past the item reads the item's last key instead (a line the
+      // workgroup loads anyway), not one shared address that every
+      // workgroup's surplus pieces would pile onto
       const int rel = rel0 + key_l;
-      const int bid = ids[min(rel >> bs_shift, p.ids_stride - 1)];
-      okp[k] = rel < n_keys_blk && bid >= 0 && bid < p.num_cache_blocks;
-      const int64_t slot = (static_cast<int64_t>(okp[k] ? bid : 0) << bs_shift) + (rel & bs_mask);
+      const int relc = min(rel, n_keys_blk - 1);
+      const int bid = ids[min(relc >> bs_shift, p.ids_stride - 1)];
+      const bool bid_ok = bid >= 0 && bid < p.num_cache_blocks;
+      okp[k] = rel < n_keys_blk && bid_ok;
+      const int64_t slot = (static_cast<int64_t>(bid_ok ? bid : 0) << bs_shift) + (relc & bs_mask);
       const int64_t off = (slot * kv_stride + kvh * HD + c * 8) * 2;
       kv[0][k] = ld16_stream(kbase + off);
       kv[1][k] = ld16_stream(vbase + off);
-      dst[k] = key_l * L::ROW + c * 16;
     }
   };
   auto stash = [&]() {
 #pragma unroll
     for (int k = 0; k < PER / 2; k++) {
-      *reinterpret_cast<uint4*>(lds + dst[k]) = okp[k] ? kv[0][k] : make_uint4(0, 0, 0, 0);
-      *reinterpret_cast<uint4*>(lds + L::K_BYTES + dst[k]) = okp[k] ? kv[1][k] : make_uint4(0, 0, 0, 0);
+      const int piece = tid + k * kThreads;  // as in issue(): the LDS place is recomputed, not kept
+      const int key_l = piece / CPR, c = piece - key_l * CPR;
+      const int dst = key_l * L::ROW + c * 16;
+      *reinterpret_cast<uint4*>(lds + dst) = okp[k] ? kv[0][k] : make_uint4(0, 0, 0, 0);
+      *reinterpret_cast<uint4*>(lds + L::K_BYTES + dst) = okp[k] ? kv[1][k] : make_uint4(0, 0, 0, 0);
     }
   };
   // Query rows first (they are needed last, and a wait for them must not
@@ -343,7 +352,7 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
 #endif
       const int key_end = min(key_begin + n_keys_blk, pos0 + nq);  // past the last row's position: dead
 #pragma unroll 1
-      for (int kt = 0; kt < kStageKeys / kTileKeys; kt++) {
+      for (int kt = 0; kt < kStageKeys<HD> / kTileKeys; kt++) {
         const int t0 = s0 + kt * kTileKeys;
         if (t0 >= key_end) break;
         const char* kt_lds = lds + kt * kTileKeys * L::ROW;
@@ -443,7 +452,7 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
         }
       }
     }
-    rel0 += kStageKeys;
+    rel0 += kStageKeys<HD>;
     CHUNK_TS(3);
     if (rel0 >= n_keys_blk) break;
     __syncthreads();  // the stage is no longer read
