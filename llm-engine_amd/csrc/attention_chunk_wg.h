@@ -15,7 +15,7 @@
 //     partition); wave w computes query head kv_head*G + w for all 32 rows
 //     (two 16-row MFMA tiles), so one LDS copy of the keys serves the whole
 //     GQA group and both row tiles;
-//   * a partition's keys are staged 256 at a time: every thread issues its
+//   * a partition's keys are staged 384 (head_dim 128: 256) at a time: every thread issues its
 //     16-byte K and V loads at once (block ids come from the plan, fetched in
 //     the same round trip as the item), so a stage costs one memory latency;
 //     K and V rows land row-major in LDS;
