@@ -63,7 +63,7 @@ __device__ int g_xcd_probe[kProbeW * kProbeH];  // static: the check allocates n
 int probe_placement(hipStream_t stream) {
   int* d = nullptr;
   if (hipGetSymbolAddress(reinterpret_cast<void**>(&d), HIP_SYMBOL(g_xcd_probe)) != hipSuccess) return 0;
-  static int h[kProbeW * kProbeH];
+  int h[kProbeW * kProbeH];  // the caller's own copy: concurrent probes of two devices do not share it
   bool ok = true;
   for (int shape = 0; shape < 2 && ok; shape++) {
     const dim3 grid = shape == 0 ? dim3(kProbeW * kProbeH) : dim3(kProbeW, kProbeH);
