@@ -372,3 +372,43 @@ def test_split_rows_both_partial_paths(gpu, monkeypatch, kv_bf16):
                   f"decode items {plan.plan.n_decode_items} max|err| {err:.3e}")
             assert plan.plan.n_parts > 0 and plan.plan.n_decode_items % 8 == 0
             assert err < tol_for(kv_bf16, torch.float32)
+
+
+def test_graph_replays_match_eager(gpu):
+    """The ragged attention captured in a HIP graph (plan upload not included)
+    and replayed several times, with eager launches sharing the workspace in
+    between: every replay equals the eager output bit for bit (partials merge
+    in partition order whatever the arrival order), and the oracle within
+    tolerance. The launch allocates and clears nothing, and its arrival
+    counters reset themselves, so replays need no workspace reset."""
+    from llm_engine_amd import kernels
+    ctx = [2900, 40, 1800, 3500, 700, 1300]
+    q_len = [1, 40, 1, 1, 96, 1]
+    case = make_case(ctx, q_len=q_len, num_blocks=2048, seed=91, kv_bf16=True)
+    q, qh = device_q(case, torch.float32, gpu)
+    kc, vc = to_dev_cache(case.k_cache, gpu), to_dev_cache(case.v_cache, gpu)
+    plan = kernels.Plan(slices_of(case), case.q_heads, case.kv_heads, case.head_dim, case.block_size,
+                        kc.dtype, partition_tokens=640).upload()
+    assert plan.plan.n_chunk_items > 0 and plan.plan.n_parts > 0
+    ws = kernels.new_workspace(plan.workspace_size(), gpu)
+    eager = kernels.ragged_paged_attention(q, kc, vc, plan, case.scale, workspace=ws)
+    torch.cuda.synchronize()
+    want = oracle_out(case, qh)
+    assert max_abs(eager.float().cpu().numpy(), want) < TOL_BF16
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    out = torch.empty_like(eager)
+    with torch.cuda.stream(s):
+        kernels.ragged_paged_attention(q, kc, vc, plan, case.scale, out=out, workspace=ws, stream=s)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            kernels.ragged_paged_attention(q, kc, vc, plan, case.scale, out=out, workspace=ws, stream=s)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {rep} differs from the eager launch"
+        again = kernels.ragged_paged_attention(q, kc, vc, plan, case.scale, workspace=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(again, eager)
