@@ -288,42 +288,47 @@ __device__ __forceinline__ void merge_parts(const DecodeParams& p, __amdgpu_buff
   }
 }
 
-// Final stage shared by both kernels. fin_acc[g * HD + d] holds the
-// workgroup's unnormalised output for head g of the group, fin_ml[g] its
-// (max, sum). Writes the output (single partition) or the partial, and in the
-// latter case the last arriving workgroup of the row merges all partials.
-template <typename ACT, int HD, int NTHR>
-__device__ __forceinline__ void finish(const DecodeParams& p, const Work& w, int G, int kvh,
-                                       const float* fin_acc, const float2* fin_ml, int* flag) {
-  const int tid = threadIdx.x;
-  const int64_t head0 = static_cast<int64_t>(w.token) * p.q_heads + kvh * G;
+// Final stage, per 16-byte piece (4 dims of head g): the workgroup's
+// unnormalised output o and the head's (m, l). A single-partition row writes
+// its normalised output; a split row writes the piece of its partial (head g
+// of partition part is record part * q_heads + kvh * G + g: HD fp32
+// accumulators, then the (m, l) pairs beside).
+template <typename ACT, int HD>
+__device__ __forceinline__ void write_piece(const DecodeParams& p, const Work& w, int G, int kvh, int c, f32x4 o,
+                                            float M, float Ls) {
+  const int g = c * 4 / HD;
   if (w.part < 0) {
-    for (int i = tid; i < G * HD; i += NTHR) {
-      const int g = i / HD;
-      elem<ACT>::store1(static_cast<ACT*>(p.out) + head0 * HD + i, fin_acc[i] / fin_ml[g].y);
-    }
+    ACT* out = static_cast<ACT*>(p.out) + (static_cast<int64_t>(w.token) * p.q_heads + kvh * G) * HD + c * 4;
+    const float inv = 1.f / Ls;
+#pragma unroll
+    for (int e = 0; e < 4; e++) elem<ACT>::store1(out + e, o[e] * inv);
     return;
   }
-  // The partial: the group's G records (head g of partition part is record
-  // part * q_heads + kvh * G + g) of HD fp32 accumulators, contiguous, written
-  // in 16-byte pieces; its (m, l) pairs beside.
-  const int n4 = G * HD / 4;
   const int64_t rec0 = static_cast<int64_t>(w.part) * p.q_heads + kvh * G;
   float* ml = reinterpret_cast<float*>(p.parts.ml);
+  const __amdgpu_buffer_rsrc_t r = coherent_rsrc(p.parts.acc + rec0 * HD);
+  const bool first = c * 4 - g * HD == 0;  // the head's first piece also writes (m, l)
   if (p.l2_local) {  // partitions of the row share this XCD's L2
-    const __amdgpu_buffer_rsrc_t r = coherent_rsrc(p.parts.acc + rec0 * HD);
-    for (int c = tid; c < n4; c += NTHR)
-      st_l2_16(r, static_cast<uint32_t>(c * 16), *reinterpret_cast<const f32x4*>(fin_acc + c * 4));
-    if (tid < G) reinterpret_cast<float2*>(ml)[rec0 + tid] = fin_ml[tid];
+    st_l2_16(r, static_cast<uint32_t>(c * 16), o);
+    if (first) reinterpret_cast<float2*>(ml)[rec0 + g] = make_float2(M, Ls);
   } else {
-    const __amdgpu_buffer_rsrc_t r = coherent_rsrc(p.parts.acc + rec0 * HD);
-    for (int c = tid; c < n4; c += NTHR)
-      st_coherent16(r, static_cast<uint32_t>(c * 16), *reinterpret_cast<const f32x4*>(fin_acc + c * 4));
-    if (tid < G) {
-      st_dev(ml + (rec0 + tid) * 2, fin_ml[tid].x);
-      st_dev(ml + (rec0 + tid) * 2 + 1, fin_ml[tid].y);
+    st_coherent16(r, static_cast<uint32_t>(c * 16), o);
+    if (first) {
+      st_dev(ml + (rec0 + g) * 2, M);
+      st_dev(ml + (rec0 + g) * 2 + 1, Ls);
     }
   }
+}
+
+// After every piece is written: a split row's partitions arrive on the
+// row's counter, and the last to arrive merges all partials.
+template <typename ACT, int HD, int NTHR>
+__device__ __forceinline__ void arrive_and_merge(const DecodeParams& p, const Work& w, int G, int kvh, int* flag) {
+  if (w.part < 0) return;
+  const int tid = threadIdx.x;
+  const int n4 = G * HD / 4;
+  const int64_t head0 = static_cast<int64_t>(w.token) * p.q_heads + kvh * G;
+  float* ml = reinterpret_cast<float*>(p.parts.ml);
 #ifndef LE_PROBE_NOSTOREWAIT  // measurement variant: results may be stale
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are performed
 #endif
@@ -731,8 +736,6 @@ template <int HD> struct DecodeTile<float, HD> {
 template <typename KV, int HD, int NW> struct DecodeSmem {
   using L = MfmaLds<HD, DecodeTile<KV, HD>::VT_BYTES, NW>;
   __attribute__((aligned(16))) char lds[L::BYTES];
-  float fin_acc[kMaxG * HD];
-  float2 fin_ml[kMaxG];
   int tab[kTabCap];
   int flag;
 };
@@ -749,8 +752,6 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
   constexpr int DT = HD / 16;  // 16-dim output tiles
   constexpr bool kPipe = T::kPipe;
   char* lds = sm.lds;
-  float* fin_acc = sm.fin_acc;
-  float2* fin_ml = sm.fin_ml;
   int* tab = sm.tab;
 
   PROBE_TS(0);
@@ -907,31 +908,31 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
     if (grp == 0) { r[HD] = st.m; r[HD + 1] = l_tot; }
   }
   __syncthreads();
-  // each output element folds the waves' (m, l) itself: no separate phase
-  // (and barrier) for the per-head statistics
-  for (int i = tid; i < G * HD; i += kMfmaThreads) {
-    const int g = i / HD, d = i - g * HD;
+  // Each thread folds the waves' partial results for one 16-byte piece (4
+  // dims of a head), with the head's (m, l), and writes the piece straight
+  // to the output or the partial: no LDS copy of the folded result and no
+  // barrier before the stores.
+  for (int c = tid; c < G * HD / 4; c += kMfmaThreads) {
+    const int g = c * 4 / HD, d0 = c * 4 - g * HD;
     float M = -FLT_MAX;
 #pragma unroll
     for (int v = 0; v < kMfmaWaves; v++) M = fmaxf(M, red[(v * kMaxG + g) * L::RED_STRIDE + HD]);
-    float o = 0.f, Ls = 0.f;
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+    float Ls = 0.f;
 #pragma unroll
     for (int v = 0; v < kMfmaWaves; v++) {
       const float* r = red + (v * kMaxG + g) * L::RED_STRIDE;
       const float e = __builtin_amdgcn_exp2f(r[HD] - M);
-      o += r[d] * e;
+      o += *reinterpret_cast<const f32x4*>(r + d0) * e;
       Ls += r[HD + 1] * e;
     }
-    fin_acc[i] = o;
-    if (d == 0) fin_ml[g] = make_float2(M, Ls);
+    write_piece<ACT, HD>(p, w, G, kvh, c, o, M, Ls);
   }
-  __syncthreads();
   PROBE_TS(3);
 #ifdef LE_PROBE_NOCROSS  // measurement variant: the four-wave merge only
-  if (fin_acc[tid] == 12345.f) static_cast<float*>(p.out)[0] = 0.f;
   return;
 #endif
-  finish<ACT, HD, kMfmaThreads>(p, w, G, kvh, fin_acc, fin_ml, &sm.flag);
+  arrive_and_merge<ACT, HD, kMfmaThreads>(p, w, G, kvh, &sm.flag);
   PROBE_TS(7);
 }
 }  // namespace
