@@ -48,6 +48,8 @@ extern "C" {
 #define LE_EINVAL (-1)       /* a pointer, size or shape is invalid */
 #define LE_EUNSUPPORTED (-2) /* valid, but outside what the kernels are built for */
 #define LE_ENOSPACE (-3)     /* a caller buffer (host plan buffer, workspace) is too small */
+#define LE_EDEVICE (-4)      /* a device library call (rocBLAS) failed; a failed HIP call
+                                returns its positive hipError_t instead */
 
 typedef enum le_dtype { LE_F32 = 0, LE_BF16 = 1 } le_dtype;
 
@@ -147,7 +149,16 @@ typedef struct le_plan_config {
   int32_t partition_tokens;    /* split-K partition of decode rows; 0 = default */
   int32_t chunk_q_tile;        /* query rows per chunk tile (16 or 32); 0 = default (32) */
   int32_t chunk_partition_tokens; /* key partition of chunk tiles; 0 = default */
+  int32_t flags;               /* LE_PLAN_* bits below; 0 = the defaults */
+  int32_t reserved_;           /* must be 0 */
 } le_plan_config;
+
+/* le_plan_config.flags. Both select slower, equivalent launches; the tests
+ * use them to check that every launch shape gives the same result. */
+#define LE_PLAN_WRITE_THROUGH 1 /* split rows exchange partials through write-through
+                                   stores, without relying on the XCD placement */
+#define LE_PLAN_TWO_LAUNCHES 2  /* a mixed step runs its decode and chunk rows as two
+                                   launches instead of one */
 
 typedef struct le_step_plan {
   le_plan_config cfg;

@@ -4,7 +4,6 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
-#include <cstdlib>
 #include <cstring>
 
 #include "le_internal.h"
@@ -77,6 +76,7 @@ const char* le_status_string(int status) {
     case LE_EINVAL: return "invalid argument";
     case LE_EUNSUPPORTED: return "unsupported shape";
     case LE_ENOSPACE: return "buffer too small";
+    case LE_EDEVICE: return "device library failure";
     default: return status > 0 ? hipGetErrorString(static_cast<hipError_t>(status)) : "unknown";
   }
 }
@@ -224,10 +224,7 @@ int ragged_attention(const void* q, le_dtype act_dtype, const void* k_new, const
   d.n_rows = plan->n_decode_items; d.nsplit = 1;
   d.q_heads = cfg.q_heads; d.kv_heads = cfg.kv_heads; d.head_dim = cfg.head_dim;
   d.block_size = cfg.block_size; d.scale_log2 = scale_log2; d.num_cache_blocks = num_cache_blocks;
-  // LE_DECODE_COHERENT=1 keeps the write-through partials (read per call:
-  // tests run both paths)
-  const char* coh = std::getenv("LE_DECODE_COHERENT");
-  d.l2_local = plan->n_parts > 0 && !(coh && coh[0] == '1') && le::xcd_placement_holds(stream);
+  d.l2_local = plan->n_parts > 0 && !(cfg.flags & LE_PLAN_WRITE_THROUGH) && le::xcd_placement_holds(stream);
   const int64_t num_slots = num_cache_blocks * cfg.block_size;
   hipError_t e = hipSuccess;
   if (k_new) {
@@ -267,9 +264,8 @@ int ragged_attention(const void* q, le_dtype act_dtype, const void* k_new, const
   c.num_cache_blocks = num_cache_blocks;
   c.l2_local = d.l2_local;
   // A mixed step is one launch (chunk and decode workgroups in one grid);
-  // LE_RAGGED_TWO_LAUNCHES=1 runs the two kernels one after the other instead.
-  const char* two = std::getenv("LE_RAGGED_TWO_LAUNCHES");  // read per call: tests switch it
-  const bool two_launches = two && two[0] == '1';
+  // LE_PLAN_TWO_LAUNCHES runs the two kernels one after the other instead.
+  const bool two_launches = (cfg.flags & LE_PLAN_TWO_LAUNCHES) != 0;
   if (plan->n_decode_items > 0 && !two_launches)
     return hip_status(le::attention_ragged(d, c, act_dtype == LE_BF16, stream));
   e = le::attention_decode(d, act_dtype == LE_BF16, kv_dtype == LE_BF16, stream);

@@ -15,15 +15,6 @@ __global__ __launch_bounds__(chk::kThreads) void chunk_kernel(ChunkParams p) {
 
 }  // namespace
 
-#ifdef LE_PROBE_TIMING
-extern "C" int le_probe_chunk_timing(void* host, size_t bytes) {
-  return hipMemcpyFromSymbol(host, HIP_SYMBOL(chk::g_chunk_ts), bytes < sizeof(chk::g_chunk_ts) ? bytes : sizeof(chk::g_chunk_ts)) == hipSuccess ? 0 : 1;
-}
-extern "C" int le_probe_chunk_timing_clear(void) {
-  static uint64_t zeros[8192][8];
-  return hipMemcpyToSymbol(HIP_SYMBOL(chk::g_chunk_ts), zeros, sizeof(zeros)) == hipSuccess ? 0 : 1;
-}
-#endif
 
 hipError_t attention_chunk(const ChunkParams& p, int act_bf16, hipStream_t s) {
   if (p.n_items <= 0) return hipSuccess;

@@ -101,14 +101,6 @@ __device__ __forceinline__ float ld_dev(const float* p) {
                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
 }
 
-#ifdef LE_PROBE_TIMING
-// Diagnostic build only: per-workgroup phase timestamps (100 MHz counter).
-__device__ uint64_t g_chunk_ts[8192][8];
-#define CHUNK_TS(k) do { if (threadIdx.x == 0 && kvh == 0 && item < 8192) \
-    g_chunk_ts[item][k] = __builtin_amdgcn_s_memrealtime(); } while (0)
-#else
-#define CHUNK_TS(k) do {} while (0)
-#endif
 
 // fp16 (round to nearest even) transport of normalised partial outputs.
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
@@ -231,7 +223,6 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
   char* lds = sm.lds;
   int& last = sm.last;
 
-  CHUNK_TS(0);
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
@@ -307,7 +298,6 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
       for (int h = 0; h < static_cast<int>(sizeof(ACT) / 2); h++) qraw[rs][ks][h] = ld16(q + ks * 32 + h * (16 / sizeof(ACT)));
   }
   issue(0);
-  CHUNK_TS(1);
   // Q^T operands: this lane's 8 dims per k-step of rows col and 16 + col.
   bf16x8 qb[2][KS];
 #pragma unroll
@@ -326,7 +316,6 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
       for (int e = 0; e < 8; e++) qb[rs][ks][e] = static_cast<__bf16>(ok ? f[e] : 0.f);
     }
   }
-  CHUNK_TS(7);
 
   f32x4 acc[2][DT];
 #pragma unroll
@@ -343,13 +332,8 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
   for (int rel0 = 0;;) {
     stash();
     __syncthreads();
-    CHUNK_TS(2);
     const int s0 = key_begin + rel0;
-#ifdef LE_CHUNK_PROBE_NOCOMPUTE
-    if (computes && s0 < 0) {
-#else
     if (computes) {
-#endif
       const int key_end = min(key_begin + n_keys_blk, pos0 + nq);  // past the last row's position: dead
 #pragma unroll 1
       for (int kt = 0; kt < kStageKeys<HD> / kTileKeys; kt++) {
@@ -453,7 +437,6 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
       }
     }
     rel0 += kStageKeys<HD>;
-    CHUNK_TS(3);
     if (rel0 >= n_keys_blk) break;
     __syncthreads();  // the stage is no longer read
     issue(rel0);
@@ -524,17 +507,11 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
   }
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are performed
   __syncthreads();                // ... and every other thread's
-  CHUNK_TS(4);
   int32_t* counter = p.parts.counters + static_cast<int64_t>(tok0) * p.kv_heads + kvh;
   if (tid == 0)
     last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == it.part_stride - 1;
   __syncthreads();
-  CHUNK_TS(5);
   if (!last) return;
-#ifdef LE_CHUNK_PROBE_NOMERGE
-  if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return;
-#endif
 
   // Every other partition incremented the counter after its partials were
   // performed, so the coherent loads of the merge see all of them.
@@ -548,7 +525,6 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
   } else {
     merge_tile<ACT, HD, 3>(p, it, acc_rsrc, ml, rec_tile, base, J, G, kvh, nq, tok0);
   }
-  CHUNK_TS(6);
   if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 }  // namespace

@@ -52,14 +52,6 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-#ifdef LE_PROBE_TIMING
-// Diagnostic build only: per-workgroup phase timestamps (100 MHz counter).
-__device__ uint64_t g_probe_ts[16384][8];
-#define PROBE_TS(k) do { if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 16384) \
-    g_probe_ts[blockIdx.x][k] = __builtin_amdgcn_s_memrealtime(); } while (0)
-#else
-#define PROBE_TS(k) do {} while (0)
-#endif
 
 struct Work {
   int token, pos, table_off, b_begin, b_end, part, part_begin, n_parts;
@@ -329,17 +321,13 @@ __device__ __forceinline__ void arrive_and_merge(const DecodeParams& p, const Wo
   const int n4 = G * HD / 4;
   const int64_t head0 = static_cast<int64_t>(w.token) * p.q_heads + kvh * G;
   float* ml = reinterpret_cast<float*>(p.parts.ml);
-#ifndef LE_PROBE_NOSTOREWAIT  // measurement variant: results may be stale
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are performed
-#endif
   __syncthreads();                // ... and every other thread's
-  PROBE_TS(4);
   int32_t* counter = p.parts.counters + static_cast<int64_t>(w.token) * p.kv_heads + kvh;
   if (tid == 0)
     *flag = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
             w.n_parts - 1;
   __syncthreads();
-  PROBE_TS(5);
   if (!*flag) return;
   // Every other partition incremented the counter after its partial was
   // performed, so the coherent loads of the merge see all of them.
@@ -352,7 +340,6 @@ __device__ __forceinline__ void arrive_and_merge(const DecodeParams& p, const Wo
     merge_parts<ACT, HD, NTHR, kMergeBatch / 2>(p, r, ml, rbase, np, n4, head0);
   else
     merge_parts<ACT, HD, NTHR, kMergeBatch>(p, r, ml, rbase, np, n4, head0);
-  PROBE_TS(6);
   if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -457,17 +444,6 @@ __device__ __forceinline__ void compute_tile(WaveAcc<HD>& st, const TileRegs<HD 
   constexpr int V_STRIDE = kVStrideBf16<HD>;
   constexpr int KS = HD / 32;
   constexpr int DT = HD / 16;
-#ifdef LE_PROBE_NOCOMPUTE
-  // Measurement variant: consume the loads, skip the attention arithmetic.
-  uint32_t x = 0;
-#pragma unroll
-  for (int i = 0; i < 4; i++)
-#pragma unroll
-    for (int ks = 0; ks < KS; ks++) x ^= r.k[i][ks].x ^ r.k[i][ks].w ^ r.v[i][ks].y ^ r.v[i][ks].z;
-  st.acc[0][0] += __uint_as_float(x & 0x3fffffff) * 1e-30f;
-  st.l += 1.f;
-  return;
-#endif
   // S^T = K . Q^T: lane holds head `col`, keys key0 + 16i + 4grp + j
   f32x4 s[4];
 #pragma unroll
@@ -754,7 +730,6 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
   char* lds = sm.lds;
   int* tab = sm.tab;
 
-  PROBE_TS(0);
   // With a plan, the item's block ids sit at a fixed stride: fetch them now,
   // in the same memory round trip as the item itself, and issue each wave's
   // first tile straight from them: its addresses need no field of the item.
@@ -779,11 +754,6 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
   }
   const Work w = resolve(p, bx, bz);
   if (!w.valid) return;
-#ifdef LE_PROBE_TIMING
-  if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 16384) {
-    g_probe_ts[blockIdx.x][4] = __builtin_amdgcn_s_memrealtime() + (w.token & 0) ;
-  }
-#endif
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
@@ -821,16 +791,6 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
   for (int d = 0; d < DT; d++) st.acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
   st.m = -FLT_MAX;
   st.l = 0.f;
-#ifdef LE_PROBE_TIMING
-  {
-    float qs = 0.f;
-    qs += static_cast<float>(reinterpret_cast<const float*>(&qb)[0]);
-    if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 16384)
-      g_probe_ts[blockIdx.x][5] = __builtin_amdgcn_s_memrealtime() + (qs == 12345.f);
-    if (threadIdx.x == 0 && blockIdx.y == 0 && blockIdx.x < 16384)
-      g_probe_ts[blockIdx.x][6] = __builtin_amdgcn_s_memrealtime() + (pre_ids[0] == 12345);
-  }
-#endif
 
   const int bs_shift = __builtin_ctz(bs);  // block sizes are powers of two
   const int stride = kMfmaWaves * T::kKeys;
@@ -855,7 +815,6 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
     }
     if (p.k_new != nullptr) __builtin_amdgcn_s_waitcnt(0);  // the new row is stored
     __syncthreads();
-    PROBE_TS(1);
     const int key_end = min(sb1 << bs_shift, w.pos + 1);
     int key0 = (sb0 << bs_shift) + wave * T::kKeys;
     if (key0 >= key_end) continue;
@@ -888,12 +847,6 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
     }
   }
 
-  PROBE_TS(2);
-#ifdef LE_PROBE_NOFINISH
-  // Measurement variant: stream the tiles, skip the merges (output unwritten).
-  if (st.l == 12345.f) static_cast<float*>(p.out)[0] = st.acc[0][0];
-  return;
-#endif
   // ---- merge the four waves ----
   float l_tot = st.l + __shfl_xor(st.l, 16, kWave);
   l_tot += __shfl_xor(l_tot, 32, kWave);
@@ -928,12 +881,7 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
     }
     write_piece<ACT, HD>(p, w, G, kvh, c, o, M, Ls);
   }
-  PROBE_TS(3);
-#ifdef LE_PROBE_NOCROSS  // measurement variant: the four-wave merge only
-  return;
-#endif
   arrive_and_merge<ACT, HD, kMfmaThreads>(p, w, G, kvh, &sm.flag);
-  PROBE_TS(7);
 }
 }  // namespace
 }  // namespace dec

@@ -49,17 +49,6 @@ __global__ __launch_bounds__(kRaggedThreads) void ragged_kernel(DecodeParams dp,
 
 }  // namespace
 
-#ifdef LE_PROBE_TIMING
-// Diagnostic build only: this file's copies of the phase timestamps (the
-// workgroup bodies keep them in file-local device arrays).
-extern "C" int le_probe_ragged_timing(void* dec_host, size_t dec_bytes, void* chk_host, size_t chk_bytes) {
-  const bool a = hipMemcpyFromSymbol(dec_host, HIP_SYMBOL(dec::g_probe_ts),
-                                     dec_bytes < sizeof(dec::g_probe_ts) ? dec_bytes : sizeof(dec::g_probe_ts)) == hipSuccess;
-  const bool b = hipMemcpyFromSymbol(chk_host, HIP_SYMBOL(chk::g_chunk_ts),
-                                     chk_bytes < sizeof(chk::g_chunk_ts) ? chk_bytes : sizeof(chk::g_chunk_ts)) == hipSuccess;
-  return a && b ? 0 : 1;
-}
-#endif
 
 hipError_t attention_ragged(const DecodeParams& d, const ChunkParams& c, int act_bf16, hipStream_t s) {
   const int64_t n = static_cast<int64_t>(c.n_items + d.n_rows) * c.kv_heads;

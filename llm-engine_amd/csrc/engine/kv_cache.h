@@ -10,7 +10,6 @@
 #pragma once
 
 #include <cstdint>
-#include <list>
 #include <optional>
 #include <unordered_map>
 #include <vector>
@@ -48,7 +47,7 @@ class KVCacheManager {
   int num_total_blocks() const { return num_blocks_; }
   int capacity_tokens() const { return num_blocks_ * block_size_; }
   int num_free_blocks() const { return static_cast<int>(free_.size()); }
-  int num_cached_blocks() const { return static_cast<int>(lru_.size()); }
+  int num_cached_blocks() const { return cached_count_; }
   int num_available_blocks() const { return num_free_blocks() + num_cached_blocks(); }
   int num_used_blocks() const { return num_blocks_ - num_available_blocks(); }
   bool prefix_caching_enabled() const { return prefix_caching_; }
@@ -75,19 +74,34 @@ class KVCacheManager {
   static uint64_t hash_block(uint64_t prev_hash, const int32_t* tokens, int n);
 
  private:
-  std::optional<BlockId> take_block();
-  void release_block(BlockId b, uint64_t hash);
-  void unlink_lru(BlockId b);
-  void publish(BlockTable& bt, int block_idx, const std::vector<int32_t>& tokens);
+  // State of one physical block. A block with no owner but a published hash
+  // waits in the reuse queue (an intrusive doubly linked list through
+  // `older`/`newer`, oldest release at the head): a later prompt with the same
+  // prefix takes it back, memory pressure takes the head first.
+  struct Slot {
+    int32_t owners = 0;
+    uint64_t hash = 0;  // content hash published for this block, 0 if none
+    BlockId older = -1, newer = -1;
+    bool queued = false;
+  };
+
+  // Leading full blocks of `tokens` already published: their ids and hashes
+  // (either may be null). Returns how many.
+  int walk_prefix(const std::vector<int32_t>& tokens, std::vector<BlockId>* ids,
+                  std::vector<uint64_t>* hashes) const;
+  BlockId claim();                      // free stack first, else the queue's head; -1 if neither
+  void enqueue(BlockId b);              // at the tail (newest)
+  void dequeue(BlockId b);
+  void forget_hash(BlockId b);
+  void drop_owner(BlockId b, uint64_t table_hash);
 
   int num_blocks_, block_size_;
   bool prefix_caching_;
-  std::vector<BlockId> free_;             // back() is handed out next
-  std::vector<int> refs_;
-  std::vector<uint64_t> hash_of_;         // per physical block, 0 if unpublished
-  std::unordered_map<uint64_t, BlockId> by_hash_;
-  std::list<BlockId> lru_;                // front = released longest ago
-  std::unordered_map<BlockId, std::list<BlockId>::iterator> lru_at_;
+  std::vector<Slot> slot_;
+  std::vector<BlockId> free_;           // a stack: back() is handed out next
+  BlockId queue_head_ = -1, queue_tail_ = -1;
+  int cached_count_ = 0;
+  std::unordered_map<uint64_t, BlockId> published_;
   KVCacheStats stats_;
 };
 

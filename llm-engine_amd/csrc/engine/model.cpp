@@ -17,6 +17,7 @@
 #include <cmath>
 #include <cstring>
 #include <memory>
+#include <new>
 #include <stdexcept>
 #include <string>
 #include <thread>
@@ -30,15 +31,26 @@
 namespace le::engine {
 namespace {
 
+}  // namespace
+
+// A failure that carries the status the C ABI returns for it: a HIP error
+// code, LE_EDEVICE for rocBLAS, or the LE_E* code of an inner call.
+struct StatusError : std::runtime_error {
+  int status;
+  StatusError(int st, const std::string& msg) : std::runtime_error(msg), status(st) {}
+};
+
+namespace {
+
 void hip_ok(hipError_t e, const char* what) {
-  if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+  if (e != hipSuccess) throw StatusError(static_cast<int>(e), std::string(what) + ": " + hipGetErrorString(e));
 }
 void blas_ok(rocblas_status s, const char* what) {
   if (s != rocblas_status_success)
-    throw std::runtime_error(std::string(what) + ": rocBLAS status " + std::to_string(static_cast<int>(s)));
+    throw StatusError(LE_EDEVICE, std::string(what) + ": rocBLAS status " + std::to_string(static_cast<int>(s)));
 }
 void le_ok(int st, const char* what) {
-  if (st != LE_OK) throw std::runtime_error(std::string(what) + ": " + le_status_string(st));
+  if (st != LE_OK) throw StatusError(st, std::string(what) + ": " + le_status_string(st));
 }
 
 uint16_t to_bf16(float f) {  // round to nearest even, inf/nan unrounded (tensor.h:23-28)
@@ -246,7 +258,7 @@ void Model::gemm(const void* A, const void* B, void* C, int m, int n, int k, boo
 }
 
 void Model::forward(const le_step_slice* slices, int n_slices, int32_t* tokens_out, float* logits_out) {
-  le_plan_config cfg{nh_, nkv_, hd_, bs_, kv_bf16_ ? LE_BF16 : LE_F32, 0, 0, 0};
+  le_plan_config cfg{nh_, nkv_, hd_, bs_, kv_bf16_ ? LE_BF16 : LE_F32, 0, 0, 0, 0, 0};
   le_step_plan plan{};
   int st = le_plan_step(slices, n_slices, &cfg, nullptr, 0, &plan);
   if (st != LE_ENOSPACE) le_ok(st, "le_plan_step");
@@ -327,8 +339,13 @@ struct le_model {
 };
 
 namespace {
+// The status of a failed call: the one the failure carries; a rejected
+// argument (std::invalid_argument) or anything else is LE_EINVAL, host
+// memory exhaustion LE_ENOSPACE.
 int fail(const std::exception& e) {
   std::fprintf(stderr, "llm-engine-amd: %s\n", e.what());
+  if (const auto* se = dynamic_cast<const le::engine::StatusError*>(&e)) return se->status;
+  if (dynamic_cast<const std::bad_alloc*>(&e)) return LE_ENOSPACE;
   return LE_EINVAL;
 }
 }  // namespace

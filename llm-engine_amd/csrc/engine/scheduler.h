@@ -106,16 +106,37 @@ class Scheduler {
   const std::vector<SequencePtr>& running() const { return running_; }
 
  private:
-  bool admit_one(StepInput& step, int& budget);
-  bool evict_for_memory(std::vector<Sequence*>& mid_prefill, std::vector<Sequence*>& decode);
-  bool admission_fits(const Sequence& s) const;
+  // The running sequences that take part in a step, by phase. A preempted or
+  // released sequence leaves both lists.
+  struct Residents {
+    std::vector<Sequence*> prefilling, decoding;
+    void remove(const Sequence* s);
+  };
+  // The step being built and the tokens left in its budget.
+  struct Draft {
+    StepInput step;
+    int budget = 0;
+    void add_chunk(Sequence& s, int len);
+    void add_decode(Sequence& s);
+  };
+
+  Residents residents() const;
+  void grant_decode_slots(Residents& r);
+  bool reclaim_memory(Residents& r);
+  void requeue(const SequencePtr& s);  // preempted: back to the queue head, to be recomputed
+  int chunk_len(const Sequence& s, int budget) const;
+  void drop_expired();
+  void admit(Draft& d);
+  size_t pick_admission();
+  bool reserve_blocks(Sequence& s);
+  bool leaves_headroom(const Sequence& s) const;
+  bool take_token(Sequence& s, int32_t tok, Clock::time_point now);
   void retire(const SequencePtr& s, FinishReason r);
-  void add_prefill_slice(StepInput& step, Sequence& s, int len);
 
   SchedulerConfig cfg_;
   KVCacheManager& kv_;
   std::deque<SequencePtr> waiting_;
-  std::vector<SequencePtr> running_;
+  std::vector<SequencePtr> running_;  // admission order: back() is the youngest
   bool static_batch_open_ = true;
   SchedulerStats stats_;
 };

@@ -129,6 +129,8 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
   if (cfg.block_size <= 0 || cfg.q_heads <= 0 || cfg.kv_heads <= 0 || cfg.head_dim <= 0)
     return LE_EINVAL;
   if (cfg.kv_dtype != LE_F32 && cfg.kv_dtype != LE_BF16) return LE_EINVAL;
+  if ((cfg.flags & ~(LE_PLAN_WRITE_THROUGH | LE_PLAN_TWO_LAUNCHES)) != 0 || cfg.reserved_ != 0)
+    return LE_EINVAL;
   const int bs = cfg.block_size;
   if (cfg.partition_tokens <= 0) {
     // Size decode partitions so the step has about kTargetItems workgroups,
@@ -181,6 +183,11 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
       seq_first_slice.push_back(i);
       n_table += s.num_blocks;
     } else {
+      // Slots and block ids come from the sequence's first slice (one table
+      // per sequence, as one Sequence object holds it): every later slice of
+      // the key must fit that table.
+      const le_step_slice& f = slices[seq_first_slice[it->second]];
+      if (last / bs >= f.num_blocks) return LE_EINVAL;
       slice_seq[i] = it->second;
     }
     n_tok += s.len;

@@ -17,8 +17,11 @@ LE_OK = 0
 LE_EINVAL = -1
 LE_EUNSUPPORTED = -2
 LE_ENOSPACE = -3
+LE_EDEVICE = -4
 LE_F32 = 0
 LE_BF16 = 1
+LE_PLAN_WRITE_THROUGH = 1
+LE_PLAN_TWO_LAUNCHES = 2
 
 c_i32p = ctypes.POINTER(ctypes.c_int32)
 
@@ -45,6 +48,8 @@ class PlanConfig(ctypes.Structure):
         ("partition_tokens", ctypes.c_int32),
         ("chunk_q_tile", ctypes.c_int32),
         ("chunk_partition_tokens", ctypes.c_int32),
+        ("flags", ctypes.c_int32),
+        ("reserved_", ctypes.c_int32),
     ]
 
 

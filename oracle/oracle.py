@@ -93,6 +93,8 @@ def ref() -> ctypes.CDLL:
                                           _f, _P, _i]
         R.ref_schedule_trace.restype = ctypes.c_int64
         R.ref_schedule_trace.argtypes = [_i] * 9 + [_P, _P, _P, _i, _P, ctypes.c_int64]
+        R.ref_schedule_trace_ex.restype = ctypes.c_int64
+        R.ref_schedule_trace_ex.argtypes = [_i] * 12 + [_P, _P, _P, _i, _P, ctypes.c_int64]
         _ref = R
     return _ref
 

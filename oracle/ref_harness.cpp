@@ -91,12 +91,15 @@ void ref_paged_attention(const float* q, int q_stride, const float* k_cache, con
 //   num_blocks, blocks[num_blocks]
 // followed by a terminator -1, then per sequence: n_tokens, tokens[n_tokens].
 // Returns the number of int32 written, or -(needed) if out_cap is too small.
-int64_t ref_schedule_trace(int num_blocks, int block_size, int prefix_caching,
-                           int max_num_seqs, int max_num_batched_tokens, int prefill_chunk_size,
-                           int watermark_blocks, int fragment_blocks, int n_seqs,
-                           const int32_t* prompt_lens, const int32_t* prompts_flat,
-                           const int32_t* max_tokens, int max_steps, int32_t* out,
-                           int64_t out_cap) {
+// _ex: also the static-batching switch (continuous = 0), the admission
+// lookahead and the starvation bound (scheduler.h:24-37).
+int64_t ref_schedule_trace_ex(int num_blocks, int block_size, int prefix_caching,
+                              int max_num_seqs, int max_num_batched_tokens, int prefill_chunk_size,
+                              int watermark_blocks, int fragment_blocks, int continuous,
+                              int admission_lookahead, int starvation_wait_steps, int n_seqs,
+                              const int32_t* prompt_lens, const int32_t* prompts_flat,
+                              const int32_t* max_tokens, int max_steps, int32_t* out,
+                              int64_t out_cap) {
   KVCacheManager kv(num_blocks, block_size, prefix_caching != 0);
   std::vector<BlockTable> held;
   for (int i = 0; i < fragment_blocks; i++) {
@@ -113,6 +116,9 @@ int64_t ref_schedule_trace(int num_blocks, int block_size, int prefix_caching,
   cfg.max_num_batched_tokens = max_num_batched_tokens;
   cfg.prefill_chunk_size = prefill_chunk_size;
   cfg.watermark_blocks = watermark_blocks;
+  cfg.continuous = continuous != 0;
+  cfg.admission_lookahead = admission_lookahead;
+  cfg.starvation_wait_steps = starvation_wait_steps;
   Scheduler sch(cfg, kv);
   std::vector<SequencePtr> seqs;
   size_t off = 0;
@@ -157,6 +163,20 @@ int64_t ref_schedule_trace(int num_blocks, int block_size, int prefix_caching,
   if (static_cast<int64_t>(rec.size()) > out_cap) return -static_cast<int64_t>(rec.size());
   std::memcpy(out, rec.data(), rec.size() * sizeof(int32_t));
   return static_cast<int64_t>(rec.size());
+}
+
+int64_t ref_schedule_trace(int num_blocks, int block_size, int prefix_caching,
+                           int max_num_seqs, int max_num_batched_tokens, int prefill_chunk_size,
+                           int watermark_blocks, int fragment_blocks, int n_seqs,
+                           const int32_t* prompt_lens, const int32_t* prompts_flat,
+                           const int32_t* max_tokens, int max_steps, int32_t* out,
+                           int64_t out_cap) {
+  const SchedulerConfig defaults;
+  return ref_schedule_trace_ex(num_blocks, block_size, prefix_caching, max_num_seqs,
+                               max_num_batched_tokens, prefill_chunk_size, watermark_blocks,
+                               fragment_blocks, defaults.continuous ? 1 : 0,
+                               defaults.admission_lookahead, defaults.starvation_wait_steps, n_seqs,
+                               prompt_lens, prompts_flat, max_tokens, max_steps, out, out_cap);
 }
 
 }  // extern "C"

@@ -135,33 +135,61 @@ def write_ops():
 
 
 TRACE_CONFIGS = {
-    # name: (num_blocks, bs, prefix, max_seqs, max_batched, chunk, watermark, fragment, n_seqs, len range, max_tokens)
-    "fragmented": (256, 16, 0, 32, 4096, 512, -1, 40, 6, (20, 300), 8),
-    "chunked16": (256, 16, 0, 32, 4096, 16, -1, 0, 4, (40, 200), 6),
-    "preempt": (48, 16, 0, 8, 4096, 512, -1, 0, 8, (30, 120), 24),
-    "budget512": (1024, 16, 0, 64, 512, 512, -1, 0, 20, (128, 1024), 16),
-    "prefix": (256, 16, 1, 32, 4096, 512, -1, 0, 4, (20, 100), 8),
+    # name: (num_blocks, bs, prefix, max_seqs, max_batched, chunk, watermark, fragment, n_seqs,
+    #        prompt length range, max_tokens (or a range), continuous, lookahead, starvation)
+    "fragmented": (256, 16, 0, 32, 4096, 512, -1, 40, 6, (20, 300), 8, 1, 1, 64),
+    "chunked16": (256, 16, 0, 32, 4096, 16, -1, 0, 4, (40, 200), 6, 1, 1, 64),
+    "preempt": (48, 16, 0, 8, 4096, 512, -1, 0, 8, (30, 120), 24, 1, 1, 64),
+    "budget512": (1024, 16, 0, 64, 512, 512, -1, 0, 20, (128, 1024), 16, 1, 1, 64),
+    "prefix": (256, 16, 1, 32, 4096, 512, -1, 0, 4, (20, 100), 8, 1, 1, 64),
+    # static batching: members finish at different lengths and keep their
+    # blocks until the batch drains; a small pool closes the batch early and
+    # makes decode release finished members
+    "static": (256, 16, 0, 4, 4096, 512, -1, 0, 10, (20, 200), (4, 30), 0, 1, 64),
+    "static_mem": (40, 16, 0, 6, 4096, 128, 0, 0, 9, (40, 160), (10, 60), 0, 1, 64),
+    # admission lookahead past a head that does not fit, bounded by starvation
+    "lookahead": (40, 16, 0, 16, 4096, 256, -1, 0, 12, (16, 500), (8, 40), 1, 4, 3),
+    # prefix cache under pressure: cached blocks are evicted and reused
+    "prefix_evict": (72, 16, 1, 8, 4096, 512, -1, 0, 16, (10, 90), (4, 20), 1, 1, 64),
+    # no admission headroom: decode growth preempts repeatedly
+    "watermark0": (40, 16, 0, 8, 4096, 512, 0, 0, 10, (30, 120), (20, 60), 1, 1, 64),
+    # the config-4 shape at trace size: budget 512, up to 64 running
+    "config4": (2048, 16, 0, 64, 512, 512, -1, 0, 48, (128, 1024), (16, 64), 1, 1, 64),
 }
+
+
+def trace_inputs(name, n, lo, hi, mt, prefix):
+    """Seeded prompts and max_tokens of one trace scenario."""
+    rng = np.random.default_rng(len(name))
+    lens = rng.integers(lo, hi + 1, size=n).astype(np.int32)
+    if name == "prefix":  # a shared 96-token prefix (test_cuda_invariance.cpp:235-242)
+        prompts = [np.concatenate([np.full(96, 1234), rng.integers(0, 32000, l)]).astype(np.int32) for l in lens]
+    elif name == "prefix_evict":  # three shared prefixes of 2-4 blocks, taken in turn
+        heads = [rng.integers(0, 32000, 16 * k).astype(np.int32) for k in (2, 3, 4)]
+        prompts = [np.concatenate([heads[i % 3], rng.integers(0, 32000, l)]).astype(np.int32)
+                   for i, l in enumerate(lens)]
+    else:
+        prompts = [rng.integers(0, 32000, l).astype(np.int32) for l in lens]
+    lens = np.array([len(p) for p in prompts], dtype=np.int32)
+    if isinstance(mt, tuple):
+        maxt = rng.integers(mt[0], mt[1] + 1, size=n).astype(np.int32)
+    else:
+        maxt = np.full(n, mt, dtype=np.int32)
+    return lens, np.concatenate(prompts).astype(np.int32), maxt
 
 
 def write_schedules():
     R = oracle.ref()
     out = {}
-    for name, (nb, bs, prefix, ms, mbt, chunk, wm, frag, n, (lo, hi), mt) in TRACE_CONFIGS.items():
-        rng = np.random.default_rng(len(name))
-        lens = rng.integers(lo, hi + 1, size=n).astype(np.int32)
-        if name == "prefix":  # a shared 96-token prefix (test_cuda_invariance.cpp:235-242)
-            prompts = [np.concatenate([np.full(96, 1234), rng.integers(0, 32000, l)]).astype(np.int32) for l in lens]
-            lens = np.array([len(p) for p in prompts], dtype=np.int32)
-        else:
-            prompts = [rng.integers(0, 32000, l).astype(np.int32) for l in lens]
-        flat = np.concatenate(prompts).astype(np.int32)
-        maxt = np.full(n, mt, dtype=np.int32)
-        buf = np.zeros(1 << 22, dtype=np.int32)
-        got = R.ref_schedule_trace(nb, bs, prefix, ms, mbt, chunk, wm, frag, n, ptr(lens), ptr(flat),
-                                   ptr(maxt), 100000, ptr(buf), buf.size)
+    for name, c in TRACE_CONFIGS.items():
+        nb, bs, prefix, ms, mbt, chunk, wm, frag, n, (lo, hi), mt, cont, look, starve = c
+        lens, flat, maxt = trace_inputs(name, n, lo, hi, mt, prefix)
+        buf = np.zeros(1 << 23, dtype=np.int32)
+        got = R.ref_schedule_trace_ex(nb, bs, prefix, ms, mbt, chunk, wm, frag, cont, look, starve, n,
+                                      ptr(lens), ptr(flat), ptr(maxt), 100000, ptr(buf), buf.size)
         assert got > 0, name
-        out[f"{name}.config"] = np.array([nb, bs, prefix, ms, mbt, chunk, wm, frag, n], dtype=np.int32)
+        out[f"{name}.config"] = np.array([nb, bs, prefix, ms, mbt, chunk, wm, frag, n, cont, look, starve],
+                                         dtype=np.int32)
         out[f"{name}.prompt_lens"] = lens
         out[f"{name}.prompts"] = flat
         out[f"{name}.max_tokens"] = maxt

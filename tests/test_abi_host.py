@@ -197,3 +197,20 @@ def test_plan_errors():
     # an empty step packs to an empty plan
     plan = _plan([])
     assert plan.plan.n_tokens == 0 and plan.plan.n_decode_items == 0
+
+
+def test_plan_rejects_slices_outgrowing_their_sequence_table():
+    """Slices that share a sequence key share the first slice's table (one
+    Sequence, one table). A later slice whose positions need more blocks than
+    that table holds is rejected (its slots would otherwise be read past the
+    table), whatever table it carries itself."""
+    from llm_engine_amd.kernels import Slice
+    toks = np.zeros(200, np.int32)
+    short = np.array([5], np.int32)
+    long = np.arange(10, dtype=np.int32)
+    with pytest.raises(ValueError):
+        _plan([Slice(7, 0, 1, False, short, toks), Slice(7, 150, 1, True, long, toks)])
+    # the same two slices under distinct keys are fine
+    plan = _plan([Slice(7, 0, 1, False, short, toks), Slice(8, 150, 1, True, long, toks)])
+    assert plan.plan.n_seqs == 2
+    assert list(plan.host_array("slots")) == [5 * 16, 9 * 16 + 150 % 16]

@@ -19,9 +19,11 @@ NAMES = sorted({k.split(".")[0] for k in TR.files})
 
 def cfg_of(c):
     from llm_engine_amd.engine import sched_config
-    nb, bs, prefix, ms, mbt, chunk, wm, frag, n = (int(v) for v in c)
+    nb, bs, prefix, ms, mbt, chunk, wm, frag, n, cont, look, starve = (int(v) for v in c)
     return nb, bs, prefix, frag, sched_config(max_num_seqs=ms, max_num_batched_tokens=mbt,
-                                              prefill_chunk_size=chunk, watermark_blocks=wm)
+                                              prefill_chunk_size=chunk, watermark_blocks=wm,
+                                              continuous=bool(cont), admission_lookahead=look,
+                                              starvation_wait_steps=starve)
 
 
 @pytest.mark.parametrize("name", NAMES)

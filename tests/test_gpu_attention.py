@@ -10,6 +10,7 @@ import torch
 
 from cases import loguniform_ctx, make_case
 from gpu_util import device_q, i32, max_abs, oracle_out, slices_of, to_dev_cache
+from llm_engine_amd._lib import LE_PLAN_TWO_LAUNCHES, LE_PLAN_WRITE_THROUGH
 
 pytestmark = pytest.mark.gpu
 
@@ -171,17 +172,16 @@ def test_mixed_step_config3(gpu, act):
     assert err < tol_for(True, act)
 
 
-def test_mixed_step_two_launches(gpu, monkeypatch):
-    """A mixed step runs as one launch by default; LE_RAGGED_TWO_LAUNCHES=1
-    runs the chunk and decode kernels one after the other. Both against the
+def test_mixed_step_two_launches(gpu):
+    """A mixed step runs as one launch by default; the LE_PLAN_TWO_LAUNCHES
+    plan flag runs the chunk and decode kernels one after the other. Both against the
     oracle, on a step with split decode rows and split chunk tiles."""
     ctx = [900, 40, 2500, 1700, 300]
     q_len = [300, 40, 1, 1, 1]
     case = make_case(ctx, q_len=q_len, num_blocks=1024, seed=61, kv_bf16=True)
     want = None
-    for two in ("0", "1"):
-        monkeypatch.setenv("LE_RAGGED_TWO_LAUNCHES", two)
-        got, qh, plan = run_ragged(case, torch.float32, gpu, partition_tokens=640)
+    for two in (0, LE_PLAN_TWO_LAUNCHES):
+        got, qh, plan = run_ragged(case, torch.float32, gpu, partition_tokens=640, flags=two)
         if want is None:
             want = oracle_out(case, qh)
         err = max_abs(got, want)
@@ -351,10 +351,10 @@ def test_random_ragged_steps(gpu, seed):
 
 
 @pytest.mark.parametrize("kv_bf16", [False, True])
-def test_split_rows_both_partial_paths(gpu, monkeypatch, kv_bf16):
+def test_split_rows_both_partial_paths(gpu, kv_bf16):
     """Split decode rows of a plan launch merge through the XCD's L2 (the plan
-    places a row's partitions on one XCD) unless LE_DECODE_COHERENT=1 keeps
-    the write-through partials. Both paths against the oracle, on rows split
+    places a row's partitions on one XCD) unless the LE_PLAN_WRITE_THROUGH
+    plan flag keeps the write-through partials. Both paths against the oracle, on rows split
     into 2..7 partitions, with a mixed step (chunk rows in the same launch)
     as well."""
     rng = np.random.default_rng(77)
@@ -362,9 +362,8 @@ def test_split_rows_both_partial_paths(gpu, monkeypatch, kv_bf16):
     for q_len in (None, [1] * 23 + [64]):
         case = make_case(ctx, q_len=q_len, num_blocks=8192, seed=78, kv_bf16=kv_bf16)
         want = None
-        for coherent in ("0", "1"):
-            monkeypatch.setenv("LE_DECODE_COHERENT", coherent)
-            got, qh, plan = run_ragged(case, torch.float32, gpu, partition_tokens=640)
+        for coherent in (0, LE_PLAN_WRITE_THROUGH):
+            got, qh, plan = run_ragged(case, torch.float32, gpu, partition_tokens=640, flags=coherent)
             if want is None:
                 want = oracle_out(case, qh)
             err = max_abs(got, want)

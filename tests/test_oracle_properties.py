@@ -125,3 +125,51 @@ def test_argmax_first_maximum_wins():
     assert oracle.argmax(np.array([-1, 5, 2, 5], np.float32)) == 1
     assert oracle.argmax(np.array([3], np.float32)) == 0
     assert oracle.argmax(np.array([-9, -8, -100], np.float32)) == 1
+
+
+def test_pack_step_closed_forms():
+    """orc_pack_step's non-slot arrays against closed forms of the reference's
+    packing (cuda_model.cu:434-491): token_seq = rank of the slice's sequence
+    in first-seen order; tables = the distinct sequences' tables back to back,
+    table_offset their exclusive prefix sums; logit_rows = the last row of
+    each slice with needs_logits (cu_seqlens[i+1] - 1); token_ids and
+    positions = tokens[start:start+len] and arange(start, start+len)."""
+    rng = np.random.default_rng(11)
+    for trial in range(20):
+        n_seq = int(rng.integers(1, 9))
+        tabs = [rng.permutation(500)[:int(rng.integers(1, 20))].astype(np.int32) for _ in range(n_seq)]
+        toks = [rng.integers(0, 32000, t.size * 16).astype(np.int32) for t in tabs]
+        keys = rng.permutation(10 ** 6)[:n_seq] * 7 + 3  # arbitrary, unordered keys
+        # one slice per sequence (a step holds each sequence once), in a random order
+        order = rng.permutation(n_seq)
+        slices = []
+        for s in order:
+            cap = tabs[s].size * 16
+            start = int(rng.integers(0, cap))
+            ln = int(rng.integers(1, cap - start + 1))
+            slices.append((int(keys[s]), start, ln, bool(rng.integers(0, 2)), tabs[s], toks[s]))
+        got = oracle.pack_step(slices, 16)
+        lens = np.array([sl[2] for sl in slices])
+        cu = np.concatenate([[0], np.cumsum(lens)])
+        # distinct sequences in first-seen order: here every slice is a new one
+        rank = np.arange(len(slices))
+        assert np.array_equal(got.token_seq, np.repeat(rank, lens))
+        sizes = np.array([sl[4].size for sl in slices])
+        assert np.array_equal(got.table_offset, np.concatenate([[0], np.cumsum(sizes)[:-1]]))
+        assert np.array_equal(got.tables, np.concatenate([sl[4] for sl in slices]))
+        nl = np.array([sl[3] for sl in slices], dtype=bool)
+        assert np.array_equal(got.logit_rows, (cu[1:] - 1)[nl])
+        assert np.array_equal(got.positions, np.concatenate([np.arange(s, s + l) for _, s, l, *_ in slices]))
+        assert np.array_equal(got.token_ids, np.concatenate([t[s:s + l] for _, s, l, _, _, t in slices]))
+
+
+def test_pack_step_repeated_sequence_shares_one_table():
+    """Two slices of one sequence (a key seen twice): one table, one rank."""
+    t = np.arange(5, dtype=np.int32) + 40
+    u = np.arange(3, dtype=np.int32) + 90
+    toks = np.zeros(80, np.int32)
+    got = oracle.pack_step([(9, 0, 3, False, t, toks), (4, 2, 2, True, u, toks), (9, 3, 1, True, t, toks)], 16)
+    assert list(got.token_seq) == [0, 0, 0, 1, 1, 0]
+    assert list(got.tables) == list(t) + list(u)
+    assert list(got.table_offset) == [0, 5]
+    assert list(got.logit_rows) == [4, 5]
