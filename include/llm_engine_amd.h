@@ -30,7 +30,8 @@
  *                              + pos % block_size
  *   q, out                  :  [n_tokens][q_heads][head_dim], row-contiguous
  *   new k, v rows           :  [n_tokens][kv_heads * head_dim]
- * Element types: LE_F32 (float) or LE_BF16 (raw bf16 bits, uint16).
+ * Element types: LE_F32 (float), LE_BF16 (raw bf16 bits, uint16) or LE_F16
+ * (raw IEEE binary16 bits, uint16; the reference's __half).
  */
 #ifndef LLM_ENGINE_AMD_H
 #define LLM_ENGINE_AMD_H
@@ -51,7 +52,7 @@ extern "C" {
 #define LE_EDEVICE (-4)      /* a device library call (rocBLAS) failed; a failed HIP call
                                 returns its positive hipError_t instead */
 
-typedef enum le_dtype { LE_F32 = 0, LE_BF16 = 1 } le_dtype;
+typedef enum le_dtype { LE_F32 = 0, LE_BF16 = 1, LE_F16 = 2 } le_dtype;
 
 /* Library version and build identification (for logs). */
 const char* le_version(void);

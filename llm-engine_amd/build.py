@@ -22,6 +22,8 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = ROOT / "_build"
 LIB = PKG / "lib" / "libllm_engine_amd.so"
+BRIDGE_SRC = PKG / "bridge" / "le_cuda_kernels.cpp"
+BRIDGE_LIB = PKG / "lib" / "libllm_engine_amd_bridge.so"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 COMMON = [
@@ -65,9 +67,25 @@ def build(jobs: int | None = None, verbose: bool = False, out: Path = LIB, defin
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr[-6000:]}")
     shutil.move(str(tmp), str(out))
+    if out == LIB:
+        build_bridge()
     if verbose:
-        print(f"built {out} from {len(srcs)} sources")
+        print(f"built {out} from {len(srcs)} sources, and {BRIDGE_LIB.name}")
     return out
+
+
+def build_bridge() -> Path:
+    """libllm_engine_amd_bridge.so: the reference's launcher signatures
+    (include/le_cuda_kernels.h) over the C ABI; host code only."""
+    tmp = BRIDGE_LIB.with_suffix(".so.tmp")
+    cmd = [HIPCC, "-O2", "-std=c++17", "-fPIC", "-shared", "-I", str(ROOT / "include"), str(BRIDGE_SRC),
+           "-L", str(LIB.parent), "-lllm_engine_amd", "-Wl,-rpath,$ORIGIN", "-Wl,--no-undefined",
+           "-o", str(tmp)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"bridge build failed:\n{r.stderr[-6000:]}")
+    shutil.move(str(tmp), str(BRIDGE_LIB))
+    return BRIDGE_LIB
 
 
 if __name__ == "__main__":

@@ -17,7 +17,7 @@ namespace {
 
 int hip_status(hipError_t e) { return e == hipSuccess ? LE_OK : static_cast<int>(e); }
 
-bool valid_dtype(int d) { return d == LE_F32 || d == LE_BF16; }
+bool valid_dtype(int d) { return d == LE_F32 || d == LE_BF16 || d == LE_F16; }
 
 bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
 
@@ -90,9 +90,8 @@ int le_kv_cache_write(const void* k, const void* v, le_dtype src_dtype,
   if (kv_dim % 8 != 0) return LE_EUNSUPPORTED;
   if (n_tokens == 0) return LE_OK;  // the reference returns early on an empty grid
   if (!k || !v || !slot_mapping || !k_cache || !v_cache) return LE_EINVAL;
-  return hip_status(le::kv_cache_write(k, v, src_dtype == LE_BF16, slot_mapping, k_cache, v_cache,
-                                       cache_dtype == LE_BF16, n_tokens, kv_dim, num_slots,
-                                       stream));
+  return hip_status(le::kv_cache_write(k, v, src_dtype, slot_mapping, k_cache, v_cache, cache_dtype, n_tokens,
+                                       kv_dim, num_slots, stream));
 }
 
 int le_rope_kv_cache_write(const void* qkv, le_dtype act_dtype, int64_t qkv_row_stride,
@@ -112,10 +111,9 @@ int le_rope_kv_cache_write(const void* qkv, le_dtype act_dtype, int64_t qkv_row_
   if (!qkv || !positions || !slot_mapping || !cos_table || !sin_table || !q_out || !k_cache ||
       !v_cache)
     return LE_EINVAL;
-  return hip_status(le::rope_kv_cache_write(qkv, act_dtype == LE_BF16, qkv_row_stride, bias, positions,
-                                            slot_mapping, cos_table, sin_table, max_positions, n_tokens,
-                                            q_heads, kv_heads, head_dim, q_out, k_cache, v_cache,
-                                            cache_dtype == LE_BF16, num_slots, stream));
+  return hip_status(le::rope_kv_cache_write(qkv, act_dtype, qkv_row_stride, bias, positions, slot_mapping,
+                                            cos_table, sin_table, max_positions, n_tokens, q_heads, kv_heads,
+                                            head_dim, q_out, k_cache, v_cache, cache_dtype, num_slots, stream));
 }
 
 size_t le_attention_decode_workspace_size(int n_tokens, int q_heads, int kv_heads, int head_dim) {
@@ -155,7 +153,7 @@ int le_attention_decode(const void* q, le_dtype act_dtype, const void* k_cache,
   p.scale_log2 = scale * 1.4426950408889634f;
   p.num_cache_blocks = num_cache_blocks;
   // Split rows are merged inside the launch (last-arriving partition).
-  const hipError_t e = le::attention_decode(p, act_dtype == LE_BF16, kv_dtype == LE_BF16, stream);
+  const hipError_t e = le::attention_decode(p, act_dtype, kv_dtype, stream);
   return hip_status(e);
 }
 
@@ -232,12 +230,12 @@ int ragged_attention(const void* q, le_dtype act_dtype, const void* k_new, const
     // rows of one sequence (a prefill chunk, which an fp32 cache runs as
     // decode rows) read each other's new keys across workgroups.
     if (plan->n_tokens != plan->n_seqs || plan->n_decode_items == 0) {
-      e = le::kv_cache_write(k_new, v_new, new_dtype == LE_BF16, arr(plan->off_slots),
-                             const_cast<void*>(k_cache), const_cast<void*>(v_cache), kv_dtype == LE_BF16,
-                             plan->n_tokens, cfg.kv_heads * cfg.head_dim, num_slots, stream);
+      e = le::kv_cache_write(k_new, v_new, new_dtype, arr(plan->off_slots), const_cast<void*>(k_cache),
+                             const_cast<void*>(v_cache), kv_dtype, plan->n_tokens, cfg.kv_heads * cfg.head_dim,
+                             num_slots, stream);
       if (e != hipSuccess) return hip_status(e);
     } else {
-      d.k_new = k_new; d.v_new = v_new; d.new_bf16 = new_dtype == LE_BF16;
+      d.k_new = k_new; d.v_new = v_new; d.new_dtype = new_dtype;
       d.slots = arr(plan->off_slots); d.num_slots = num_slots;
       if (rope) {
         d.rope_row_stride = rope->row_stride; d.rope_bias = rope->bias;
@@ -247,9 +245,9 @@ int ragged_attention(const void* q, le_dtype act_dtype, const void* k_new, const
   }
   if (rope && !d.k_new) return LE_EINVAL;  // q rows in QKV form need the in-launch path
   if (plan->n_chunk_items == 0)
-    return hip_status(le::attention_decode(d, act_dtype == LE_BF16, kv_dtype == LE_BF16, stream));
+    return hip_status(le::attention_decode(d, act_dtype, kv_dtype, stream));
 
-  if (kv_dtype != LE_BF16) return LE_EINVAL;  // chunk items exist only for bf16 caches
+  if (kv_dtype == LE_F32) return LE_EINVAL;  // chunk items exist only for 16-bit caches
   le::ChunkParams c{};
   c.q = q; c.k_cache = k_cache; c.v_cache = v_cache;
   c.tables = d.tables; c.table_offset = d.table_offset; c.token_pos = d.token_pos;
@@ -267,10 +265,10 @@ int ragged_attention(const void* q, le_dtype act_dtype, const void* k_new, const
   // LE_PLAN_TWO_LAUNCHES runs the two kernels one after the other instead.
   const bool two_launches = (cfg.flags & LE_PLAN_TWO_LAUNCHES) != 0;
   if (plan->n_decode_items > 0 && !two_launches)
-    return hip_status(le::attention_ragged(d, c, act_dtype == LE_BF16, stream));
-  e = le::attention_decode(d, act_dtype == LE_BF16, kv_dtype == LE_BF16, stream);
+    return hip_status(le::attention_ragged(d, c, act_dtype, kv_dtype, stream));
+  e = le::attention_decode(d, act_dtype, kv_dtype, stream);
   if (e != hipSuccess) return hip_status(e);
-  e = le::attention_chunk(c, act_dtype == LE_BF16, stream);
+  e = le::attention_chunk(c, act_dtype, kv_dtype, stream);
   return hip_status(e);
 }
 
@@ -315,7 +313,7 @@ int le_ragged_paged_attention_qkv(const void* qkv, le_dtype act_dtype, int64_t q
   if (qkv_row_stride < static_cast<int64_t>(qd) + 2 * kvd) return LE_EINVAL;
   if (qkv_row_stride % 8 != 0) return LE_EUNSUPPORTED;  // 16-byte vector rows
   if (!qkv || !cos_table || !sin_table || !plan->dev) return LE_EINVAL;
-  const size_t esz = act_dtype == LE_BF16 ? 2 : 4;
+  const size_t esz = act_dtype == LE_F32 ? 4 : 2;
   const char* row0 = static_cast<const char*>(qkv);
   const void* k_new = row0 + qd * esz;
   const void* v_new = row0 + (static_cast<int64_t>(qd) + kvd) * esz;
@@ -330,9 +328,9 @@ int le_ragged_paged_attention_qkv(const void* qkv, le_dtype act_dtype, int64_t q
   const int32_t* positions = reinterpret_cast<const int32_t*>(dev + plan->off_positions);
   const int32_t* slots = reinterpret_cast<const int32_t*>(dev + plan->off_slots);
   const hipError_t e = le::rope_kv_cache_write(
-      qkv, act_dtype == LE_BF16, qkv_row_stride, bias, positions, slots, cos_table, sin_table,
-      max_positions, plan->n_tokens, cfg.q_heads, cfg.kv_heads, cfg.head_dim, q_scratch, k_cache,
-      v_cache, kv_dtype == LE_BF16, num_cache_blocks * cfg.block_size, stream);
+      qkv, act_dtype, qkv_row_stride, bias, positions, slots, cos_table, sin_table, max_positions, plan->n_tokens,
+      cfg.q_heads, cfg.kv_heads, cfg.head_dim, q_scratch, k_cache, v_cache, kv_dtype,
+      num_cache_blocks * cfg.block_size, stream);
   if (e != hipSuccess) return hip_status(e);
   return ragged_attention(q_scratch, act_dtype, nullptr, nullptr, LE_F32, k_cache, v_cache, kv_dtype,
                           num_cache_blocks, plan, scale, out, workspace, workspace_bytes, stream, nullptr);

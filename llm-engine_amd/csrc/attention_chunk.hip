@@ -7,26 +7,27 @@
 namespace le {
 namespace {
 
-template <typename ACT, int HD>
+template <typename ACT, typename KV, int HD>
 __global__ __launch_bounds__(chk::kThreads) void chunk_kernel(ChunkParams p) {
   __shared__ chk::ChunkSmem<HD> sm;
-  chk::chunk_wg<ACT, HD>(p, sm, blockIdx.x, blockIdx.y);
+  chk::chunk_wg<ACT, KV, HD>(p, sm, blockIdx.x, blockIdx.y);
 }
 
 }  // namespace
 
 
-hipError_t attention_chunk(const ChunkParams& p, int act_bf16, hipStream_t s) {
+hipError_t attention_chunk(const ChunkParams& p, int act_dtype, int kv_dtype, hipStream_t s) {
   if (p.n_items <= 0) return hipSuccess;
   const dim3 grid(p.n_items, p.kv_heads);
-  if (p.head_dim == 64) {
-    if (act_bf16) chunk_kernel<bf16_t, 64><<<grid, chk::kThreads, 0, s>>>(p);
-    else chunk_kernel<float, 64><<<grid, chk::kThreads, 0, s>>>(p);
-  } else {
-    if (act_bf16) chunk_kernel<bf16_t, 128><<<grid, chk::kThreads, 0, s>>>(p);
-    else chunk_kernel<float, 128><<<grid, chk::kThreads, 0, s>>>(p);
-  }
-  return hipGetLastError();
+  return with_dtype(act_dtype, [&](auto a) {
+    return with_dtype16(kv_dtype, [&](auto k) {
+      using ACT = decltype(a);
+      using KV = decltype(k);
+      if (p.head_dim == 64) chunk_kernel<ACT, KV, 64><<<grid, chk::kThreads, 0, s>>>(p);
+      else chunk_kernel<ACT, KV, 128><<<grid, chk::kThreads, 0, s>>>(p);
+      return hipGetLastError();
+    });
+  });
 }
 
 }  // namespace le

@@ -19,7 +19,7 @@
 //     16-byte K and V loads at once (block ids come from the plan, fetched in
 //     the same round trip as the item), so a stage costs one memory latency;
 //     K and V rows land row-major in LDS;
-//   * S^T = K . Q^T on v_mfma_f32_16x16x32_bf16 (A = 16 keys x 32 dims from
+//   * S^T = K . Q^T on the 16x16x32 MFMA of the cache type, bf16 or fp16 (A = 16 keys x 32 dims from
 //     LDS, B = Q^T in registers); the accumulator puts one query row per lane
 //     column, so the online-softmax statistics of a row live in that lane and
 //     P^T is already the B operand of O^T = V^T . P^T, whose A operand comes
@@ -37,10 +37,11 @@
 //     kp <= pos[t]; masked scores are -inf and the running max starts at
 //     -FLT_MAX, so fully masked tiles add zero;
 //   * a tile whose keys were split stores each partition's normalised output
-//     (fp16, bounded by max |v|) and its fp32 (max, sum) with device-coherent
+//     (fp32) and its fp32 (max, sum) with device-coherent
 //     stores; the last partition to arrive (atomic counter per tile and kv
 //     head, reset by it) merges them in partition order, inside the launch.
-// bf16 operands, fp32 accumulation; fp32 caches never come here (their chunk
+// 16-bit operands (q and P rounded to the cache type), fp32 accumulation;
+// fp32 caches never come here (their chunk
 // rows run on the decode kernel for exact fp32 arithmetic).
 #include <float.h>
 
@@ -51,10 +52,6 @@ namespace le {
 namespace chk {
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * kWave;
@@ -80,18 +77,6 @@ template <int HD> struct ChunkLds {
   static constexpr int BYTES = 2 * K_BYTES;  // K rows, then V rows
 };
 
-__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-// ds_read_b64_tr_b16: in each group of 16 lanes, lane i receives 16-bit
-// element (i % 4) of the 8-byte chunks addressed by lanes 4j + i/4, j = 0..3.
-__device__ __forceinline__ bf16x4 lds_read_tr(const char* p) {
-  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) i16x4*)(p));
-  return __builtin_bit_cast(bf16x4, v);
-}
-
 __device__ __forceinline__ void st_dev(float* p, float v) {
   __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
@@ -102,26 +87,10 @@ __device__ __forceinline__ float ld_dev(const float* p) {
 }
 
 
-// fp16 (round to nearest even) transport of normalised partial outputs.
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-__device__ __forceinline__ uint2 pack_half4(f32x4 v) {
-  const f16x4 h = {static_cast<_Float16>(v[0]), static_cast<_Float16>(v[1]), static_cast<_Float16>(v[2]),
-                   static_cast<_Float16>(v[3])};
-  return __builtin_bit_cast(uint2, h);
-}
-__device__ __forceinline__ void unpack_half8(uint4 r, float* o) {
-  const f16x8 h = __builtin_bit_cast(f16x8, r);
-#pragma unroll
-  for (int e = 0; e < 8; e++) o[e] = static_cast<float>(h[e]);
-}
-
-template <typename ACT> __device__ __forceinline__ void store4(ACT* p, f32x4 v);
-template <> __device__ __forceinline__ void store4<float>(float* p, f32x4 v) {
-  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
-}
-template <> __device__ __forceinline__ void store4<bf16_t>(bf16_t* p, f32x4 v) {
-  *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+template <typename ACT>
+__device__ __forceinline__ void store4(ACT* p, f32x4 v) {
+  const float f[4] = {v[0], v[1], v[2], v[3]};
+  elem<ACT>::store4(p, f);
 }
 
 // LDS of one chunk workgroup.
@@ -131,17 +100,17 @@ template <int HD> struct ChunkSmem {
 };
 
 // The last partition's merge of a split tile. Each thread owns kMG output
-// 8-vectors (a row, a head, 8 dims) and merges their partials itself, kMJ
-// partitions per round of loads: the partition's (m, l) for the row and head,
-// and its normalised output, requested together, then folded in partition
-// order into a running (max, sum) with rescaling. With at most kMJ
-// partitions the whole merge is one memory round trip, with no LDS phase or
-// barrier.
+// 8-vectors (a row, a head, 8 consecutive dims) and merges their partials
+// itself, kMJ partitions per round of loads: the partition's (m, l) for the
+// row and head, and its normalised output (fp32), requested together, then
+// folded in partition order into a running (max, sum) with rescaling. With at
+// most kMJ partitions the whole merge is one memory round trip, with no LDS
+// phase or barrier.
 template <typename ACT, int HD, int kMJ>
 __device__ __forceinline__ void merge_tile(const ChunkParams& p, const ChunkItem& it, __amdgpu_buffer_rsrc_t acc_rsrc,
                                            float* ml, int64_t rec_tile, int base, int J, int G, int kvh, int nq,
                                            int tok0) {
-  constexpr int kMG = 4;  // output 8-vectors per thread and round
+  constexpr int kMG = 2;  // output 8-vectors per thread and round
   const int tid = threadIdx.x;
   const int per_row = G * (HD / 8);
   const int n_out = nq * per_row;
@@ -162,14 +131,16 @@ __device__ __forceinline__ void merge_tile(const ChunkParams& p, const ChunkItem
       for (int e = 0; e < 8; e++) sum[gi][e] = 0.f;
     }
     for (int j0 = 0; j0 < J; j0 += kMJ) {
-      uint4 x[kMG][kMJ];
+      f32x4 x[kMG][kMJ][2];
       float mj[kMG][kMJ], lj[kMG][kMJ];
 #pragma unroll
       for (int gi = 0; gi < kMG; gi++)
 #pragma unroll
         for (int jj = 0; jj < kMJ; jj++) {
           const int64_t rec = rec_base[gi] + static_cast<int64_t>(min(j0 + jj, J - 1)) * p.q_heads;
-          x[gi][jj] = ld_coherent16u(acc_rsrc, static_cast<uint32_t>((rec - rec_tile) * HD * 4 + d8[gi] * 16));
+          const uint32_t off = static_cast<uint32_t>(((rec - rec_tile) * HD + d8[gi] * 8) * 4);
+          x[gi][jj][0] = ld_coherent16(acc_rsrc, off);
+          x[gi][jj][1] = ld_coherent16(acc_rsrc, off + 16);
           mj[gi][jj] = ld_dev(ml + rec * 2);
           lj[gi][jj] = ld_dev(ml + rec * 2 + 1);
         }
@@ -178,15 +149,13 @@ __device__ __forceinline__ void merge_tile(const ChunkParams& p, const ChunkItem
 #pragma unroll
         for (int jj = 0; jj < kMJ; jj++)
           if (j0 + jj < J) {
-            // partition j holds o_j / l_j (fp16); fold in l_j * o_j at weight exp2(m_j - max)
+            // partition j holds o_j / l_j; fold in l_j * o_j at weight exp2(m_j - max)
             const float m_new = fmaxf(M[gi], mj[gi][jj]);
             const float a = __builtin_amdgcn_exp2f(M[gi] - m_new), w = __builtin_amdgcn_exp2f(mj[gi][jj] - m_new) * lj[gi][jj];
             M[gi] = m_new;
             L[gi] = L[gi] * a + w;
-            float f[8];
-            unpack_half8(x[gi][jj], f);
 #pragma unroll
-            for (int e = 0; e < 8; e++) sum[gi][e] = sum[gi][e] * a + w * f[e];
+            for (int e = 0; e < 8; e++) sum[gi][e] = sum[gi][e] * a + w * x[gi][jj][e >> 2][e & 3];
           }
     }
 #pragma unroll
@@ -195,12 +164,12 @@ __device__ __forceinline__ void merge_tile(const ChunkParams& p, const ChunkItem
       if (o < n_out) {
         const int r = o / per_row, rem = o - r * per_row;
         const int g = rem / (HD / 8);
-        // piece d8 = (d / 2) * 4 + g4: dims (d8 / 4) * 32 + (d8 % 4) * 4 .. +4, then +16
-        ACT* out = static_cast<ACT*>(p.out) + (static_cast<int64_t>(tok0 + r) * p.q_heads + kvh * G + g) * HD +
-                   (d8[gi] >> 2) * 32 + (d8[gi] & 3) * 4;
+        ACT* out = static_cast<ACT*>(p.out) + (static_cast<int64_t>(tok0 + r) * p.q_heads + kvh * G + g) * HD + d8[gi] * 8;
         const float inv = 1.f / L[gi];
-        store4<ACT>(out, f32x4{sum[gi][0], sum[gi][1], sum[gi][2], sum[gi][3]} * inv);
-        store4<ACT>(out + 16, f32x4{sum[gi][4], sum[gi][5], sum[gi][6], sum[gi][7]} * inv);
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[e] = sum[gi][e] * inv;
+        elem<ACT>::store8(out, v);
       }
     }
   }
@@ -208,8 +177,11 @@ __device__ __forceinline__ void merge_tile(const ChunkParams& p, const ChunkItem
 
 // One chunk workgroup (kThreads threads): chunk item `item`, kv head `kvh`.
 // Shared by the chunk kernel and the fused ragged kernel.
-template <typename ACT, int HD>
+template <typename ACT, typename KV, int HD>
 __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm, int item, int kvh) {
+  using M = mma16<KV>;  // K/V element type = the MFMA operand type
+  using V8 = typename M::v8;
+  using S16 = typename M::scalar;
   using L = ChunkLds<HD>;
   constexpr int KS = HD / 32;  // MFMA k-steps over head dims
   constexpr int DT = HD / 16;  // 16-dim output tiles
@@ -285,7 +257,7 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
   // Query rows first (they are needed last, and a wait for them must not
   // cover the K/V loads issued after them), then the stage's K/V.
   const int pos0 = p.token_pos[tok0];  // the tile's rows are consecutive positions
-  uint4 qraw[2][KS][sizeof(ACT) / 2];  // 8 elements per k-step: 16 bytes (bf16) or 32 (fp32)
+  uint4 qraw[2][KS][sizeof(ACT) / 2];  // 8 elements per k-step: 16 bytes (16-bit types) or 32 (fp32)
 #pragma unroll
   for (int rs = 0; rs < 2; rs++) {
     const int r = rs * 16 + col;
@@ -299,7 +271,7 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
   }
   issue(0);
   // Q^T operands: this lane's 8 dims per k-step of rows col and 16 + col.
-  bf16x8 qb[2][KS];
+  V8 qb[2][KS];
 #pragma unroll
   for (int rs = 0; rs < 2; rs++) {
     const bool ok = computes && rs * 16 + col < nq;
@@ -307,13 +279,13 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
     for (int ks = 0; ks < KS; ks++) {
       float f[8];
       if constexpr (sizeof(ACT) == 2) {
-        elem<bf16_t>::widen(qraw[rs][ks][0], f);
+        elem<ACT>::widen(qraw[rs][ks][0], f);
       } else {
         elem<float>::widen(qraw[rs][ks][0], f);
         elem<float>::widen(qraw[rs][ks][1], f + 4);
       }
 #pragma unroll
-      for (int e = 0; e < 8; e++) qb[rs][ks][e] = static_cast<__bf16>(ok ? f[e] : 0.f);
+      for (int e = 0; e < 8; e++) qb[rs][ks][e] = static_cast<S16>(ok ? f[e] : 0.f);
     }
   }
 
@@ -326,8 +298,8 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
   // lsum[rs][0] of the lanes of group 0 = the row's sum of p (row col); the
   // other entries stay zero
   f32x4 lsum[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-  const __bf16 one = static_cast<__bf16>(col == 0 ? 1.f : 0.f);
-  const bf16x8 ones = {one, one, one, one, one, one, one, one};
+  const S16 one = static_cast<S16>(col == 0 ? 1.f : 0.f);
+  const V8 ones = {one, one, one, one, one, one, one, one};
 
   for (int rel0 = 0;;) {
     stash();
@@ -351,10 +323,9 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
         for (int i = 0; i < 4; i++)
 #pragma unroll
           for (int ks = 0; ks < KS; ks++) {
-            const bf16x8 a =
-                *reinterpret_cast<const bf16x8*>(kt_lds + (i * 16 + col) * L::ROW + (ks * 32 + grp * 8) * 2);
+            const V8 a = *reinterpret_cast<const V8*>(kt_lds + (i * 16 + col) * L::ROW + (ks * 32 + grp * 8) * 2);
 #pragma unroll
-            for (int rs = 0; rs < 2; rs++) s[rs][i] = mfma16(a, qb[rs][ks], s[rs][i]);
+            for (int rs = 0; rs < 2; rs++) s[rs][i] = M::mma(a, qb[rs][ks], s[rs][i]);
           }
         // ---- causal mask, online softmax per row (log2 domain) ----
         // A tile wholly below the diagonal and inside the range needs no
@@ -409,13 +380,13 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
         // ---- O^T += V^T . P^T over the tile's 64 keys (2 k-steps of 32) ----
 #pragma unroll
         for (int kk = 0; kk < 2; kk++) {
-          bf16x8 pb[2];
+          V8 pb[2];
 #pragma unroll
           for (int rs = 0; rs < 2; rs++)
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-              pb[rs][j] = static_cast<__bf16>(s[rs][2 * kk][j]);
-              pb[rs][4 + j] = static_cast<__bf16>(s[rs][2 * kk + 1][j]);
+              pb[rs][j] = static_cast<S16>(s[rs][2 * kk][j]);
+              pb[rs][4 + j] = static_cast<S16>(s[rs][2 * kk + 1][j]);
             }
           // lane (col, grp) addresses key row kk*32 + 4*grp + col/4 (then +16)
           // at dims 16*d + 4*(col%4), and receives dim 16*d + col of four
@@ -424,15 +395,15 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
           const char* r_hi = r_lo + 16 * L::ROW;
 #pragma unroll
           for (int d = 0; d < DT; d++) {
-            const bf16x4 lo = lds_read_tr(r_lo + d * 32);
-            const bf16x4 hi = lds_read_tr(r_hi + d * 32);
-            const bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            const typename M::v4 lo = lds_read_tr16<KV>(r_lo + d * 32);
+            const typename M::v4 hi = lds_read_tr16<KV>(r_hi + d * 32);
+            const V8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 #pragma unroll
-            for (int rs = 0; rs < 2; rs++) acc[rs][d] = mfma16(a, pb[rs], acc[rs][d]);
+            for (int rs = 0; rs < 2; rs++) acc[rs][d] = M::mma(a, pb[rs], acc[rs][d]);
           }
           // row sums on the MFMA: a V^T row of ones (lanes of column 0)
 #pragma unroll
-          for (int rs = 0; rs < 2; rs++) lsum[rs] = mfma16(ones, pb[rs], lsum[rs]);
+          for (int rs = 0; rs < 2; rs++) lsum[rs] = M::mma(ones, pb[rs], lsum[rs]);
         }
       }
     }
@@ -478,19 +449,15 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
       const int r = rs * 16 + col;
       if (r < nq) {
         const int64_t rec = static_cast<int64_t>(it.part0 + r * it.part_stride) * p.q_heads + head;
-        // the partition's normalised output in fp16 (|o| <= max |v|; a row
-        // with no live key in the partition stores zeros and l = 0), in the
-        // first half of the record's fp32-sized slot: partition indices are
-        // shared with the decode rows, whose fp32 partials may be live in the
-        // same launch (the fused ragged kernel)
+        // the partition's normalised output, fp32, in the record's natural
+        // layout (a row with no live key in the partition stores zeros and
+        // l = 0): lane (col, grp) holds dims d*16 + grp*4 .. +4 of each
+        // output tile d
         const float inv = l_tot[rs] > 0.f ? 1.f / l_tot[rs] : 0.f;
-        // 16-byte piece c = (d / 2) * 4 + grp holds the lane's 4 dims of
-        // output tiles d and d + 1: dims d*16 + grp*4 .. +4, then +16
 #pragma unroll
-        for (int d = 0; d < DT; d += 2) {
-          const uint2 lo = pack_half4(acc[rs][d] * inv), hi = pack_half4(acc[rs][d + 1] * inv);
-          const uint32_t off = static_cast<uint32_t>((rec - rec_tile) * HD * 4 + ((d / 2) * 4 + grp) * 16);
-          const f32x4v v = __builtin_bit_cast(f32x4v, make_uint4(lo.x, lo.y, hi.x, hi.y));
+        for (int d = 0; d < DT; d++) {
+          const uint32_t off = static_cast<uint32_t>(((rec - rec_tile) * HD + d * 16 + grp * 4) * 4);
+          const f32x4v v = __builtin_bit_cast(f32x4v, acc[rs][d] * inv);
           if (p.l2_local) st_l2_16(acc_rsrc, off, v);
           else st_coherent16(acc_rsrc, off, v);
         }

@@ -18,19 +18,13 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_kernel(DecodeParams p) {
   dec::decode_wg<ACT, KV, HD, kMfmaWaves>(p, sm, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
-template <typename ACT>
-hipError_t dispatch(const DecodeParams& p, int kv_bf16, hipStream_t s) {
+template <typename ACT, typename KV>
+hipError_t launch(const DecodeParams& p, hipStream_t s) {
   const dim3 grid(p.n_rows, p.kv_heads, p.items ? 1 : p.nsplit);
-  if (kv_bf16) {
-    if (p.head_dim == 64) mfma_kernel<ACT, bf16_t, 64><<<grid, kMfmaThreads, 0, s>>>(p);
-    else mfma_kernel<ACT, bf16_t, 128><<<grid, kMfmaThreads, 0, s>>>(p);
-    return hipGetLastError();
-  }
-  if (p.head_dim == 64) mfma_kernel<ACT, float, 64><<<grid, kMfmaThreads, 0, s>>>(p);
-  else mfma_kernel<ACT, float, 128><<<grid, kMfmaThreads, 0, s>>>(p);
+  if (p.head_dim == 64) mfma_kernel<ACT, KV, 64><<<grid, kMfmaThreads, 0, s>>>(p);
+  else mfma_kernel<ACT, KV, 128><<<grid, kMfmaThreads, 0, s>>>(p);
   return hipGetLastError();
 }
-
 
 }  // namespace
 
@@ -88,9 +82,11 @@ int decode_nsplit(int n_tokens, int kv_heads) {
   return ns < 1 ? 1 : (ns > 32 ? 32 : ns);
 }
 
-hipError_t attention_decode(const DecodeParams& p, int act_bf16, int kv_bf16, hipStream_t s) {
+hipError_t attention_decode(const DecodeParams& p, int act_dtype, int kv_dtype, hipStream_t s) {
   if (p.n_rows <= 0) return hipSuccess;
-  return act_bf16 ? dispatch<bf16_t>(p, kv_bf16, s) : dispatch<float>(p, kv_bf16, s);
+  return with_dtype(act_dtype, [&](auto a) {
+    return with_dtype(kv_dtype, [&](auto k) { return launch<decltype(a), decltype(k)>(p, s); });
+  });
 }
 
 

@@ -23,8 +23,8 @@
 //     the B operand (an MFMA only needs A and B to agree on the order of k
 //     inside a lane group). Each wave runs its own online softmax over its
 //     tiles; the waves merge at the end.
-//       bf16 cache: 64-key tiles on v_mfma_f32_16x16x32_bf16, V^T read with
-//       the transposing ds_read_b64_tr_b16.
+//       bf16 / fp16 cache: 64-key tiles on v_mfma_f32_16x16x32_bf16 / _f16,
+//       V^T read with the transposing ds_read_b64_tr_b16.
 //       fp32 cache: 32-key tiles on v_mfma_f32_16x16x4_f32 (exact fp32
 //       products), V^T read as single floats of the row-major tile.
 //
@@ -44,13 +44,10 @@ namespace le {
 namespace dec {
 namespace {
 
-constexpr int kTile = 64;     // bf16 tiles: keys per wave tile
+constexpr int kTile = 64;     // 16-bit tiles: keys per wave tile
 constexpr int kMaxG = 16;     // heads per kv head the MFMA columns can hold
 constexpr int kMergeBatch = 8;       // partial accumulators loaded per batch in the merge
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 
 struct Work {
@@ -80,22 +77,6 @@ __device__ __forceinline__ Work resolve(const DecodeParams& p, int bx, int bz) {
 }
 
 // ---- Rows straight from the stacked QKV projection ----
-// Eight consecutive elements of a row as fp32.
-template <typename ACT>
-__device__ __forceinline__ void load8(const ACT* p, float* o) {
-  if constexpr (sizeof(ACT) == 2) {
-    elem<bf16_t>::widen(ld16(p), o);
-  } else {
-    elem<float>::widen(ld16(p), o);
-    elem<float>::widen(ld16(p + 4), o + 4);
-  }
-}
-template <typename ACT>
-__device__ __forceinline__ float round_act(float x) {
-  if constexpr (sizeof(ACT) == 2) return __uint_as_float(f32_to_bf16_bits(x) << 16);
-  return x;
-}
-
 // Dims [d0, d0 + 8) of one head after bias and rotate_half RoPE (rope.cu:53,
 // ops.h:55-66): head is the head's first element in the row, hb its bias (or
 // null), cs/sn the position's cos/sin rows. The operations and their order
@@ -110,15 +91,15 @@ __device__ __forceinline__ void rope8(const ACT* head, const float* hb, int d0, 
   const bool lo = d0 < half;
   const int dp = lo ? d0 + half : d0 - half;  // the partner dims
   float own[8], oth[8], c[8], s[8];
-  load8<ACT>(head + d0, own);
-  load8<ACT>(head + dp, oth);
-  load8<float>(cs + (lo ? d0 : dp), c);
-  load8<float>(sn + (lo ? d0 : dp), s);
+  elem<ACT>::load8(head + d0, own);
+  elem<ACT>::load8(head + dp, oth);
+  elem<float>::load8(cs + (lo ? d0 : dp), c);
+  elem<float>::load8(sn + (lo ? d0 : dp), s);
   if (hb) {
 #pragma unroll
     for (int e = 0; e < 8; e++) {
-      own[e] = round_act<ACT>(own[e] + hb[d0 + e]);
-      oth[e] = round_act<ACT>(oth[e] + hb[dp + e]);
+      own[e] = elem<ACT>::round(own[e] + hb[d0 + e]);
+      oth[e] = elem<ACT>::round(oth[e] + hb[dp + e]);
     }
   }
 #pragma unroll
@@ -133,7 +114,7 @@ __device__ __forceinline__ void rope8(const ACT* head, const float* hb, int d0, 
 // of a stacked QKV row, biased and rotated on the way in.
 template <typename ACT> struct QRow {
   const ACT* row;
-  __device__ __forceinline__ void piece8(int d0, float* o) const { load8<ACT>(row + d0, o); }
+  __device__ __forceinline__ void piece8(int d0, float* o) const { elem<ACT>::load8(row + d0, o); }
 };
 template <typename ACT> struct QRope {
   const ACT* head;
@@ -145,7 +126,7 @@ template <typename ACT> struct QRope {
   __device__ __forceinline__ void piece8(int d0, float* o) const {
     rope8<ACT>(head, hb, d0, half, cs, sn, o);
 #pragma unroll
-    for (int e = 0; e < 8; e++) o[e] = round_act<ACT>(o[e]);
+    for (int e = 0; e < 8; e++) o[e] = elem<ACT>::round(o[e]);
   }
 };
 
@@ -174,50 +155,30 @@ __device__ __forceinline__ void store_new_row(const DecodeParams& p, const Work&
   const int64_t src = (static_cast<int64_t>(w.token) * p.kv_heads + kvh) * hd + c * 8;
   const int64_t dst = (slot * p.kv_heads + kvh) * hd + c * 8;
   float v[8];
-  if (p.rope_max_pos > 0) {
-    // k biased and rotated, v biased, as rope_kv_write_kernel stores them; a
-    // position outside the tables stores nothing
-    if (w.pos < 0 || w.pos >= p.rope_max_pos) return;
-    const int half = hd / 2;
-    const int64_t tab = static_cast<int64_t>(w.pos) * half;
-    const int64_t row = static_cast<int64_t>(w.token) * p.rope_row_stride + kvh * hd;
-    const float* hb = p.rope_bias ? p.rope_bias + (p.q_heads + which * p.kv_heads + kvh) * hd : nullptr;
-    if (p.new_bf16) {
-      const bf16_t* h = static_cast<const bf16_t*>(which ? p.v_new : p.k_new) + row;
+  if (p.rope_max_pos > 0 && (w.pos < 0 || w.pos >= p.rope_max_pos)) return;  // as rope_kv_write_kernel
+  const void* src_rows = which ? p.v_new : p.k_new;
+  with_dtype(p.new_dtype, [&](auto tag) {
+    using S = decltype(tag);
+    if (p.rope_max_pos > 0) {
+      // k biased and rotated, v biased, as rope_kv_write_kernel stores them
+      const int half = hd / 2;
+      const int64_t tab = static_cast<int64_t>(w.pos) * half;
+      const S* h = static_cast<const S*>(src_rows) + static_cast<int64_t>(w.token) * p.rope_row_stride + kvh * hd;
+      const float* hb = p.rope_bias ? p.rope_bias + (p.q_heads + which * p.kv_heads + kvh) * hd : nullptr;
       if (!which) {
-        rope8<bf16_t>(h, hb, c * 8, half, p.rope_cos + tab, p.rope_sin + tab, v);
+        rope8<S>(h, hb, c * 8, half, p.rope_cos + tab, p.rope_sin + tab, v);
       } else {
-        load8<bf16_t>(h + c * 8, v);
+        elem<S>::load8(h + c * 8, v);
         if (hb)
 #pragma unroll
-          for (int e = 0; e < 8; e++) v[e] = round_act<bf16_t>(v[e] + hb[c * 8 + e]);
+          for (int e = 0; e < 8; e++) v[e] = elem<S>::round(v[e] + hb[c * 8 + e]);
       }
     } else {
-      const float* h = static_cast<const float*>(which ? p.v_new : p.k_new) + row;
-      if (!which) {
-        rope8<float>(h, hb, c * 8, half, p.rope_cos + tab, p.rope_sin + tab, v);
-      } else {
-        load8<float>(h + c * 8, v);
-        if (hb)
-#pragma unroll
-          for (int e = 0; e < 8; e++) v[e] = v[e] + hb[c * 8 + e];
-      }
+      elem<S>::load8(static_cast<const S*>(src_rows) + src, v);
     }
-  } else if (p.new_bf16) {
-    elem<bf16_t>::widen(ld16(static_cast<const bf16_t*>(which ? p.v_new : p.k_new) + src), v);
-  } else {
-    const float* f = static_cast<const float*>(which ? p.v_new : p.k_new) + src;
-    elem<float>::widen(ld16(f), v);
-    elem<float>::widen(ld16(f + 4), v + 4);
-  }
-  C* out = static_cast<C*>(const_cast<void*>(which ? p.v_cache : p.k_cache)) + dst;
-  if constexpr (sizeof(C) == 2) {
-    *reinterpret_cast<uint4*>(out) = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
-                                                pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
-  } else {
-    reinterpret_cast<float4*>(out)[0] = make_float4(v[0], v[1], v[2], v[3]);
-    reinterpret_cast<float4*>(out)[1] = make_float4(v[4], v[5], v[6], v[7]);
-  }
+    return 0;
+  });
+  elem<C>::store8(static_cast<C*>(const_cast<void*>(which ? p.v_cache : p.k_cache)) + dst, v);
 }
 
 // Partials cross workgroups through loads that miss the CU's L1 (the sc1
@@ -344,7 +305,7 @@ __device__ __forceinline__ void arrive_and_merge(const DecodeParams& p, const Wo
 }
 
 // ---------------------------------------------------------------------------
-// bf16 cache: MFMA kernel
+// 16-bit caches (bf16, fp16): MFMA tile
 // ---------------------------------------------------------------------------
 template <int HD, int VT_BYTES, int NW> struct MfmaLds {
   static constexpr int RED_STRIDE = HD + 4;              // floats per head in the merge area
@@ -352,23 +313,9 @@ template <int HD, int VT_BYTES, int NW> struct MfmaLds {
   static constexpr int BYTES = (NW * VT_BYTES > RED_BYTES ? NW * VT_BYTES : RED_BYTES);
 };
 // bytes per key row of a wave's V tile: the row plus 16 bytes against bank conflicts
-template <int HD> constexpr int kVStrideBf16 = HD * 2 + 16;
+template <int HD> constexpr int kVStride16 = HD * 2 + 16;
 
 constexpr int kTabCap = 1024;  // block ids of a partition staged in LDS
-
-__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-// ds_read_b64_tr_b16: in each group of 16 lanes, lane i receives 16-bit
-// element (i % 4) of the 8-byte chunks addressed by lanes 4j + i/4, j = 0..3.
-__device__ __forceinline__ bf16x4 lds_read_tr(const char* p) {
-  // C-style cast: the generic LDS pointer becomes an address-space-3 pointer.
-  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) i16x4*)(p));
-  return __builtin_bit_cast(bf16x4, v);
-}
 
 // One wave's K/V registers for a 64-key tile: this lane's key of each of the
 // four 16-key subtiles, KS 16-byte chunks (8 dims) each.
@@ -417,8 +364,8 @@ __device__ __forceinline__ void softmax_tile(WaveAcc<HD>& st, f32x4 (&s)[NS], fl
   for (int d = 0; d < HD / 16; d++) st.acc[d] *= alpha;
 }
 
-template <int HD>
-__device__ __forceinline__ void load_tile(TileRegs<HD / 32>& r, const bf16_t* kc, const bf16_t* vc,
+template <typename T, int HD>
+__device__ __forceinline__ void load_tile(TileRegs<HD / 32>& r, const T* kc, const T* vc,
                                           int key0, int key_end, int kv_stride, int bs_shift,
                                           const int* tab, int tab_base, int col) {
   constexpr int KS = HD / 32;
@@ -437,11 +384,12 @@ __device__ __forceinline__ void load_tile(TileRegs<HD / 32>& r, const bf16_t* kc
   }
 }
 
-template <int HD>
+template <typename T, int HD>
 __device__ __forceinline__ void compute_tile(WaveAcc<HD>& st, const TileRegs<HD / 32>& r,
-                                             const bf16x8* qb, int key0, int key_end,
+                                             const typename mma16<T>::v8* qb, int key0, int key_end,
                                              float scale_log2, char* vt, int col, int grp) {
-  constexpr int V_STRIDE = kVStrideBf16<HD>;
+  using M = mma16<T>;
+  constexpr int V_STRIDE = kVStride16<HD>;
   constexpr int KS = HD / 32;
   constexpr int DT = HD / 16;
   // S^T = K . Q^T: lane holds head `col`, keys key0 + 16i + 4grp + j
@@ -451,7 +399,7 @@ __device__ __forceinline__ void compute_tile(WaveAcc<HD>& st, const TileRegs<HD 
     s[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < KS; ks++)
-      s[i] = mfma16(__builtin_bit_cast(bf16x8, r.k[i][ks]), qb[ks], s[i]);
+      s[i] = M::mma(__builtin_bit_cast(typename M::v8, r.k[i][ks]), qb[ks], s[i]);
   }
   float mt = -INFINITY;
 #pragma unroll
@@ -493,20 +441,20 @@ __device__ __forceinline__ void compute_tile(WaveAcc<HD>& st, const TileRegs<HD 
   // dim 16*d + col of four keys, the same keys P^T holds for that group.
 #pragma unroll
   for (int kk = 0; kk < 2; kk++) {
-    bf16x8 pb;
+    typename M::v8 pb;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      pb[j] = static_cast<__bf16>(s[2 * kk][j]);
-      pb[4 + j] = static_cast<__bf16>(s[2 * kk + 1][j]);
+      pb[j] = static_cast<typename M::scalar>(s[2 * kk][j]);
+      pb[4 + j] = static_cast<typename M::scalar>(s[2 * kk + 1][j]);
     }
     const char* r_lo = vt + (kk * 32 + grp * 4 + (col >> 2)) * V_STRIDE + (col & 3) * 8;
     const char* r_hi = r_lo + 16 * V_STRIDE;
 #pragma unroll
     for (int d = 0; d < DT; d++) {
-      const bf16x4 lo = lds_read_tr(r_lo + d * 32);
-      const bf16x4 hi = lds_read_tr(r_hi + d * 32);
-      const bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      st.acc[d] = mfma16(a, pb, st.acc[d]);
+      const typename M::v4 lo = lds_read_tr16<T>(r_lo + d * 32);
+      const typename M::v4 hi = lds_read_tr16<T>(r_hi + d * 32);
+      const typename M::v8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      st.acc[d] = M::mma(a, pb, st.acc[d]);
     }
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -519,16 +467,17 @@ __device__ __forceinline__ void compute_tile(WaveAcc<HD>& st, const TileRegs<HD 
 // pipelining, cross-wave and cross-workgroup merge) is shared.
 template <typename KV, int HD> struct DecodeTile;
 
-// bf16 cache: 64-key tiles on v_mfma_f32_16x16x32_bf16 (load_tile,
+// 16-bit cache of element type T: 64-key tiles on the 16x16x32 MFMA of T (load_tile,
 // compute_tile above).
-template <int HD> struct DecodeTile<bf16_t, HD> {
+template <typename T, int HD> struct DecodeTile16 {
   static constexpr int kKeys = kTile;
-  static constexpr int VT_BYTES = kKeys * kVStrideBf16<HD>;
+  static constexpr int VT_BYTES = kKeys * kVStride16<HD>;
   static constexpr bool kPipe = HD == 64;  // double-buffered where the registers allow it
   static constexpr bool kEarly = HD == 64;  // first tile issued before the item is read (HD 128: too many registers)
   static constexpr int kLaneElems = 8;     // dims per lane group and k-step
   using Regs = TileRegs<HD / 32>;
-  struct QOp { bf16x8 b[HD / 32]; };
+  using M = mma16<T>;
+  struct QOp { typename M::v8 b[HD / 32]; };
   template <typename Src>
   __device__ __forceinline__ static void load_q(QOp& q, const Src& src, bool ok, int grp) {
     // unconditional 16-byte loads (the row pointer is valid for every
@@ -540,23 +489,23 @@ template <int HD> struct DecodeTile<bf16_t, HD> {
 #pragma unroll
     for (int ks = 0; ks < HD / 32; ks++)
 #pragma unroll
-      for (int e = 0; e < 8; e++) q.b[ks][e] = static_cast<__bf16>(ok ? f[ks][e] : 0.f);
+      for (int e = 0; e < 8; e++) q.b[ks][e] = static_cast<typename M::scalar>(ok ? f[ks][e] : 0.f);
   }
-  __device__ __forceinline__ static const bf16_t* lane_base(const void* cache, int kvh, int grp) {
-    return static_cast<const bf16_t*>(cache) + kvh * HD + grp * 8;
+  __device__ __forceinline__ static const T* lane_base(const void* cache, int kvh, int grp) {
+    return static_cast<const T*>(cache) + kvh * HD + grp * 8;
   }
-  __device__ __forceinline__ static void load(Regs& r, const bf16_t* kc, const bf16_t* vc, int key0, int key_end,
+  __device__ __forceinline__ static void load(Regs& r, const T* kc, const T* vc, int key0, int key_end,
                                               int kv_stride, int bs_shift, const int* tab, int tab_base, int col) {
-    load_tile<HD>(r, kc, vc, key0, key_end, kv_stride, bs_shift, tab, tab_base, col);
+    load_tile<T, HD>(r, kc, vc, key0, key_end, kv_stride, bs_shift, tab, tab_base, col);
   }
   __device__ __forceinline__ static void compute(WaveAcc<HD>& st, const Regs& r, const QOp& q, int key0, int key_end,
                                                  float scale_log2, char* vt, int col, int grp) {
-    compute_tile<HD>(st, r, q.b, key0, key_end, scale_log2, vt, col, grp);
+    compute_tile<T, HD>(st, r, q.b, key0, key_end, scale_log2, vt, col, grp);
   }
   // The first tile, addressed without the item: key rel0 + 16i + col of the
   // item reads block ids[rel >> bs_shift] (the plan pads ids with -1 past
   // the item, so those keys read block 0 and are masked by the caller).
-  __device__ __forceinline__ static void load_direct(Regs& r, const bf16_t* kc, const bf16_t* vc, int rel0,
+  __device__ __forceinline__ static void load_direct(Regs& r, const T* kc, const T* vc, int rel0,
                                                      const int32_t* ids, int n_ids, int bs_shift, int kv_stride,
                                                      int64_t num_blocks, int col) {
     constexpr int KS = HD / 32;
@@ -575,6 +524,9 @@ template <int HD> struct DecodeTile<bf16_t, HD> {
     }
   }
 };
+
+template <int HD> struct DecodeTile<bf16_t, HD> : DecodeTile16<bf16_t, HD> {};
+template <int HD> struct DecodeTile<f16_t, HD> : DecodeTile16<f16_t, HD> {};
 
 // fp32 cache: 32-key tiles on v_mfma_f32_16x16x4_f32, exact fp32 products.
 //   S^T = K . Q^T: lane (col, grp) holds key col of each 16-key subtile with

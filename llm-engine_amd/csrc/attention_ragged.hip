@@ -24,46 +24,48 @@ namespace {
 constexpr int kRaggedThreads = chk::kThreads;
 constexpr int kDecodeWaves = kRaggedThreads / kWave;
 
-template <int HD> union RaggedSmem {
+template <typename KV, int HD> union RaggedSmem {
   chk::ChunkSmem<HD> c;
-  dec::DecodeSmem<bf16_t, HD, kDecodeWaves> d;
+  dec::DecodeSmem<KV, HD, kDecodeWaves> d;
 };
 
-template <typename ACT, int HD>
+template <typename ACT, typename KV, int HD>
 __global__ __launch_bounds__(kRaggedThreads) void ragged_kernel(DecodeParams dp, ChunkParams cp) {
-  __shared__ RaggedSmem<HD> sm;
+  __shared__ RaggedSmem<KV, HD> sm;
   const int n_chunk_wg = cp.n_items * cp.kv_heads;
   const int b = blockIdx.x;
   if (b < n_chunk_wg) {
     // item-major within each kv head, as the chunk kernel's 2-D grid (the
     // plan places a split tile's partitions at item indices equal modulo 8)
-    chk::chunk_wg<ACT, HD>(cp, sm.c, b % cp.n_items, b / cp.n_items);
+    chk::chunk_wg<ACT, KV, HD>(cp, sm.c, b % cp.n_items, b / cp.n_items);
   } else {
     // item-major within each kv head, as the decode kernel's 2-D grid: the
     // plan places a split row's partitions at item indices equal modulo 8,
     // so they share an XCD in either launch
     const int d = b - n_chunk_wg;
-    dec::decode_wg<ACT, bf16_t, HD, kDecodeWaves>(dp, sm.d, d % dp.n_rows, d / dp.n_rows, 0);
+    dec::decode_wg<ACT, KV, HD, kDecodeWaves>(dp, sm.d, d % dp.n_rows, d / dp.n_rows, 0);
   }
 }
 
 }  // namespace
 
 
-hipError_t attention_ragged(const DecodeParams& d, const ChunkParams& c, int act_bf16, hipStream_t s) {
+hipError_t attention_ragged(const DecodeParams& d, const ChunkParams& c, int act_dtype, int kv_dtype,
+                            hipStream_t s) {
   const int64_t n = static_cast<int64_t>(c.n_items + d.n_rows) * c.kv_heads;
   if (n <= 0) return hipSuccess;
   if (n > 0x7fffffff || d.kv_heads != c.kv_heads || d.head_dim != c.head_dim || !d.items)
     return hipErrorInvalidValue;
   const dim3 grid(static_cast<unsigned>(n));
-  if (c.head_dim == 64) {
-    if (act_bf16) ragged_kernel<bf16_t, 64><<<grid, kRaggedThreads, 0, s>>>(d, c);
-    else ragged_kernel<float, 64><<<grid, kRaggedThreads, 0, s>>>(d, c);
-  } else {
-    if (act_bf16) ragged_kernel<bf16_t, 128><<<grid, kRaggedThreads, 0, s>>>(d, c);
-    else ragged_kernel<float, 128><<<grid, kRaggedThreads, 0, s>>>(d, c);
-  }
-  return hipGetLastError();
+  return with_dtype(act_dtype, [&](auto a) {
+    return with_dtype16(kv_dtype, [&](auto k) {
+      using ACT = decltype(a);
+      using KV = decltype(k);
+      if (c.head_dim == 64) ragged_kernel<ACT, KV, 64><<<grid, kRaggedThreads, 0, s>>>(d, c);
+      else ragged_kernel<ACT, KV, 128><<<grid, kRaggedThreads, 0, s>>>(d, c);
+      return hipGetLastError();
+    });
+  });
 }
 
 }  // namespace le

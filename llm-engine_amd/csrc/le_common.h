@@ -1,4 +1,4 @@
-// Device helpers shared by the gfx950 kernels: bf16 conversion, 16-byte vector
+// Device helpers shared by the gfx950 kernels: bf16/fp16 conversion, 16-byte vector
 // loads and wave64 reductions.
 #pragma once
 
@@ -9,9 +9,12 @@ namespace le {
 
 constexpr int kWave = 64;
 
-// bf16 is carried as its raw 16-bit pattern: the cache, the activations and the
-// MFMA operands all move it as bits, and widening is a shift.
+// bf16 and fp16 are carried as raw 16-bit patterns: the caches, the
+// activations and the MFMA operands all move them as bits.
 struct bf16_t {
+  uint16_t bits;
+};
+struct f16_t {
   uint16_t bits;
 };
 
@@ -19,8 +22,8 @@ __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w 
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
 // Round to nearest even, inf/nan passed through unrounded: the same rule as the
-// host conversion the caches are checked against, so a stored bf16 is
-// bit-identical to a host-rounded one.
+// host conversion the caches are checked against (tensor.h:23-28), so a
+// stored bf16 is bit-identical to a host-rounded one.
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
   const uint32_t u = __float_as_uint(f);
   if ((u & 0x7f800000u) == 0x7f800000u) return u >> 16;
@@ -31,7 +34,30 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
 }
 
-// Element type traits: VEC = elements per 16-byte load.
+// fp16: the hardware conversion rounds to nearest even, with subnormal
+// results and overflow to infinity, as the host rule (tensor.h:38-56) does.
+// A NaN becomes the host rule's quiet NaN (sign kept, payload 0x200).
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) & 0x8000u) | 0x7e00u;
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h & 0xffffu)));
+}
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  return f32_to_f16_bits(lo) | (f32_to_f16_bits(hi) << 16);
+}
+__device__ __forceinline__ float f16_lo(uint32_t w) { return f16_bits_to_f32(w); }
+__device__ __forceinline__ float f16_hi(uint32_t w) { return f16_bits_to_f32(w >> 16); }
+
+__device__ __forceinline__ uint4 ld16(const void* p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+
+// Element type traits. VEC = elements per 16-byte load; widen turns those 16
+// bytes into floats; load/store move 4 or 8 consecutive elements as floats
+// (stores round to the type); round(x) is x as the type would store it.
 template <typename T> struct elem;
 template <> struct elem<float> {
   static constexpr int VEC = 4;
@@ -41,24 +67,83 @@ template <> struct elem<float> {
   }
   __device__ __forceinline__ static float load1(const float* p) { return *p; }
   __device__ __forceinline__ static void store1(float* p, float v) { *p = v; }
-};
-template <> struct elem<bf16_t> {
-  static constexpr int VEC = 8;
-  __device__ __forceinline__ static void widen(const uint4& r, float* o) {
-    o[0] = bf16_lo(r.x); o[1] = bf16_hi(r.x); o[2] = bf16_lo(r.y); o[3] = bf16_hi(r.y);
-    o[4] = bf16_lo(r.z); o[5] = bf16_hi(r.z); o[6] = bf16_lo(r.w); o[7] = bf16_hi(r.w);
+  __device__ __forceinline__ static float round(float x) { return x; }
+  __device__ __forceinline__ static void load4(const float* p, float* o) { widen(ld16(p), o); }
+  __device__ __forceinline__ static void load8(const float* p, float* o) {
+    widen(ld16(p), o);
+    widen(ld16(p + 4), o + 4);
   }
-  __device__ __forceinline__ static float load1(const bf16_t* p) {
-    return __uint_as_float(static_cast<uint32_t>(p->bits) << 16);
+  __device__ __forceinline__ static void store4(float* p, const float* v) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
   }
-  __device__ __forceinline__ static void store1(bf16_t* p, float v) {
-    p->bits = static_cast<uint16_t>(f32_to_bf16_bits(v));
+  __device__ __forceinline__ static void store8(float* p, const float* v) {
+    store4(p, v);
+    store4(p + 4, v + 4);
   }
 };
 
-__device__ __forceinline__ uint4 ld16(const void* p) {
-  return *reinterpret_cast<const uint4*>(p);
+// The two 16-bit types share everything but the conversions.
+template <typename T, float (*LO)(uint32_t), float (*HI)(uint32_t), uint32_t (*TO)(float),
+          uint32_t (*PACK)(float, float)>
+struct elem16 {
+  static constexpr int VEC = 8;
+  __device__ __forceinline__ static void widen(const uint4& r, float* o) {
+    o[0] = LO(r.x); o[1] = HI(r.x); o[2] = LO(r.y); o[3] = HI(r.y);
+    o[4] = LO(r.z); o[5] = HI(r.z); o[6] = LO(r.w); o[7] = HI(r.w);
+  }
+  __device__ __forceinline__ static float load1(const T* p) { return LO(p->bits); }
+  __device__ __forceinline__ static void store1(T* p, float v) { p->bits = static_cast<uint16_t>(TO(v)); }
+  __device__ __forceinline__ static float round(float x) { return LO(TO(x)); }
+  __device__ __forceinline__ static void load4(const T* p, float* o) {
+    const uint2 r = *reinterpret_cast<const uint2*>(p);
+    o[0] = LO(r.x); o[1] = HI(r.x); o[2] = LO(r.y); o[3] = HI(r.y);
+  }
+  __device__ __forceinline__ static void load8(const T* p, float* o) { widen(ld16(p), o); }
+  __device__ __forceinline__ static void store4(T* p, const float* v) {
+    *reinterpret_cast<uint2*>(p) = make_uint2(PACK(v[0], v[1]), PACK(v[2], v[3]));
+  }
+  __device__ __forceinline__ static void store8(T* p, const float* v) {
+    *reinterpret_cast<uint4*>(p) =
+        make_uint4(PACK(v[0], v[1]), PACK(v[2], v[3]), PACK(v[4], v[5]), PACK(v[6], v[7]));
+  }
+};
+template <> struct elem<bf16_t> : elem16<bf16_t, bf16_lo, bf16_hi, f32_to_bf16_bits, pack_bf16x2> {};
+template <> struct elem<f16_t> : elem16<f16_t, f16_lo, f16_hi, f32_to_f16_bits, pack_f16x2> {};
+
+// The 16-bit MFMA operand types and the 16x16x32 MFMA of each 16-bit type.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+template <typename T> struct mma16;
+template <> struct mma16<bf16_t> {
+  using scalar = __bf16;
+  using v8 = bf16x8;
+  using v4 = bf16x4;
+  __device__ __forceinline__ static f32x4 mma(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct mma16<f16_t> {
+  using scalar = _Float16;
+  using v8 = f16x8;
+  using v4 = f16x4;
+  __device__ __forceinline__ static f32x4 mma(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// ds_read_b64_tr_b16: in each group of 16 lanes, lane i receives 16-bit
+// element (i % 4) of the 8-byte chunks addressed by lanes 4j + i/4, j = 0..3.
+template <typename T>
+__device__ __forceinline__ typename mma16<T>::v4 lds_read_tr16(const char* p) {
+  // C-style cast: the generic LDS pointer becomes an address-space-3 pointer.
+  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4*)(p));
+  return __builtin_bit_cast(typename mma16<T>::v4, v);
 }
+
 // K/V history load (read once per step). A non-temporal variant measured no
 // faster on the decode rows.
 __device__ __forceinline__ uint4 ld16_stream(const void* p) { return ld16(p); }
@@ -152,6 +237,21 @@ __device__ __forceinline__ void st_coherent8(__amdgpu_buffer_rsrc_t r, uint32_t 
 __device__ __forceinline__ uint4 ld_coherent16u(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
   const u32x4raw v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCachePolicySc1);
   return __builtin_bit_cast(uint4, v);
+}
+
+// Calls f with a value of the element type a dtype code names (0 fp32,
+// 1 bf16, 2 fp16), so host code picks a kernel instantiation in one place.
+template <typename F>
+__host__ __device__ inline auto with_dtype(int dt, F&& f) {
+  if (dt == 1) return f(bf16_t{});
+  if (dt == 2) return f(f16_t{});
+  return f(float{});
+}
+// The same over the 16-bit types only (the MFMA kernels' operand types).
+template <typename F>
+__host__ __device__ inline auto with_dtype16(int dt, F&& f) {
+  if (dt == 2) return f(f16_t{});
+  return f(bf16_t{});
 }
 
 }  // namespace le

@@ -38,14 +38,17 @@ struct ChunkItem {
   int32_t tok_begin, n_q, blk_begin, blk_end, part0, part_stride, seq, part;
 };
 
-hipError_t kv_cache_write(const void* k, const void* v, int src_bf16, const int32_t* slots,
-                          void* kc, void* vc, int cache_bf16, int n_tokens, int kv_dim,
+// Element types are passed as le_dtype codes: 0 fp32, 1 bf16, 2 fp16.
+constexpr int kDtF32 = 0, kDtBF16 = 1, kDtF16 = 2;
+
+hipError_t kv_cache_write(const void* k, const void* v, int src_dtype, const int32_t* slots,
+                          void* kc, void* vc, int cache_dtype, int n_tokens, int kv_dim,
                           int64_t num_slots, hipStream_t stream);
-hipError_t rope_kv_cache_write(const void* qkv, int act_bf16, int64_t row_stride, const float* bias,
+hipError_t rope_kv_cache_write(const void* qkv, int act_dtype, int64_t row_stride, const float* bias,
                                const int32_t* positions, const int32_t* slots, const float* cos_t,
                                const float* sin_t, int max_pos, int n_tokens, int q_heads,
                                int kv_heads, int head_dim, void* q_out, void* kc, void* vc,
-                               int cache_bf16, int64_t num_slots, hipStream_t stream);
+                               int cache_dtype, int64_t num_slots, hipStream_t stream);
 
 struct DecodeParams {
   const void* q;
@@ -58,13 +61,13 @@ struct DecodeParams {
   void* out;
   PartialLayout parts;
   // With a plan and a pure decode step: the step's new K/V rows ([n_tokens]
-  // [kv_heads * head_dim], dtype new_bf16 ? bf16 : fp32). The last partition
+  // [kv_heads * head_dim], element type new_dtype). The last partition
   // of each row stores its row (for its kv head) at slots[token] before any
   // K/V load of the launch reads it. Null: the rows are already in the cache.
   const void* k_new;
   const void* v_new;
   const int32_t* slots;
-  int new_bf16;
+  int new_dtype;
   int64_t num_slots;
   // Rows straight from the stacked QKV projection (rope_max_pos > 0): q and
   // the new K/V rows are read at rope_row_stride elements per token (q, k_new
@@ -98,7 +101,7 @@ struct DecodeParams {
 // is being captured and the device is not checked yet, or on any error.
 bool xcd_placement_holds(hipStream_t stream);
 
-hipError_t attention_decode(const DecodeParams& p, int act_bf16, int kv_bf16, hipStream_t stream);
+hipError_t attention_decode(const DecodeParams& p, int act_dtype, int kv_dtype, hipStream_t stream);
 
 struct ChunkParams {
   const void* q;
@@ -121,11 +124,12 @@ struct ChunkParams {
   int l2_local;
 };
 
-hipError_t attention_chunk(const ChunkParams& p, int act_bf16, hipStream_t stream);
+hipError_t attention_chunk(const ChunkParams& p, int act_dtype, int kv_dtype, hipStream_t stream);
 
-// A mixed step's chunk rows and decode rows (bf16 cache, plan items) in one
+// A mixed step's chunk rows and decode rows (16-bit cache, plan items) in one
 // launch: chunk workgroups first, then decode workgroups.
-hipError_t attention_ragged(const DecodeParams& d, const ChunkParams& c, int act_bf16, hipStream_t stream);
+hipError_t attention_ragged(const DecodeParams& d, const ChunkParams& c, int act_dtype, int kv_dtype,
+                            hipStream_t stream);
 
 // Split count for the reference-shaped entry point, where the host does not
 // know the context lengths: enough workgroups to cover the chip several times.

@@ -19,30 +19,6 @@
 namespace le {
 namespace {
 
-template <typename T> struct vec4;
-template <> struct vec4<float> {
-  __device__ __forceinline__ static void load(const float* p, float* o) {
-    const float4 r = *reinterpret_cast<const float4*>(p);
-    o[0] = r.x; o[1] = r.y; o[2] = r.z; o[3] = r.w;
-  }
-  __device__ __forceinline__ static void store(float* p, const float* v) {
-    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
-  }
-  __device__ __forceinline__ static float round(float x) { return x; }
-};
-template <> struct vec4<bf16_t> {
-  __device__ __forceinline__ static void load(const bf16_t* p, float* o) {
-    const uint2 r = *reinterpret_cast<const uint2*>(p);
-    o[0] = bf16_lo(r.x); o[1] = bf16_hi(r.x); o[2] = bf16_lo(r.y); o[3] = bf16_hi(r.y);
-  }
-  __device__ __forceinline__ static void store(bf16_t* p, const float* v) {
-    *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-  }
-  __device__ __forceinline__ static float round(float x) {
-    return __uint_as_float(f32_to_bf16_bits(x) << 16);
-  }
-};
-
 // No contraction: a*c - b*s is two roundings of products and one of the
 // difference, as the reference's CPU op computes it.
 #pragma clang fp contract(off)
@@ -70,13 +46,13 @@ __global__ __launch_bounds__(256) void rope_kv_write_kernel(
       const int i = (u - h * gph) * 4;
       const int off = h * hd + i;
       float a[4], b[4];
-      vec4<T>::load(row + off, a);
-      vec4<T>::load(row + off + half, b);
+      elem<T>::load4(row + off, a);
+      elem<T>::load4(row + off + half, b);
       if (bias) {
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          a[e] = vec4<T>::round(a[e] + bias[off + e]);
-          b[e] = vec4<T>::round(b[e] + bias[off + half + e]);
+          a[e] = elem<T>::round(a[e] + bias[off + e]);
+          b[e] = elem<T>::round(b[e] + bias[off + half + e]);
         }
       }
       float ra[4], rb[4];
@@ -90,25 +66,25 @@ __global__ __launch_bounds__(256) void rope_kv_write_kernel(
       }
       if (h < nh) {
         T* dst = q_out + static_cast<int64_t>(t) * qd + off;
-        vec4<T>::store(dst, ra);
-        vec4<T>::store(dst + half, rb);
+        elem<T>::store4(dst, ra);
+        elem<T>::store4(dst + half, rb);
       } else if (kv_ok) {
         C* dst = kc + slot * kvd + (off - qd);
-        vec4<C>::store(dst, ra);
-        vec4<C>::store(dst + half, rb);
+        elem<C>::store4(dst, ra);
+        elem<C>::store4(dst + half, rb);
       }
     } else if (kv_ok) {
       const int j = (u - n_rope) * 8;
       float x[8];
-      vec4<T>::load(row + qd + kvd + j, x);
-      vec4<T>::load(row + qd + kvd + j + 4, x + 4);
+      elem<T>::load4(row + qd + kvd + j, x);
+      elem<T>::load4(row + qd + kvd + j + 4, x + 4);
       if (bias) {
 #pragma unroll
-        for (int e = 0; e < 8; e++) x[e] = vec4<T>::round(x[e] + bias[qd + kvd + j + e]);
+        for (int e = 0; e < 8; e++) x[e] = elem<T>::round(x[e] + bias[qd + kvd + j + e]);
       }
       C* dst = vc + slot * kvd + j;
-      vec4<C>::store(dst, x);
-      vec4<C>::store(dst + 4, x + 4);
+      elem<C>::store4(dst, x);
+      elem<C>::store4(dst + 4, x + 4);
     }
   }
 }
@@ -126,18 +102,18 @@ hipError_t launch(const void* qkv, int64_t stride, const float* bias, const int3
 
 }  // namespace
 
-hipError_t rope_kv_cache_write(const void* qkv, int act_bf16, int64_t row_stride, const float* bias,
+hipError_t rope_kv_cache_write(const void* qkv, int act_dtype, int64_t row_stride, const float* bias,
                                const int32_t* positions, const int32_t* slots, const float* cos_t,
                                const float* sin_t, int max_pos, int n_tokens, int q_heads,
                                int kv_heads, int head_dim, void* q_out, void* kc, void* vc,
-                               int cache_bf16, int64_t num_slots, hipStream_t stream) {
-#define LE_ROPE_ARGS                                                                             \
-  qkv, row_stride, bias, positions, slots, cos_t, sin_t, max_pos, n_tokens, q_heads, kv_heads, \
-      head_dim, q_out, kc, vc, num_slots, stream
-  if (act_bf16)
-    return cache_bf16 ? launch<bf16_t, bf16_t>(LE_ROPE_ARGS) : launch<bf16_t, float>(LE_ROPE_ARGS);
-  return cache_bf16 ? launch<float, bf16_t>(LE_ROPE_ARGS) : launch<float, float>(LE_ROPE_ARGS);
-#undef LE_ROPE_ARGS
+                               int cache_dtype, int64_t num_slots, hipStream_t stream) {
+  return with_dtype(act_dtype, [&](auto a) {
+    return with_dtype(cache_dtype, [&](auto c) {
+      return launch<decltype(a), decltype(c)>(qkv, row_stride, bias, positions, slots, cos_t, sin_t, max_pos,
+                                              n_tokens, q_heads, kv_heads, head_dim, q_out, kc, vc, num_slots,
+                                              stream);
+    });
+  });
 }
 
 }  // namespace le

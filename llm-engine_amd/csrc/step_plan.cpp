@@ -16,6 +16,7 @@
 // rows of a longer slice (a prefill chunk) are cut into tiles of chunk_q_tile
 // consecutive positions; each tile's keys 0..last position are cut into
 // partitions of ~chunk_partition_tokens, one ChunkItem each, run on MFMA.
+// (fp16 caches are planned like bf16 ones.)
 // With an fp32 cache, chunk rows are decode rows (exact fp32 products on the
 // fp32 MFMA). Split rows of either kind are merged inside their launch by
 // the last partition to finish.
@@ -128,7 +129,7 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
   le_plan_config cfg = *cfg_in;
   if (cfg.block_size <= 0 || cfg.q_heads <= 0 || cfg.kv_heads <= 0 || cfg.head_dim <= 0)
     return LE_EINVAL;
-  if (cfg.kv_dtype != LE_F32 && cfg.kv_dtype != LE_BF16) return LE_EINVAL;
+  if (cfg.kv_dtype != LE_F32 && cfg.kv_dtype != LE_BF16 && cfg.kv_dtype != LE_F16) return LE_EINVAL;
   if ((cfg.flags & ~(LE_PLAN_WRITE_THROUGH | LE_PLAN_TWO_LAUNCHES)) != 0 || cfg.reserved_ != 0)
     return LE_EINVAL;
   const int bs = cfg.block_size;
@@ -142,7 +143,7 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
     // 16.3 us, 1024 17.1 us, 512 18.0 us).
     int64_t ctx = 0;
     for (int i = 0; i < n_slices; i++)
-      if (slices[i].len == 1 || cfg.kv_dtype != LE_BF16)
+      if (slices[i].len == 1 || cfg.kv_dtype == LE_F32)
         for (int r = 0; r < slices[i].len; r++) ctx += slices[i].start + r + 1;
     const int64_t per_kvh = std::max<int64_t>(1, kTargetItems / cfg.kv_heads);
     int64_t part = (ctx + per_kvh - 1) / per_kvh;
@@ -152,7 +153,7 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
     // of the launch; splitting the decode rows further only adds merges
     // (config 3: 22.7 us with the rule above, 22.4 us with 2048 tokens).
     bool chunk_rows = false;
-    for (int i = 0; i < n_slices; i++) chunk_rows |= slices[i].len > 1 && cfg.kv_dtype == LE_BF16;
+    for (int i = 0; i < n_slices; i++) chunk_rows |= slices[i].len > 1 && cfg.kv_dtype != LE_F32;
     if (chunk_rows) part = std::max<int64_t>(part, kMixedStepPartition);
     cfg.partition_tokens = static_cast<int32_t>(std::min<int64_t>(part, kMaxAutoPartition));
   }
@@ -161,7 +162,7 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
   if (cfg.chunk_q_tile != 16 && cfg.chunk_q_tile != 32) return LE_EUNSUPPORTED;  // MFMA row tiles
   const int dec_pb = round_to_blocks(cfg.partition_tokens, bs);
   const int chk_pb = round_to_blocks(cfg.chunk_partition_tokens, bs);
-  const bool mfma_chunks = cfg.kv_dtype == LE_BF16;
+  const bool mfma_chunks = cfg.kv_dtype != LE_F32;  // 16-bit caches: chunk rows on MFMA tiles
   const int max_decode_parts = std::max(1, kMaxMergeEntries / (cfg.q_heads / cfg.kv_heads));
 
   // ---- sizes, and validation of every slice against its table ----

@@ -20,6 +20,7 @@ LE_ENOSPACE = -3
 LE_EDEVICE = -4
 LE_F32 = 0
 LE_BF16 = 1
+LE_F16 = 2
 LE_PLAN_WRITE_THROUGH = 1
 LE_PLAN_TWO_LAUNCHES = 2
 

@@ -15,15 +15,17 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import LE_BF16, LE_F32, PlanConfig, StepPlan, StepSlice, check
+from ._lib import LE_BF16, LE_F16, LE_F32, PlanConfig, StepPlan, StepSlice, check
 
 
-def _dt(t: torch.Tensor) -> int:
-    if t.dtype == torch.float32:
-        return LE_F32
-    if t.dtype == torch.bfloat16:
-        return LE_BF16
-    raise TypeError(f"unsupported dtype {t.dtype}: expected float32 or bfloat16")
+_DTYPES = {torch.float32: LE_F32, torch.bfloat16: LE_BF16, torch.float16: LE_F16}
+
+
+def _dt(t: torch.Tensor | torch.dtype) -> int:
+    d = t if isinstance(t, torch.dtype) else t.dtype
+    if d not in _DTYPES:
+        raise TypeError(f"unsupported dtype {d}: expected float32, bfloat16 or float16")
+    return _DTYPES[d]
 
 
 def _stream(stream) -> ctypes.c_void_p:
@@ -166,8 +168,7 @@ class Plan:
                  block_size: int, kv_dtype: torch.dtype, partition_tokens: int = 0,
                  chunk_partition_tokens: int = 0, device="cuda", pin: bool = True, chunk_q_tile: int = 0,
                  flags: int = 0):
-        self.cfg = PlanConfig(q_heads, kv_heads, head_dim, block_size,
-                              LE_BF16 if kv_dtype == torch.bfloat16 else LE_F32,
+        self.cfg = PlanConfig(q_heads, kv_heads, head_dim, block_size, _dt(kv_dtype),
                               partition_tokens, chunk_q_tile, chunk_partition_tokens, flags, 0)
         keep = []
         arr = (StepSlice * max(1, len(slices)))()

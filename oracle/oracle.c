@@ -40,6 +40,58 @@ void orc_bf16_to_f32_n(const uint16_t* in, float* out, size_t n) {
   for (size_t i = 0; i < n; i++) out[i] = orc_bf16_to_f32(in[i]);
 }
 
+/* ---------------- tensor.h:29-56 (fp16) ----------------
+ * IEEE binary16 from binary32, round to nearest even: the result of
+ * tensor.h's f32_to_f16 for every input (NaN becomes the quiet NaN with the
+ * sign kept and payload 0x200). Written from the format: a normal result
+ * rebiases the exponent and rounds the 13 dropped mantissa bits; a subnormal
+ * result is the value in units of 2^-24, rounded. */
+uint16_t orc_f32_to_f16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  const uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u);  /* NaN */
+  if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* >= 65520 (and inf): infinity */
+  if (a <= 0x33000000u) return sign;                        /* <= 2^-25: zero (2^-25 ties to even 0) */
+  if (a < 0x38800000u) {                                    /* below 2^-14: subnormal result */
+    const uint32_t m = (a & 0x7fffffu) | 0x800000u;         /* 24-bit significand */
+    const int shift = 126 - (int)(a >> 23);                 /* 14..24 */
+    uint32_t q = m >> shift;
+    const uint32_t rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1);
+    q += (rem > half || (rem == half && (q & 1u))) ? 1u : 0u;  /* may carry into the smallest normal */
+    return (uint16_t)(sign | q);
+  }
+  const uint32_t r = a - 0x38000000u; /* exponent rebiased from 127 to 15 */
+  uint32_t q = r >> 13;
+  const uint32_t rem = r & 0x1fffu;
+  q += (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) ? 1u : 0u;
+  return (uint16_t)(sign | q);
+}
+
+float orc_f16_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  uint32_t u;
+  if (e == 0) {
+    const float v = (float)m * 0x1p-24f; /* exact: m < 2^10 */
+    return sign ? -v : v;
+  }
+  if (e == 0x1f) u = sign | 0x7f800000u | (m << 13);
+  else u = sign | ((e + 112u) << 23) | (m << 13);
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+void orc_f32_to_f16_n(const float* in, uint16_t* out, size_t n) {
+  for (size_t i = 0; i < n; i++) out[i] = orc_f32_to_f16(in[i]);
+}
+
+void orc_f16_to_f32_n(const uint16_t* in, float* out, size_t n) {
+  for (size_t i = 0; i < n; i++) out[i] = orc_f16_to_f32(in[i]);
+}
+
 /* ---------------- kv_cache.h:29-31 ---------------- */
 int64_t orc_slot(const int32_t* blocks, int pos, int block_size) {
   return (int64_t)blocks[pos / block_size] * block_size + pos % block_size;

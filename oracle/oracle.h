@@ -28,6 +28,11 @@ uint16_t orc_f32_to_bf16(float f);
 float orc_bf16_to_f32(uint16_t h);
 void orc_f32_to_bf16_n(const float* in, uint16_t* out, size_t n);
 void orc_bf16_to_f32_n(const uint16_t* in, float* out, size_t n);
+/* ---- scalar formats: include/engine/tensor.h:29-56 (fp16, the reference's __half) ---- */
+uint16_t orc_f32_to_f16(float f);
+float orc_f16_to_f32(uint16_t h);
+void orc_f32_to_f16_n(const float* in, uint16_t* out, size_t n);
+void orc_f16_to_f32_n(const uint16_t* in, float* out, size_t n);
 
 /* ---- paging: include/engine/kv_cache.h:29-31 ---- */
 int64_t orc_slot(const int32_t* blocks, int pos, int block_size);

@@ -46,6 +46,8 @@ def lib() -> ctypes.CDLL:
         L.orc_bf16_to_f32.argtypes = [ctypes.c_uint16]
         L.orc_f32_to_bf16_n.argtypes = [_P, _P, ctypes.c_size_t]
         L.orc_bf16_to_f32_n.argtypes = [_P, _P, ctypes.c_size_t]
+        L.orc_f32_to_f16_n.argtypes = [_P, _P, ctypes.c_size_t]
+        L.orc_f16_to_f32_n.argtypes = [_P, _P, ctypes.c_size_t]
         L.orc_slot.restype = ctypes.c_int64
         L.orc_slot.argtypes = [_P, _i, _i]
         L.orc_pack_step.argtypes = [_P, _i, _i] + [_P] * 8
@@ -79,6 +81,10 @@ def ref() -> ctypes.CDLL:
         R = ctypes.CDLL(str(REF_LIB))
         R.ref_f32_to_bf16.restype = ctypes.c_uint16
         R.ref_f32_to_bf16.argtypes = [_f]
+        R.ref_f32_to_f16.restype = ctypes.c_uint16
+        R.ref_f32_to_f16.argtypes = [_f]
+        R.ref_f16_to_f32.restype = _f
+        R.ref_f16_to_f32.argtypes = [ctypes.c_uint16]
         R.ref_bf16_to_f32.restype = _f
         R.ref_bf16_to_f32.argtypes = [ctypes.c_uint16]
         R.ref_slot.restype = ctypes.c_int64
@@ -161,14 +167,36 @@ def pack_step(slices, block_size: int) -> Packed:
     return Packed(*[x[:k] for x, k in zip(a, sizes)])
 
 
+def f32_to_f16(x) -> np.ndarray:
+    """fp32 -> fp16 (orc_f32_to_f16: tensor.h:38-56, round to nearest even),
+    returned as a float16 array."""
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(a.shape, dtype=np.uint16)
+    lib().orc_f32_to_f16_n(ptr(a), ptr(out), a.size)
+    return out.view(np.float16)
+
+
+def f16_to_f32(h) -> np.ndarray:
+    """fp16 (float16 array or uint16 bits) -> fp32 (orc_f16_to_f32, exact)."""
+    a = np.ascontiguousarray(h).view(np.uint16)
+    out = np.empty(a.shape, dtype=np.float32)
+    lib().orc_f16_to_f32_n(ptr(a), ptr(out), a.size)
+    return out
+
+
 def paged_attention(q, k_cache, v_cache, tables, table_offset, token_seq, token_pos, q_heads,
                     kv_heads, head_dim, block_size, scale, threads=None):
-    """q: [N, q_heads*head_dim] f32; caches [slots, kv_heads*head_dim] as f32 or
-    uint16 (bf16 bits). Returns out [N, q_heads*head_dim] f32."""
+    """q: [N, q_heads*head_dim] f32; caches [slots, kv_heads*head_dim] as f32,
+    uint16 (bf16 bits) or float16. Returns out [N, q_heads*head_dim] f32.
+    fp16 caches are widened to fp32 first (exact), as the reference's fp16
+    kernels widen each element in registers (attention_decode.cu:94-103)."""
     q = np.ascontiguousarray(q, dtype=np.float32)
     n = q.shape[0]
     out = np.zeros((n, q_heads * head_dim), dtype=np.float32)
     args = [np.ascontiguousarray(x, dtype=np.int32) for x in (tables, table_offset, token_seq, token_pos)]
+    if k_cache.dtype == np.float16:
+        k_cache = f16_to_f32(k_cache)
+        v_cache = f16_to_f32(v_cache)
     kc = np.ascontiguousarray(k_cache)
     vc = np.ascontiguousarray(v_cache)
     fn = lib().orc_paged_attention_bf16kv if kc.dtype == np.uint16 else lib().orc_paged_attention
@@ -183,6 +211,11 @@ def store_kv(k, v, slots, k_cache, v_cache):
     v = np.ascontiguousarray(v, dtype=np.float32)
     s = np.ascontiguousarray(slots, dtype=np.int32)
     kv_dim = k.shape[1]
+    if k_cache.dtype == np.float16:  # store_kv.cu:20-36 into an fp16 cache
+        ok = (s >= 0) & (s < k_cache.shape[0])
+        k_cache[s[ok]] = f32_to_f16(k[ok])
+        v_cache[s[ok]] = f32_to_f16(v[ok])
+        return
     fn = lib().orc_store_kv_bf16 if k_cache.dtype == np.uint16 else lib().orc_store_kv
     fn(ptr(k), ptr(v), ptr(s), ptr(k_cache), ptr(v_cache), k.shape[0], kv_dim)
 

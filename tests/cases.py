@@ -17,7 +17,7 @@ class AttnCase:
     block_size: int
     num_blocks: int
     q: np.ndarray            # [N, q_heads*head_dim] f32
-    k_cache: np.ndarray      # [num_blocks*bs, kv_heads*head_dim] f32 or uint16 (bf16 bits)
+    k_cache: np.ndarray      # [num_blocks*bs, kv_heads*head_dim] f32, uint16 (bf16 bits) or float16
     v_cache: np.ndarray
     tables: np.ndarray       # concatenated block tables (int32)
     table_offset: np.ndarray  # [S]
@@ -45,7 +45,7 @@ def loguniform_ctx(rng: np.random.Generator, n: int, lo: int, hi: int) -> np.nda
 
 
 def make_case(ctx, q_heads=14, kv_heads=2, head_dim=64, block_size=16, num_blocks=None,
-              q_len=None, seed=0, kv_bf16=False, fill="normal") -> AttnCase:
+              q_len=None, seed=0, kv_bf16=False, fill="normal", kv_f16=False) -> AttnCase:
     """ctx[s] = context length of sequence s after this step; q_len[s] = rows of
     sequence s in the step (1 = decode row; >1 = the last q_len positions, a
     prefill chunk). Tables are a random permutation of the pool, so no two
@@ -79,6 +79,10 @@ def make_case(ctx, q_heads=14, kv_heads=2, head_dim=64, block_size=16, num_block
         import oracle  # test infrastructure: host RNE rounding identical to tensor.h
         k = oracle.f32_to_bf16(k)
         v = oracle.f32_to_bf16(v)
+    elif kv_f16 and fill == "normal":
+        import oracle
+        k = oracle.f32_to_f16(k)
+        v = oracle.f32_to_f16(v)
     return AttnCase(q_heads, kv_heads, head_dim, block_size, num_blocks, q, k, v, tables,
                     table_offset, nblk.astype(np.int32), token_seq, token_pos, seq_start,
                     q_len.astype(np.int32))

@@ -10,9 +10,16 @@ from cases import AttnCase
 
 
 def to_dev_cache(c: np.ndarray, dev) -> torch.Tensor:
+    """uint16 arrays hold bf16 bits; float16 and float32 map to themselves."""
     if c.dtype == np.uint16:
         return torch.from_numpy(c.view(np.int16)).to(dev).view(torch.bfloat16)
     return torch.from_numpy(c).to(dev)
+
+
+def from_dev_cache(c: torch.Tensor) -> np.ndarray:
+    if c.dtype == torch.bfloat16:
+        return c.view(torch.int16).cpu().numpy().view(np.uint16)
+    return c.cpu().numpy()
 
 
 def i32(a, dev) -> torch.Tensor:
@@ -24,6 +31,9 @@ def device_q(case: AttnCase, act: torch.dtype, dev) -> tuple[torch.Tensor, np.nd
     if act == torch.bfloat16:
         qh = oracle.bf16_to_f32(oracle.f32_to_bf16(case.q))
         return torch.from_numpy(qh).to(dev).to(torch.bfloat16), qh
+    if act == torch.float16:
+        qh = oracle.f32_to_f16(case.q).astype(np.float32)
+        return torch.from_numpy(qh).to(dev).to(torch.float16), qh
     return torch.from_numpy(case.q).to(dev), case.q
 
 
@@ -48,3 +58,26 @@ def slices_of(case: AttnCase):
         out.append(Slice(s, start, ln, True, case.blocks_of(s),
                          np.zeros(start + ln, dtype=np.int32)))
     return out
+
+
+# Element types by name, as the parity tests parametrize them.
+TORCH_DT = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+
+
+def round_to(a: np.ndarray, dt: str) -> np.ndarray:
+    """fp32 values as a `dt` tensor holds them (host RNE rules of tensor.h)."""
+    a = np.asarray(a, dtype=np.float32)
+    if dt == "bf16":
+        return oracle.bf16_to_f32(oracle.f32_to_bf16(a))
+    if dt == "f16":
+        return oracle.f32_to_f16(a).astype(np.float32)
+    return a
+
+
+def random_cache(rng: np.random.Generator, shape, dt: str) -> np.ndarray:
+    """A host cache in the layout to_dev_cache takes; 16-bit caches hold
+    arbitrary bit patterns (a scatter must leave untouched slots as they are)."""
+    if dt == "f32":
+        return rng.standard_normal(shape, dtype=np.float32)
+    bits = rng.integers(0, 2 ** 16, size=shape).astype(np.uint16)
+    return bits if dt == "bf16" else bits.view(np.float16)

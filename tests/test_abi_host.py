@@ -19,7 +19,11 @@ ROOT = Path(__file__).resolve().parent.parent
 
 def declared_symbols():
     syms = set()
+    # the C ABI headers; le_cuda_kernels.h (C++, the reference's launcher
+    # names, in the bridge library) is checked by test_bridge_exports_reference_signatures
     for h in (ROOT / "include").glob("*.h"):
+        if h.name == "le_cuda_kernels.h":
+            continue
         text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
         for m in re.finditer(r"^\s*(?!static)[A-Za-z_][\w\s\*]*?\b(le_\w+)\s*\(", text, flags=re.M):
             syms.add(m.group(1))
@@ -214,3 +218,25 @@ def test_plan_rejects_slices_outgrowing_their_sequence_table():
     plan = _plan([Slice(7, 0, 1, False, short, toks), Slice(8, 150, 1, True, long, toks)])
     assert plan.plan.n_seqs == 2
     assert list(plan.host_array("slots")) == [5 * 16, 9 * 16 + 150 % 16]
+
+
+def test_bridge_exports_reference_signatures():
+    """libllm_engine_amd_bridge.so exports the reference's launcher names with
+    its argument lists (cuda_kernels.h:43-64, __half buffers, hipStream_t),
+    plus the two registration calls declared in include/le_cuda_kernels.h."""
+    import subprocess
+    lib = ROOT / "llm-engine_amd" / "lib" / "libllm_engine_amd_bridge.so"
+    ctypes.CDLL(str(lib))
+    syms = subprocess.run(["nm", "-DC", str(lib)], capture_output=True, text=True, check=True).stdout
+    h = "__half const*"
+    want = [
+        f"engine::launch_store_kv({h}, {h}, int const*, __half*, __half*, int, int, ihipStream_t*)",
+        f"engine::launch_attention_decode({h}, {h}, {h}, int const*, int const*, int const*, int const*, "
+        "__half*, int, int, int, int, int, float, ihipStream_t*)",
+        f"engine::launch_attention_decode_gqa({h}, {h}, {h}, int const*, int const*, int const*, int const*, "
+        "__half*, int, int, int, int, int, float, ihipStream_t*)",
+        "engine::le_bridge_set_workspace(void*, unsigned long)",
+        "engine::le_bridge_set_cache_slots(long)",
+    ]
+    for w in want:
+        assert w in syms, w

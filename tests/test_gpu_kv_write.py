@@ -5,57 +5,52 @@ import pytest
 import torch
 
 import oracle
-from gpu_util import i32, to_dev_cache
+from gpu_util import TORCH_DT, from_dev_cache, i32, random_cache, round_to, to_dev_cache
 
 pytestmark = pytest.mark.gpu
 
 
-def _run(src_bf16, cache_bf16, n_tokens, kv_dim, num_blocks, bs, seed, pad_every=0):
+def _run(src, cache, n_tokens, kv_dim, num_blocks, bs, seed, pad_every=0):
     dev = torch.device("cuda:0")
     rng = np.random.default_rng(seed)
     slots_total = num_blocks * bs
     slots = rng.permutation(slots_total)[:n_tokens].astype(np.int32)
     if pad_every:
         slots[::pad_every] = -1
-    k = rng.standard_normal((n_tokens, kv_dim), dtype=np.float32)
-    v = rng.standard_normal((n_tokens, kv_dim), dtype=np.float32)
-    if src_bf16:  # the device source is bf16; the oracle sees the same values
-        k = oracle.bf16_to_f32(oracle.f32_to_bf16(k))
-        v = oracle.bf16_to_f32(oracle.f32_to_bf16(v))
-    cdt = np.uint16 if cache_bf16 else np.float32
-    init_k = rng.integers(0, 2**16, size=(slots_total, kv_dim)).astype(cdt) if cache_bf16 else \
-        rng.standard_normal((slots_total, kv_dim), dtype=np.float32)
+    # the device source is `src`; the oracle sees the same values
+    k = round_to(rng.standard_normal((n_tokens, kv_dim), dtype=np.float32), src)
+    v = round_to(rng.standard_normal((n_tokens, kv_dim), dtype=np.float32), src)
+    init_k = random_cache(rng, (slots_total, kv_dim), cache)
     init_v = init_k[::-1].copy()
     ok = slots >= 0
     want_k, want_v = init_k.copy(), init_v.copy()
     oracle.store_kv(k[ok], v[ok], slots[ok], want_k, want_v)
 
     from llm_engine_amd import kernels
-    tdt = torch.bfloat16 if src_bf16 else torch.float32
-    kd = torch.from_numpy(k).to(dev).to(tdt)
-    vd = torch.from_numpy(v).to(dev).to(tdt)
+    kd = torch.from_numpy(k).to(dev).to(TORCH_DT[src])
+    vd = torch.from_numpy(v).to(dev).to(TORCH_DT[src])
     kc, vc = to_dev_cache(init_k, dev), to_dev_cache(init_v, dev)
     kernels.store_kv(kd, vd, i32(slots, dev), kc, vc)
     torch.cuda.synchronize()
-    got_k = kc.cpu().view(torch.int16).numpy().view(np.uint16) if cache_bf16 else kc.cpu().numpy()
-    got_v = vc.cpu().view(torch.int16).numpy().view(np.uint16) if cache_bf16 else vc.cpu().numpy()
-    assert np.array_equal(got_k.view(np.uint8), want_k.view(np.uint8))
-    assert np.array_equal(got_v.view(np.uint8), want_v.view(np.uint8))
+    assert np.array_equal(from_dev_cache(kc).view(np.uint8), want_k.view(np.uint8))
+    assert np.array_equal(from_dev_cache(vc).view(np.uint8), want_v.view(np.uint8))
 
 
-@pytest.mark.parametrize("src_bf16,cache_bf16", [(False, False), (False, True), (True, True), (True, False)])
-def test_kv_write_config3_step(gpu, src_bf16, cache_bf16):
-    """544 rows of kv_dim 128 into a fragmented 16384-block pool (config 3)."""
-    _run(src_bf16, cache_bf16, 544, 128, 16384, 16, seed=1)
+@pytest.mark.parametrize("src,cache", [(s, c) for s in ("f32", "bf16", "f16") for c in ("f32", "bf16", "f16")])
+def test_kv_write_config3_step(gpu, src, cache):
+    """544 rows of kv_dim 128 into a fragmented 16384-block pool (config 3),
+    every source/cache type pair (fp16 is the reference's __half)."""
+    _run(src, cache, 544, 128, 16384, 16, seed=1)
 
 
 def test_kv_write_padding_and_shapes(gpu):
-    _run(False, True, 1000, 256, 512, 16, seed=2, pad_every=7)  # TinyLlama kv_dim 256
-    _run(False, False, 1, 128, 4, 16, seed=3)
-    _run(True, True, 4096, 128, 4096, 16, seed=4)
+    _run("f32", "bf16", 1000, 256, 512, 16, seed=2, pad_every=7)  # TinyLlama kv_dim 256
+    _run("f32", "f32", 1, 128, 4, 16, seed=3)
+    _run("bf16", "bf16", 4096, 128, 4096, 16, seed=4)
+    _run("f16", "f16", 777, 256, 1024, 16, seed=9, pad_every=5)
 
 
-def _run_fused(act_bf16, cache_bf16, n_tokens, q_heads, kv_heads, head_dim, num_blocks, seed,
+def _run_fused(act, cache, n_tokens, q_heads, kv_heads, head_dim, num_blocks, seed,
                bias=True, pad_every=0, bad_pos_every=0, stride_pad=0, max_pos=4096, theta=1e6):
     """le_rope_kv_cache_write against the oracle's own sequence: bias add
     (rounded to the activation dtype, as a separate add stores it), RoPE
@@ -76,7 +71,7 @@ def _run_fused(act_bf16, cache_bf16, n_tokens, q_heads, kv_heads, head_dim, num_
         pos[2::bad_pos_every] = -1
     qkv = rng.standard_normal((n_tokens, row), dtype=np.float32)
     b = rng.standard_normal(qd + 2 * kvd, dtype=np.float32) if bias else None
-    rnd = (lambda a: oracle.bf16_to_f32(oracle.f32_to_bf16(a))) if act_bf16 else (lambda a: a)
+    rnd = lambda a: round_to(a, act)
     qkv = rnd(qkv)
     cos_t, sin_t = oracle.rope_tables(head_dim, max_pos, theta)
 
@@ -90,17 +85,14 @@ def _run_fused(act_bf16, cache_bf16, n_tokens, q_heads, kv_heads, head_dim, num_
     oracle.rope(xr, np.where(ok_pos, pos, 0), cos_t, sin_t, q_heads + kv_heads, head_dim)
     want_q = rnd(np.where(ok_pos[:, None], xr[:, :qd], 0.0).astype(np.float32))
     k_rows, v_rows = xr[:, qd:qd + kvd], x[:, qd + kvd:]
-    cdt = np.uint16 if cache_bf16 else np.float32
-    init_k = rng.integers(0, 2**16, size=(slots_total, kvd)).astype(cdt) if cache_bf16 else \
-        rng.standard_normal((slots_total, kvd), dtype=np.float32)
+    init_k = random_cache(rng, (slots_total, kvd), cache)
     init_v = init_k[::-1].copy()
     want_k, want_v = init_k.copy(), init_v.copy()
     ok = (slots >= 0) & ok_pos
     oracle.store_kv(np.ascontiguousarray(k_rows[ok]), np.ascontiguousarray(v_rows[ok]), slots[ok], want_k, want_v)
 
     from llm_engine_amd import kernels
-    tdt = torch.bfloat16 if act_bf16 else torch.float32
-    qkv_d = torch.from_numpy(qkv).to(dev).to(tdt)
+    qkv_d = torch.from_numpy(qkv).to(dev).to(TORCH_DT[act])
     kc, vc = to_dev_cache(init_k, dev), to_dev_cache(init_v, dev)
     bias_d = None if b is None else torch.from_numpy(b).to(dev)
     q = kernels.rope_store_kv(qkv_d, i32(pos, dev), i32(slots, dev), torch.from_numpy(cos_t).to(dev),
@@ -109,22 +101,23 @@ def _run_fused(act_bf16, cache_bf16, n_tokens, q_heads, kv_heads, head_dim, num_
     got_q = q.float().cpu().numpy()
     assert np.array_equal(got_q.view(np.uint32), want_q.view(np.uint32)), \
         f"q mismatch: max|diff| {np.abs(got_q - want_q).max()}"
-    got_k = kc.cpu().view(torch.int16).numpy().view(np.uint16) if cache_bf16 else kc.cpu().numpy()
-    got_v = vc.cpu().view(torch.int16).numpy().view(np.uint16) if cache_bf16 else vc.cpu().numpy()
-    assert np.array_equal(got_k.view(np.uint8), want_k.view(np.uint8))
-    assert np.array_equal(got_v.view(np.uint8), want_v.view(np.uint8))
+    assert np.array_equal(from_dev_cache(kc).view(np.uint8), want_k.view(np.uint8))
+    assert np.array_equal(from_dev_cache(vc).view(np.uint8), want_v.view(np.uint8))
 
 
-@pytest.mark.parametrize("act_bf16,cache_bf16", [(False, False), (False, True), (True, True)])
-def test_rope_kv_write_qwen_step(gpu, act_bf16, cache_bf16):
+@pytest.mark.parametrize("act,cache", [("f32", "f32"), ("f32", "bf16"), ("bf16", "bf16"), ("f16", "f16"),
+                                       ("f32", "f16")])
+def test_rope_kv_write_qwen_step(gpu, act, cache):
     """Qwen2.5-0.5B shape (14/2 x 64, qkv bias), a 544-row mixed step into a
     fragmented 16384-block pool."""
-    _run_fused(act_bf16, cache_bf16, 544, 14, 2, 64, 16384, seed=5)
+    _run_fused(act, cache, 544, 14, 2, 64, 16384, seed=5)
 
 
 def test_rope_kv_write_edges(gpu):
     """TinyLlama shape without bias; padding slots, out-of-range positions,
     a padded qkv row stride, a single token, head_dim 128."""
-    _run_fused(True, True, 300, 32, 4, 64, 1024, seed=6, bias=False, pad_every=5, theta=1e4, max_pos=2048)
-    _run_fused(False, False, 257, 14, 2, 64, 512, seed=7, bad_pos_every=9, stride_pad=8)
-    _run_fused(False, True, 1, 8, 1, 128, 4, seed=8)
+    _run_fused("bf16", "bf16", 300, 32, 4, 64, 1024, seed=6, bias=False, pad_every=5, theta=1e4, max_pos=2048)
+    _run_fused("f32", "f32", 257, 14, 2, 64, 512, seed=7, bad_pos_every=9, stride_pad=8)
+    _run_fused("f32", "bf16", 1, 8, 1, 128, 4, seed=8)
+    _run_fused("f16", "f16", 300, 32, 4, 64, 1024, seed=10, pad_every=5, bad_pos_every=11, theta=1e4,
+               max_pos=2048)

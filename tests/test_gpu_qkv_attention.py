@@ -11,20 +11,20 @@ import torch
 
 import oracle
 from cases import make_case
-from gpu_util import max_abs, oracle_out, slices_of, to_dev_cache
+from gpu_util import TORCH_DT, max_abs, oracle_out, slices_of, to_dev_cache
 
 pytestmark = pytest.mark.gpu
 
 
-def _run(gpu, *, act_bf16, kv_bf16, bias, ctx, q_len=None, q_heads=14, kv_heads=2, head_dim=64,
+def _run(gpu, *, act, kv, bias, ctx, q_len=None, q_heads=14, kv_heads=2, head_dim=64,
          block_size=16, max_pos=4096, partition_tokens=None, stride_pad=0, seed=0, theta=1e6):
     from llm_engine_amd import kernels
     rng = np.random.default_rng(seed)
     case = make_case(ctx, q_len=q_len, q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim,
-                     block_size=block_size, seed=seed, kv_bf16=kv_bf16)
+                     block_size=block_size, seed=seed, kv_bf16=kv == "bf16", kv_f16=kv == "f16")
     n = len(case.token_pos)
     qd, kvd = q_heads * head_dim, kv_heads * head_dim
-    tdt = torch.bfloat16 if act_bf16 else torch.float32
+    tdt = TORCH_DT[act]
     qkv = torch.from_numpy(rng.standard_normal((n, qd + 2 * kvd + stride_pad), dtype=np.float32)).to(gpu).to(tdt)
     b = torch.from_numpy(rng.standard_normal(qd + 2 * kvd, dtype=np.float32)).to(gpu) if bias else None
     cos_t, sin_t = (torch.from_numpy(t).to(gpu) for t in oracle.rope_tables(head_dim, max_pos, theta))
@@ -42,41 +42,42 @@ def _run(gpu, *, act_bf16, kv_bf16, bias, ctx, q_len=None, q_heads=14, kv_heads=
     got = kernels.ragged_paged_attention_qkv(qkv, b, cos_t, sin_t, kc2, vc2, plan, case.scale)
     torch.cuda.synchronize()
     fused = plan.plan.n_tokens == plan.plan.n_seqs and plan.plan.n_chunk_items == 0
-    print(f"qkv attention act_bf16={act_bf16} kv_bf16={kv_bf16} bias={bias} rows={n} "
+    print(f"qkv attention act={act} kv={kv} bias={bias} rows={n} "
           f"in-launch={fused} parts={plan.plan.n_parts}")
-    bits = (lambda t: t.cpu().view(torch.int16)) if act_bf16 else (lambda t: t.cpu().view(torch.int32))
+    bits = (lambda t: t.cpu().view(torch.int16)) if act != "f32" else (lambda t: t.cpu().view(torch.int32))
     assert torch.equal(bits(got), bits(want)), f"output differs: max|diff| {max_abs(got.float().cpu(), want.float().cpu())}"
-    cbits = (lambda t: t.cpu().view(torch.int16)) if kv_bf16 else (lambda t: t.cpu().view(torch.int32))
+    cbits = (lambda t: t.cpu().view(torch.int16)) if kv != "f32" else (lambda t: t.cpu().view(torch.int32))
     assert torch.equal(cbits(kc2), cbits(kc1)), "k cache differs"
     assert torch.equal(cbits(vc2), cbits(vc1)), "v cache differs"
     return case, q, got, kc2, vc2
 
 
-@pytest.mark.parametrize("act_bf16,kv_bf16", [(False, False), (False, True), (True, True), (True, False)])
+@pytest.mark.parametrize("act,kv", [("f32", "f32"), ("f32", "bf16"), ("bf16", "bf16"), ("bf16", "f32"),
+                                    ("f16", "f16"), ("f32", "f16")])
 @pytest.mark.parametrize("bias", [False, True])
-def test_qkv_decode_step(gpu, act_bf16, kv_bf16, bias):
+def test_qkv_decode_step(gpu, act, kv, bias):
     """Decode rows only (the in-launch path), split and unsplit rows
     (partition 256), Qwen2.5-0.5B's shape with and without its qkv bias."""
-    _run(gpu, act_bf16=act_bf16, kv_bf16=kv_bf16, bias=bias, ctx=[1, 17, 300, 1500, 64, 2049, 4096],
+    _run(gpu, act=act, kv=kv, bias=bias, ctx=[1, 17, 300, 1500, 64, 2049, 4096],
          partition_tokens=256, seed=61)
 
 
-@pytest.mark.parametrize("kv_bf16", [False, True])
-def test_qkv_mixed_step(gpu, kv_bf16):
+@pytest.mark.parametrize("act,kv", [("bf16", "f32"), ("bf16", "bf16"), ("f16", "f16")])
+def test_qkv_mixed_step(gpu, act, kv):
     """A prefill chunk among decode rows: the scratch-q path (chunk tiles with
     a bf16 cache, per-row decode with fp32)."""
-    _run(gpu, act_bf16=True, kv_bf16=kv_bf16, bias=True, ctx=[600, 33, 1200, 5], q_len=[70, 1, 1, 5], seed=62)
+    _run(gpu, act=act, kv=kv, bias=True, ctx=[600, 33, 1200, 5], q_len=[70, 1, 1, 5], seed=62)
 
 
 def test_qkv_shapes_and_edges(gpu):
     """head_dim 128 with 8-key blocks, TinyLlama's 32/4 x 64 with 32-key
     blocks, a padded row stride, and positions past the RoPE tables (q = 0,
     nothing stored) on the in-launch path."""
-    _run(gpu, act_bf16=True, kv_bf16=True, bias=False, ctx=[9, 700, 2500], q_heads=8, kv_heads=1,
+    _run(gpu, act="bf16", kv="bf16", bias=False, ctx=[9, 700, 2500], q_heads=8, kv_heads=1,
          head_dim=128, block_size=8, seed=63, theta=1e4)
-    _run(gpu, act_bf16=False, kv_bf16=True, bias=True, ctx=[40, 1000, 3000, 1], q_heads=32, kv_heads=4,
+    _run(gpu, act="f32", kv="bf16", bias=True, ctx=[40, 1000, 3000, 1], q_heads=32, kv_heads=4,
          block_size=32, stride_pad=8, seed=64)
-    _run(gpu, act_bf16=False, kv_bf16=False, bias=True, ctx=[100, 1500, 2100, 3000], max_pos=2048,
+    _run(gpu, act="f32", kv="f32", bias=True, ctx=[100, 1500, 2100, 3000], max_pos=2048,
          partition_tokens=512, seed=65)
 
 
@@ -84,7 +85,7 @@ def test_qkv_decode_against_oracle(gpu):
     """The in-launch path against the oracle end to end: the oracle attends
     with the q the separate RoPE produced over the caches as stored (fp32
     throughout, tolerance 1e-3 max-abs as for the attention kernels)."""
-    case, q, got, kc, vc = _run(gpu, act_bf16=False, kv_bf16=False, bias=True, ctx=[5, 333, 2048, 4000], seed=66)
+    case, q, got, kc, vc = _run(gpu, act="f32", kv="f32", bias=True, ctx=[5, 333, 2048, 4000], seed=66)
     case.k_cache, case.v_cache = kc.cpu().numpy(), vc.cpu().numpy()
     err = max_abs(got.cpu().numpy(), oracle_out(case, q.cpu().numpy()))
     print(f"qkv attention vs oracle: max|err| {err:.3e}")

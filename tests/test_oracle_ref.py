@@ -69,10 +69,21 @@ def test_ops_match_reference_fixture():
     L.orc_silu_mul(oracle.ptr(g), oracle.ptr(np.ascontiguousarray(z["silu.up"])), g.size)
     assert bits_equal(g, z["silu.y"])
     assert np.array_equal(oracle.f32_to_bf16(z["conv.f32"]), z["conv.bf16"])
+    assert np.array_equal(oracle.f32_to_f16(z["conv.f32"]).view(np.uint16), z["conv.f16"])
     i = 0
     while f"argmax.{i}.x" in z.files:
         assert oracle.argmax(z[f"argmax.{i}.x"]) == int(z[f"argmax.{i}.y"])
         i += 1
+
+
+def test_f16_known_answers():
+    """test_tensor.cpp:13-27: bit patterns, overflow, subnormals, ties to even."""
+    h = lambda f: int(oracle.f32_to_f16(np.array([f], np.float32)).view(np.uint16)[0])
+    assert h(1.0) == 0x3C00 and h(-2.0) == 0xC000 and h(65504.0) == 0x7BFF and h(1e5) == 0x7C00
+    assert np.float32(np.array([1], np.uint16).view(np.float16)[0]) == np.float32(5.960464477539063e-08)
+    assert h(1.0 + 2 ** -11) == 0x3C00 and h(1.0 + 3 * 2 ** -11) == 0x3C02
+    for f in (0.0, 1.0, -1.0, 3.140625, 1024.0, -0.375, 2 ** -24, 65504.0):
+        assert np.float32(oracle.f32_to_f16(np.array([f], np.float32))[0]) == np.float32(f)
 
 
 def test_bf16_known_answers():
@@ -129,6 +140,22 @@ def test_scalar_ops_random_vs_reference():
     f = (rng.standard_normal(20000) * 10.0 ** rng.integers(-45, 39, 20000)).astype(np.float32)
     ref_b = np.array([R.ref_f32_to_bf16(float(v)) for v in f], dtype=np.uint16)
     assert np.array_equal(oracle.f32_to_bf16(f), ref_b)
+    # fp16 over its whole range: normals, subnormals, underflow, overflow, ties
+    g = np.concatenate([(rng.standard_normal(20000) * 2.0 ** rng.integers(-30, 18, 20000)).astype(np.float32),
+                        (np.arange(-4096, 4096) * 2.0 ** -24 + 2.0 ** -26).astype(np.float32),
+                        np.array([65504, 65519.996, 65520, -65520, 2 ** -25, 3 * 2 ** -26, np.inf, -np.inf, 0.0,
+                                  -0.0], np.float32)])
+    ref_h = np.array([R.ref_f32_to_f16(float(v)) for v in g], dtype=np.uint16)
+    assert np.array_equal(oracle.f32_to_f16(g).view(np.uint16), ref_h)
+    assert np.array_equal(g.astype(np.float16).view(np.uint16), ref_h)  # and IEEE (numpy) agrees
+    nans = np.array([0x7fc00000, 0xffc00000, 0x7f800001, 0xff812345, 0x7fffffff], np.uint32).view(np.float32)
+    ref_n = np.array([R.ref_f32_to_f16(float(v)) for v in nans], dtype=np.uint16)
+    assert np.array_equal(oracle.f32_to_f16(nans).view(np.uint16), ref_n)
+    hb = rng.integers(0, 1 << 16, 5000).astype(np.uint16)
+    hb = hb[(hb & 0x7c00) != 0x7c00]  # finite patterns
+    ref_w = np.array([R.ref_f16_to_f32(int(h)) for h in hb], dtype=np.float32)
+    assert bits_equal(oracle.f16_to_f32(hb), ref_w)
+    assert bits_equal(hb.view(np.float16).astype(np.float32), ref_w)
     x = rng.standard_normal((7, 2048), dtype=np.float32)
     w = rng.standard_normal(2048).astype(np.float32)
     y = np.empty_like(x)
