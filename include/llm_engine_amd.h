@@ -49,6 +49,8 @@ extern "C" {
 #define LE_EINVAL (-1)       /* a pointer, size or shape is invalid */
 #define LE_EUNSUPPORTED (-2) /* valid, but outside what the kernels are built for */
 #define LE_ENOSPACE (-3)     /* a caller buffer (host plan buffer, workspace) is too small */
+#define LE_ETOOLARGE (-5)    /* the step needs more scratch than le_ragged_paged_attention_noalloc
+                                has (le_noalloc_scratch_bytes); nothing was launched */
 #define LE_EDEVICE (-4)      /* a device library call (rocBLAS) failed; a failed HIP call
                                 returns its positive hipError_t instead */
 
@@ -214,6 +216,27 @@ int le_ragged_paged_attention(const void* q, le_dtype act_dtype, const void* k_c
                               const void* v_cache, le_dtype kv_dtype, int64_t num_cache_blocks,
                               const le_step_plan* plan, float scale, void* out, void* workspace,
                               size_t workspace_bytes, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * (3)(4) Ragged paged attention that allocates nothing and takes no
+ * workspace. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory or pass a workspace (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid allocation). Same arguments and
+ * the same result as le_ragged_paged_attention, bit for bit, without
+ * `workspace`: the split-K partials and arrival counters live in a static
+ * device array of le_noalloc_scratch_bytes() (32 MiB), one per GPU, held
+ * until the process ends. A step whose le_ragged_workspace_size exceeds it
+ * returns LE_ETOOLARGE and launches nothing. The first call on a device
+ * clears the array's counters with a fill kernel on `stream`; every launch
+ * leaves them at zero. All calls on one GPU share its array: calls that
+ * overlap on one GPU (different streams, different threads) race; order
+ * them on one stream.
+ * ------------------------------------------------------------------------ */
+size_t le_noalloc_scratch_bytes(void);
+
+int le_ragged_paged_attention_noalloc(const void* q, le_dtype act_dtype, const void* k_cache,
+                                      const void* v_cache, le_dtype kv_dtype, int64_t num_cache_blocks,
+                                      const le_step_plan* plan, float scale, void* out, hipStream_t stream);
 
 /* ------------------------------------------------------------------------
  * (2)+(3) The scatter and the attention of a step in one call.

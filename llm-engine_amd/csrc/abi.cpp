@@ -3,7 +3,9 @@
 // this file.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
+#include <mutex>
 #include <cstring>
 
 #include "le_internal.h"
@@ -77,6 +79,7 @@ const char* le_status_string(int status) {
     case LE_EUNSUPPORTED: return "unsupported shape";
     case LE_ENOSPACE: return "buffer too small";
     case LE_EDEVICE: return "device library failure";
+    case LE_ETOOLARGE: return "step needs more than the static scratch holds";
     default: return status > 0 ? hipGetErrorString(static_cast<hipError_t>(status)) : "unknown";
   }
 }
@@ -334,6 +337,75 @@ int le_ragged_paged_attention_qkv(const void* qkv, le_dtype act_dtype, int64_t q
   if (e != hipSuccess) return hip_status(e);
   return ragged_attention(q_scratch, act_dtype, nullptr, nullptr, LE_F32, k_cache, v_cache, kv_dtype,
                           num_cache_blocks, plan, scale, out, workspace, workspace_bytes, stream, nullptr);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// le_ragged_paged_attention_noalloc: the ragged attention with its workspace
+// in a static device array instead of a caller buffer, for callers that
+// cannot allocate. `scratch` is a host-side stand-in for the array in host
+// code: its device address comes from hipGetSymbolAddress, once per device,
+// and only that address is passed to kernels.
+namespace {
+
+constexpr size_t kScratchBytes = size_t{32} << 20;  // 32 MiB per GPU, held until the process ends
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxScratchDevices];  // device address of `scratch`, per device
+std::mutex g_scratch_mu;
+
+__global__ void fill_zero_kernel(uint4* p, size_t n16) {
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n16;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    p[i] = make_uint4(0, 0, 0, 0);
+}
+
+// The current device's address of `scratch`. On the first call on a device
+// its arrival counters are cleared with a fill kernel on `stream` (a fill
+// kernel, not a memset, so a graph that captures the first call replays
+// correctly); every launch leaves them at zero after that.
+int scratch_for_device(hipStream_t stream, void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) return LE_EINVAL;
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return static_cast<int>(e);
+      fill_zero_kernel<<<64, 256, 0, stream>>>(static_cast<uint4*>(p), kCounterRegion / 16);
+      const hipError_t f = hipGetLastError();
+      if (f != hipSuccess) return static_cast<int>(f);
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return LE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t le_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+int le_ragged_paged_attention_noalloc(const void* q, le_dtype act_dtype, const void* k_cache,
+                                      const void* v_cache, le_dtype kv_dtype, int64_t num_cache_blocks,
+                                      const le_step_plan* plan, float scale, void* out, hipStream_t stream) {
+  if (!plan) return LE_EINVAL;
+  if (plan->n_tokens == 0) return LE_OK;
+  const size_t need = le_ragged_workspace_size(plan);
+  if (need > kScratchBytes) return LE_ETOOLARGE;
+  void* ws = nullptr;
+  if (need > 0) {
+    const int st = scratch_for_device(stream, &ws);
+    if (st != LE_OK) return st;
+  }
+  return ragged_attention(q, act_dtype, nullptr, nullptr, LE_F32, k_cache, v_cache, kv_dtype, num_cache_blocks,
+                          plan, scale, out, ws, need > 0 ? kScratchBytes : 0, stream);
 }
 
 }  // extern "C"

@@ -18,6 +18,7 @@ LE_EINVAL = -1
 LE_EUNSUPPORTED = -2
 LE_ENOSPACE = -3
 LE_EDEVICE = -4
+LE_ETOOLARGE = -5
 LE_F32 = 0
 LE_BF16 = 1
 LE_F16 = 2
@@ -179,6 +180,10 @@ SIGNATURES = {
         ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
         ctypes.c_int64, ctypes.POINTER(StepPlan), ctypes.c_float, ctypes.c_void_p,
         ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "le_noalloc_scratch_bytes": (ctypes.c_size_t, []),
+    "le_ragged_paged_attention_noalloc": (ctypes.c_int, [
+        ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+        ctypes.c_int64, ctypes.POINTER(StepPlan), ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p]),
     "le_ragged_paged_attention_store": (ctypes.c_int, [
         ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
         ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.POINTER(StepPlan), ctypes.c_float,

@@ -240,3 +240,25 @@ def test_bridge_exports_reference_signatures():
     ]
     for w in want:
         assert w in syms, w
+
+
+def test_noalloc_rejects_steps_beyond_its_scratch():
+    """A step whose workspace exceeds the static scratch is rejected before
+    anything runs (LE_ETOOLARGE); an empty step is a no-op."""
+    from llm_engine_amd import _lib
+    from llm_engine_amd.kernels import Plan, Slice
+    L = _lib.load()
+    cap = int(L.le_noalloc_scratch_bytes())
+    assert cap == 32 << 20
+    # 512 rows of 8192 keys in 128-token partitions: 64 partials per row
+    rng = np.random.default_rng(1)
+    sl = [Slice(i, 8191, 1, True, rng.permutation(100000)[:512].astype(np.int32), np.zeros(8192, np.int32))
+          for i in range(512)]
+    plan = Plan(sl, 32, 4, 128, 16, torch.bfloat16, partition_tokens=128, device="cpu", pin=False)
+    assert plan.workspace_size() > cap
+    nul = ctypes.c_void_p(0)
+    assert L.le_ragged_paged_attention_noalloc(nul, 0, nul, nul, 1, 100000, ctypes.byref(plan.plan), 0.125,
+                                               nul, nul) == _lib.LE_ETOOLARGE
+    empty = Plan([], 14, 2, 64, 16, torch.bfloat16, device="cpu", pin=False)
+    assert L.le_ragged_paged_attention_noalloc(nul, 0, nul, nul, 1, 100, ctypes.byref(empty.plan), 0.125,
+                                               nul, nul) == _lib.LE_OK
