@@ -93,16 +93,21 @@ def test_second_architecture_group8(gpu):
 
 def test_bf16_kv_cache_matches_bf16_oracle(gpu):
     """fp32 model with a bf16 K/V cache against the oracle storing K/V as bf16
-    (same rounding); attention runs on MFMA with bf16 operands here, so equality
-    is expected except at near ties, which the margins show."""
+    (same rounding). Attention runs on MFMA with bf16 operands here (q and the
+    softmax weights rounded to bf16), so logits differ slightly: in lockstep
+    (one scheduler, both models continuing from the device's tokens) every
+    greedy token whose oracle top-2 margin exceeds twice the step's measured
+    logit difference equals the oracle's."""
+    from e2e_util import OracleModel, check_rows, lockstep
+    from llm_engine_amd.engine import Model
     w = qwen_small(seed=9)
     prompts = prompts_of(6, (60, 200, 17), w.arch["vocab"])
-    gpu_t, cpu_t, _ = run_both(w, prompts, [8] * 3, 256, kv="bf16")
-    agree = sum(a == b for g, c in zip(gpu_t, cpu_t) for a, b in zip(g, c))
-    total = sum(len(c) for c in cpu_t)
-    print(f"bf16 KV: {agree}/{total} tokens agree")
-    assert gpu_t[0][0] == cpu_t[0][0]
-    assert agree >= 0.9 * total
+    m = Model(w, 256, 16, dtype="f32", kv_dtype="bf16")
+    _, rows, _ = lockstep(m, OracleModel(w, 256, kv_bf16=True), prompts, [8] * 3, 256)
+    m.close()
+    checked, total = check_rows(rows, exact=False)
+    print(f"bf16 KV: {checked}/{total} tokens checked (max logit diff {max(r[3] for r in rows):.2e})")
+    assert checked >= 0.8 * total
 
 
 def test_first_step_logits_close(gpu):
@@ -188,24 +193,120 @@ def test_config5_shared_prefix_preemption(gpu, kv):
     512-token prefix (32 refcounted blocks, prefix caching on) plus unique
     suffixes, in a pool small enough that the scheduler preempts and
     recomputes. Qwen2.5-0.5B attention shape (14/2 x 64), 2 layers, vocab cut
-    to 8192 to keep the oracle's LM head cheap. Token for token against the
-    oracle driven by the same scheduler (fp32 path: exact; bf16 K/V: the
-    oracle stores bf16 too, agreement >= 90 %)."""
-    from llm_engine_amd.engine import ARCHS, sched_config, synthetic_weights
+    to 8192 to keep the oracle's LM head cheap. fp32 path: token for token
+    against the oracle driven by the same scheduler. bf16 K/V: in lockstep
+    with the oracle storing bf16 too, every token whose oracle top-2 margin
+    exceeds twice the step's logit difference equals the oracle's."""
+    from e2e_util import OracleModel, check_rows, lockstep
+    from llm_engine_amd.engine import ARCHS, Model, sched_config, synthetic_weights
     arch = dict(ARCHS["qwen2.5-0.5b"], vocab=8192)
     w = synthetic_weights(arch, 31, layers=2)
     rng = np.random.default_rng(12)
     prefix = rng.integers(0, 8192, 512).tolist()
     prompts = [prefix + rng.integers(0, 8192, int(n)).tolist() for n in rng.integers(16, 129, 128)]
     cfg = sched_config(max_num_seqs=128, max_num_batched_tokens=2048)
-    gpu_t, cpu_t, st = run_both(w, prompts, [24] * 128, 200, cfg, prefix=True, kv=kv)
-    print(f"config5 small ({kv}): {st.steps} steps, {st.preemptions} preemptions, "
-          f"{st.prompt_tokens} prompt tokens computed")
-    assert st.preemptions > 0
-    assert all(len(t) == 24 for t in gpu_t)
     if kv == "f32":
+        gpu_t, cpu_t, st = run_both(w, prompts, [24] * 128, 200, cfg, prefix=True, kv=kv)
+        print(f"config5 small ({kv}): {st.steps} steps, {st.preemptions} preemptions, "
+              f"{st.prompt_tokens} prompt tokens computed")
+        assert st.preemptions > 0
+        assert all(len(t) == 24 for t in gpu_t)
         assert gpu_t == cpu_t
-    else:
-        agree = sum(a == b for g, c in zip(gpu_t, cpu_t) for a, b in zip(g, c))
-        print(f"bf16 K/V: {agree}/{24 * 128} tokens agree")
-        assert agree >= 0.9 * 24 * 128
+        return
+    m = Model(w, 200, 16, dtype="f32", kv_dtype="bf16")
+    gpu_t, rows, _ = lockstep(m, OracleModel(w, 200, kv_bf16=True), prompts, [24] * 128, 200, cfg,
+                              prefix_caching=True)
+    m.close()
+    assert all(len(t) == 24 for t in gpu_t)
+    checked, total = check_rows(rows, exact=False)
+    print(f"config5 small (bf16 K/V): {checked}/{total} tokens checked")
+    assert checked >= 0.8 * total
+
+
+def _config4_setup(seed=41):
+    """The config-4 workload at a size the oracle finishes in seconds:
+    TinyLlama-1.1B's attention shape (32 q / 4 kv heads, head_dim 64, RoPE
+    theta 1e4, no qkv bias, untied head) with hidden 256, FFN 512, vocab 2048
+    and 2 layers; 128 requests, prompts U[64, 512], outputs U[48, 96],
+    Poisson arrivals at 8 req/s on a 0.5 s step clock; at most 64 running,
+    a 512-token step budget (chunked prefill), block 16."""
+    from e2e_util import poisson_arrival_steps
+    from llm_engine_amd.engine import ARCHS, sched_config, synthetic_weights
+    arch = dict(ARCHS["tinyllama-1.1b"], hidden=256, inter=512, vocab=2048)
+    w = synthetic_weights(arch, seed, layers=2)
+    rng = np.random.default_rng(4)
+    n = 128
+    prompts = [rng.integers(0, 2048, int(x)).tolist() for x in rng.integers(64, 513, n)]
+    max_tokens = [int(x) for x in rng.integers(48, 97, n)]
+    cfg = sched_config(max_num_seqs=64, max_num_batched_tokens=512)
+    return w, prompts, max_tokens, cfg, poisson_arrival_steps(n, 8.0, 0.5, 5)
+
+
+def test_config4_fp32_token_for_token(gpu):
+    """Config 4's shape on the fp32 path: device and oracle in lockstep under
+    one scheduler (64 sequences running at the peak, prefill chunks cut by the
+    budget): every greedy token equal."""
+    from e2e_util import OracleModel, check_rows, lockstep
+    from llm_engine_amd.engine import Model
+    w, prompts, max_tokens, cfg, arrivals = _config4_setup()
+    m = Model(w, 4096, 16, dtype="f32")
+    gen, rows, max_running = lockstep(m, OracleModel(w, 4096), prompts, max_tokens, 4096, cfg,
+                                      arrival_steps=arrivals)
+    m.close()
+    checked, total = check_rows(rows, exact=True)
+    print(f"config4 fp32: {total} tokens equal, peak {max_running} slices, "
+          f"max logit diff {max(r[3] for r in rows):.2e}")
+    assert max_running >= 64
+    assert [len(g) for g in gen] == max_tokens
+
+
+def test_config4_bf16_margin_aware(gpu):
+    """Config 4's precision: bf16 weights, activations and K/V, against the
+    oracle on the same bf16-rounded weights with a bf16 K/V cache. Every
+    greedy token whose oracle top-2 margin exceeds twice the step's measured
+    logit difference equals the oracle's."""
+    from e2e_util import OracleModel, check_rows, lockstep
+    from llm_engine_amd.engine import Model
+    w, prompts, max_tokens, cfg, arrivals = _config4_setup()
+    w = _round_weights_bf16(w)
+    m = Model(w, 4096, 16, dtype="bf16", kv_dtype="bf16")
+    gen, rows, max_running = lockstep(m, OracleModel(w, 4096, kv_bf16=True), prompts, max_tokens, 4096, cfg,
+                                      arrival_steps=arrivals)
+    m.close()
+    checked, total = check_rows(rows, exact=False)
+    errs = [r[3] / r[4] for r in rows]
+    print(f"config4 bf16: {checked}/{total} tokens checked, logit diff up to {max(errs):.2%} of the logit "
+          f"scale, peak {max_running} slices")
+    assert max_running >= 64
+    assert checked >= 0.5 * total
+
+
+def test_config4_wall_clock_arrivals(gpu):
+    """The serving loop itself (le_run_greedy) with Poisson arrival times in
+    seconds, the scheduler admitting by the wall clock: batches differ from
+    the step-clock run, and the fp32 path's tokens do not depend on the batch,
+    so each sequence's tokens equal the oracle's step-clock tokens up to the
+    first position where the oracle's top-2 margin is below 1e-4."""
+    from e2e_util import OracleModel, lockstep
+    from llm_engine_amd.engine import Model
+    w, prompts, max_tokens, cfg, arrivals = _config4_setup()
+    rng = np.random.default_rng(5)
+    arrival_s = np.cumsum(rng.exponential(1.0 / 64.0, len(prompts)))  # 64 req/s: 2 s of arrivals
+    m = Model(w, 4096, 16, dtype="f32")
+    got, stats = m.run_greedy(prompts, max_tokens, cfg, arrival_s=arrival_s)
+    want, rows, _ = lockstep(m, OracleModel(w, 4096), prompts, max_tokens, 4096, cfg, arrival_steps=arrivals)
+    m.close()
+    margins = {}
+    for _, _, margin, _, _, sid in rows:
+        margins.setdefault(sid, []).append(margin)
+    compared = 0
+    for i, (g, ww) in enumerate(zip(got, want)):
+        assert len(g) == max_tokens[i]
+        for j, (a, b) in enumerate(zip(g, ww)):
+            if margins[i][j] < 1e-4:
+                break
+            assert a == b, (i, j)
+            compared += 1
+    print(f"config4 wall clock: {stats.steps} steps, {compared}/{sum(max_tokens)} tokens compared, "
+          f"mean TTFT {stats.ttft_mean_s * 1e3:.1f} ms")
+    assert compared >= 0.9 * sum(max_tokens)
