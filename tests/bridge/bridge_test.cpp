@@ -12,8 +12,9 @@
 // K/V row is scattered by launch_store_kv first; then both attention
 // launchers run over the same step.
 //   * caches: bit-identical to the oracle's scatter of the same rows;
-//   * attention: max-abs error against the oracle below 1e-3 plus the fp16
-//     rounding of the output (2^-11 relative, |out| < 4);
+//   * attention: max-abs error against the oracle below 6e-4 (the fp16
+//     kernels' error on this shape is about 3e-4) plus the fp16 rounding of
+//     the output (2^-11 relative, |out| < 4);
 //   * launch_attention_decode and launch_attention_decode_gqa agree bit for
 //     bit (the reference requires equal greedy tokens from its two kernels,
 //     test_cuda_invariance.cpp:295-344);
@@ -161,7 +162,7 @@ int main(int argc, char** argv) {
   const std::vector<float> g1 = widen(o1);
   double err = 0.0;
   for (size_t i = 0; i < want.size(); i++) err = std::fmax(err, std::fabs(static_cast<double>(g1[i]) - want[i]));
-  const double tol = 1e-3 + 4.0 * std::ldexp(1.0, -11);
+  const double tol = 6e-4 + 4.0 * std::ldexp(1.0, -11);
   const bool same = o1 == o2;
   const bool ok = caches_equal && err < tol && same && threw;
   std::printf("bridge %s: n_seqs %d caches_equal %d max|err| %.3e (tol %.3e) decode==gqa %d throws %d\n",

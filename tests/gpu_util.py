@@ -81,3 +81,16 @@ def random_cache(rng: np.random.Generator, shape, dt: str) -> np.ndarray:
         return rng.standard_normal(shape, dtype=np.float32)
     bits = rng.integers(0, 2 ** 16, size=shape).astype(np.uint16)
     return bits if dt == "bf16" else bits.view(np.float16)
+
+
+def emulated_bar(case: AttnCase, q_f32: np.ndarray, want: np.ndarray | None = None, factor: float = 2.0) -> float:
+    """The tolerance a 16-bit-cache case is held to: `factor` times the error
+    the host emulation of the kernels' roundings (tests/precision.py) makes on
+    this very case against the fp32 oracle. Rows of prefill chunks (a
+    sequence with more than one row) are emulated as chunk-tile rows."""
+    from precision import emulate
+    dt = "bf16" if case.k_cache.dtype == np.uint16 else "f16"
+    if want is None:
+        want = oracle_out(case, q_f32)
+    chunk = np.array([case.seq_qlen[s] > 1 for s in case.token_seq])
+    return factor * float(np.abs(emulate(case, q_f32, dt, chunk) - want).max())

@@ -1,22 +1,36 @@
 """GPU parity of paged attention (reference-shaped entry and ragged plan)
 against the CPU oracle (oracle.c, restating ops.h:87-111) on identical inputs.
 
-Tolerances (max-abs against the fp32 oracle): 1e-3 with fp32 K/V, 2e-2 with
-bf16 K/V. With bf16 activations the oracle is fed the same bf16-rounded q, and
-the output's own bf16 rounding (<= 2^-9 relative, |out| < 4 here) is added."""
+Tolerances (|got - want| against the fp32 oracle, per element):
+  * fp32 K/V: 4e-6 (exact fp32 products, other summation orders; the largest
+    error seen is 1.3e-6; the north star allows 1e-3);
+  * bf16 K/V: twice the error of the host emulation of the kernels'
+    roundings on the same case (tests/precision.py: q and the softmax
+    weights rounded to bf16 for the MFMA; gpu_util.emulated_bar). The
+    emulation matches the GPU's error closely (config 2: 1.66e-3 emulated,
+    1.65e-3 measured; config 3: 5.6e-3 and 5.5e-3), and every bar stays
+    inside the north star's 2e-2.
+With bf16 activations the oracle is fed the same bf16-rounded q, and the
+output's own rounding adds 2^-8 |want| (round to nearest bf16: 2^-9
+relative, doubled for the error carried into it)."""
 import numpy as np
 import pytest
 import torch
 
 from cases import loguniform_ctx, make_case
-from gpu_util import device_q, i32, max_abs, oracle_out, slices_of, to_dev_cache
+from gpu_util import device_q, emulated_bar, i32, max_abs, oracle_out, slices_of, to_dev_cache
 from llm_engine_amd._lib import LE_PLAN_TWO_LAUNCHES, LE_PLAN_WRITE_THROUGH
 
 pytestmark = pytest.mark.gpu
 
-TOL_F32 = 1e-3
-TOL_BF16 = 2e-2
-TOL_BF16_OUT = 2e-2 + 4 * 2.0 ** -9
+TOL_F32 = 4e-6
+OUT_REL = {torch.float32: 0.0, torch.bfloat16: 2.0 ** -8}
+
+
+def within(got, want, tol, act=torch.float32) -> bool:
+    """|got - want| <= tol + OUT_REL[act] * |want|, elementwise."""
+    g, w = np.asarray(got, dtype=np.float64), np.asarray(want, dtype=np.float64)
+    return bool(np.all(np.abs(g - w) <= tol + OUT_REL[act] * np.abs(w)))
 
 
 def run_decode(case, act, dev):
@@ -42,10 +56,12 @@ def run_ragged(case, act, dev, **plan_kw):
     return out.float().cpu().numpy(), qh, plan
 
 
-def tol_for(kv_bf16, act):
-    if act == torch.bfloat16:
-        return TOL_BF16_OUT
-    return TOL_BF16 if kv_bf16 else TOL_F32
+def tol_for(case, qh, want=None):
+    """The bar for a case: TOL_F32 with an fp32 cache, else twice the
+    emulated 16-bit error of this case."""
+    if case.k_cache.dtype == np.float32:
+        return TOL_F32
+    return emulated_bar(case, qh, want)
 
 
 @pytest.mark.parametrize("kv_bf16", [False, True])
@@ -60,7 +76,7 @@ def test_decode_config2_shape(gpu, kv_bf16, act):
     want = oracle_out(case, qh)
     err = max_abs(got, want)
     print(f"config2 kv_bf16={kv_bf16} act={act}: max|err|={err:.3e}")
-    assert err < tol_for(kv_bf16, act)
+    assert within(got, want, tol_for(case, qh), act)
 
 
 @pytest.mark.parametrize("kv_bf16", [False, True])
@@ -71,9 +87,9 @@ def test_ragged_equals_reference_shaped(gpu, kv_bf16):
     a, qh = run_decode(case, torch.float32, gpu)
     b, _, plan = run_ragged(case, torch.float32, gpu)
     want = oracle_out(case, qh)
-    tol = tol_for(kv_bf16, torch.float32)
-    assert max_abs(a, want) < tol
-    assert max_abs(b, want) < tol
+    tol = tol_for(case, qh)
+    assert within(a, want, tol)
+    assert within(b, want, tol)
     assert plan.plan.n_chunk_items == 0
 
 
@@ -86,9 +102,9 @@ def test_decode_other_shapes(gpu, q_heads, kv_heads, head_dim, kv_bf16):
     case = make_case(ctx, q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim,
                      num_blocks=4096, seed=7, kv_bf16=kv_bf16)
     got, qh = run_decode(case, torch.float32, gpu)
-    assert max_abs(got, oracle_out(case, qh)) < tol_for(kv_bf16, torch.float32)
+    assert within(got, oracle_out(case, qh), tol_for(case, qh))
     got2, _, _ = run_ragged(case, torch.float32, gpu)
-    assert max_abs(got2, oracle_out(case, qh)) < tol_for(kv_bf16, torch.float32)
+    assert within(got2, oracle_out(case, qh), tol_for(case, qh))
 
 
 @pytest.mark.parametrize("block_size", [8, 32, 64])
@@ -97,9 +113,9 @@ def test_decode_block_sizes(gpu, block_size):
     ctx = loguniform_ctx(rng, 10, 1, 2000)
     case = make_case(ctx, block_size=block_size, num_blocks=2048, seed=block_size)
     got, qh = run_decode(case, torch.float32, gpu)
-    assert max_abs(got, oracle_out(case, qh)) < TOL_F32
+    assert within(got, oracle_out(case, qh), TOL_F32)
     got2, _, _ = run_ragged(case, torch.float32, gpu)
-    assert max_abs(got2, oracle_out(case, qh)) < TOL_F32
+    assert within(got2, oracle_out(case, qh), TOL_F32)
 
 
 @pytest.mark.parametrize("kv_bf16", [False, True])
@@ -114,9 +130,9 @@ def test_decode_partition_over_table_segments(gpu, kv_bf16):
     err = max_abs(got, want)
     print(f"segments kv_bf16={kv_bf16}: items {plan.plan.n_decode_items} max|err| {err:.3e}")
     assert plan.plan.n_decode_items == 3
-    assert err < tol_for(kv_bf16, torch.float32)
+    assert within(got, want, tol_for(case, qh))
     ref_shaped, _ = run_decode(case, torch.float32, gpu)
-    assert max_abs(ref_shaped, want) < tol_for(kv_bf16, torch.float32)
+    assert within(ref_shaped, want, tol_for(case, qh))
 
 
 def test_decode_edges(gpu):
@@ -126,11 +142,11 @@ def test_decode_edges(gpu):
     case = make_case(ctx, num_blocks=1024, seed=11)
     got, qh = run_decode(case, torch.float32, gpu)
     want = oracle_out(case, qh)
-    assert max_abs(got, want) < TOL_F32
+    assert within(got, want, TOL_F32)
     # one partition covering the whole context: exercises the chunked online rescale
     got2, _, plan = run_ragged(case, torch.float32, gpu, partition_tokens=16384)
     assert plan.plan.n_combine_items == 0
-    assert max_abs(got2, want) < TOL_F32
+    assert within(got2, want, TOL_F32)
     # pos 0 attends to exactly one key: output equals that V row
     v0 = case.v_cache[case.blocks_of(0)[0] * 16, :64]
     assert max_abs(got[0, :64], v0) < 1e-6
@@ -149,9 +165,9 @@ def test_chunk_rows_small(gpu, kv_bf16):
     print(f"chunk rows kv_bf16={kv_bf16}: items dec={plan.plan.n_decode_items} "
           f"chunk={plan.plan.n_chunk_items} max|err|={err:.3e}")
     assert (plan.plan.n_chunk_items > 0) == kv_bf16
-    assert err < tol_for(kv_bf16, torch.float32)
+    assert within(got, want, tol_for(case, qh))
     ref_shaped, _ = run_decode(case, torch.float32, gpu)
-    assert max_abs(ref_shaped, want) < tol_for(kv_bf16, torch.float32)
+    assert within(ref_shaped, want, tol_for(case, qh))
 
 
 @pytest.mark.parametrize("act", [torch.float32, torch.bfloat16])
@@ -169,7 +185,7 @@ def test_mixed_step_config3(gpu, act):
     want = oracle_out(case, qh)
     err = max_abs(got, want)
     print(f"config3 act={act}: max|err|={err:.3e}")
-    assert err < tol_for(True, act)
+    assert within(got, want, tol_for(case, qh), act)
 
 
 def test_mixed_step_two_launches(gpu):
@@ -188,7 +204,7 @@ def test_mixed_step_two_launches(gpu):
         print(f"two_launches={two}: chunk {plan.plan.n_chunk_items} decode {plan.plan.n_decode_items} "
               f"parts {plan.plan.n_parts} max|err| {err:.3e}")
         assert plan.plan.n_chunk_items > 0 and plan.plan.n_decode_items > 3
-        assert err < TOL_BF16
+        assert within(got, want, tol_for(case, qh))
 
 
 def test_workspace_reused_across_plans(gpu):
@@ -217,7 +233,7 @@ def test_workspace_reused_across_plans(gpu):
             err = max_abs(out.float().cpu().numpy(), oracle_out(case, qh))
             print(f"rep {rep} rows {plan.plan.n_tokens} parts {plan.plan.n_parts} "
                   f"chunk items {plan.plan.n_chunk_items}: max|err| {err:.3e}")
-            assert err < TOL_BF16
+            assert within(out.float().cpu().numpy(), oracle_out(case, qh), tol_for(case, qh))
     assert int(ws[:256 * 1024].count_nonzero().item()) == 0  # counters left at zero
 
 
@@ -236,7 +252,7 @@ def test_chunk_rows_other_shapes(gpu, q_heads, kv_heads, head_dim):
     print(f"chunk {q_heads}/{kv_heads}x{head_dim}: items {plan.plan.n_chunk_items} parts {plan.plan.n_parts} "
           f"max|err| {err:.3e}")
     assert plan.plan.n_chunk_items > 0 and plan.plan.n_parts > 0
-    assert err < TOL_BF16
+    assert within(got, want, tol_for(case, qh))
 
 
 @pytest.mark.parametrize("block_size", [8, 32, 64])
@@ -252,7 +268,7 @@ def test_chunk_rows_block_sizes(gpu, block_size):
     print(f"chunk block {block_size}: items chunk {plan.plan.n_chunk_items} decode {plan.plan.n_decode_items} "
           f"max|err| {err:.3e}")
     assert plan.plan.n_chunk_items > 0 and plan.plan.n_decode_items > 2
-    assert err < TOL_BF16_OUT
+    assert within(got, want, tol_for(case, qh), torch.bfloat16)
 
 
 def test_chunk_tile16_and_long_context(gpu):
@@ -267,7 +283,7 @@ def test_chunk_tile16_and_long_context(gpu):
         want = oracle_out(case, qh)
         err = max_abs(got, want)
         print(f"tile {tile}: items {plan.plan.n_chunk_items} parts {plan.plan.n_parts} max|err| {err:.3e}")
-        assert err < TOL_BF16
+        assert within(got, want, tol_for(case, qh))
 
 
 @pytest.mark.parametrize("kv_bf16,new_bf16", [(True, False), (True, True), (False, False)])
@@ -313,7 +329,7 @@ def test_store_then_attend(gpu, kv_bf16, new_bf16, mixed):
     err = max_abs(out.float().cpu().numpy(), oracle_out(case, qh))
     print(f"store+attend kv_bf16={kv_bf16} new_bf16={new_bf16} mixed={mixed}: parts {plan.plan.n_parts} "
           f"max|err| {err:.3e}")
-    assert err < tol_for(kv_bf16, torch.float32)
+    assert within(out.float().cpu().numpy(), oracle_out(case, qh), tol_for(case, qh))
 
 
 @pytest.mark.parametrize("seed", range(16))
@@ -347,7 +363,7 @@ def test_random_ragged_steps(gpu, seed):
     print(f"seed {seed}: {q_heads}/{kv_heads}x{head_dim} bs {block_size} kv_bf16 {kv_bf16} act {act} "
           f"rows {plan.plan.n_tokens} dec {plan.plan.n_decode_items} chunk {plan.plan.n_chunk_items} "
           f"parts {plan.plan.n_parts}: max|err| {err:.3e}")
-    assert err < tol_for(kv_bf16, act)
+    assert within(got, want, tol_for(case, qh), act)
 
 
 @pytest.mark.parametrize("kv_bf16", [False, True])
@@ -370,7 +386,7 @@ def test_split_rows_both_partial_paths(gpu, kv_bf16):
             print(f"coherent={coherent} mixed={q_len is not None}: parts {plan.plan.n_parts} "
                   f"decode items {plan.plan.n_decode_items} max|err| {err:.3e}")
             assert plan.plan.n_parts > 0 and plan.plan.n_decode_items % 8 == 0
-            assert err < tol_for(kv_bf16, torch.float32)
+            assert within(got, want, tol_for(case, qh))
 
 
 def test_graph_replays_match_eager(gpu):
@@ -393,7 +409,7 @@ def test_graph_replays_match_eager(gpu):
     eager = kernels.ragged_paged_attention(q, kc, vc, plan, case.scale, workspace=ws)
     torch.cuda.synchronize()
     want = oracle_out(case, qh)
-    assert max_abs(eager.float().cpu().numpy(), want) < TOL_BF16
+    assert within(eager.float().cpu().numpy(), want, tol_for(case, qh))
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     out = torch.empty_like(eager)

@@ -4,23 +4,21 @@ __half q, K/V caches and out; cuda_model.cu:76-78,276-285 keep fp16 weights
 and caches). The oracle sees exactly the fp16 values the device holds,
 widened to fp32 (exact), as the reference widens each element in registers.
 
-Tolerances (max-abs against the fp32 oracle), from the host emulation of the
-kernels' roundings (tests/precision.py: q and the softmax weights rounded to
-fp16 before the MFMA): config 2 emulates to 2.3e-4 and config 3 to 8.1e-4,
-so the bars are 1e-3 for decode rows and 2e-3 with chunk rows, both inside
-the north star's 2e-2 for 16-bit K/V. fp16 outputs add their own rounding
-(<= 2^-11 relative, |out| < 4)."""
+Tolerances (max-abs against the fp32 oracle): twice the error of the host
+emulation of the kernels' roundings on the same case (tests/precision.py: q
+and the softmax weights rounded to fp16 before the MFMA; emulated 2.3e-4 on
+config 2, where the GPU shows 2.9e-4, and 8.1e-4 on config 3, GPU 8.6e-4),
+inside the north star's 2e-2 for 16-bit K/V. fp16 outputs add their own
+rounding (<= 2^-11 relative, |out| < 4)."""
 import numpy as np
 import pytest
 import torch
 
 from cases import loguniform_ctx, make_case
-from gpu_util import device_q, i32, max_abs, oracle_out, slices_of, to_dev_cache
+from gpu_util import device_q, emulated_bar, i32, max_abs, oracle_out, slices_of, to_dev_cache
 
 pytestmark = pytest.mark.gpu
 
-TOL_DECODE = 1e-3
-TOL_CHUNK = 2e-3
 OUT_ROUND = 4 * 2.0 ** -11
 
 
@@ -50,7 +48,7 @@ def test_config2_f16(gpu, act):
     case = make_case(ctx, num_blocks=32768, seed=2, kv_f16=True)
     a, b, qh, _ = run_both(case, act, gpu)
     want = oracle_out(case, qh)
-    tol = TOL_DECODE + (OUT_ROUND if act == torch.float16 else 0.0)
+    tol = emulated_bar(case, qh, want) + (OUT_ROUND if act == torch.float16 else 0.0)
     ea, eb = max_abs(a, want), max_abs(b, want)
     print(f"config2 f16 act={act}: reference-shaped {ea:.3e} ragged {eb:.3e}")
     assert ea < tol and eb < tol
@@ -67,7 +65,7 @@ def test_config3_f16(gpu, act):
     a, b, qh, plan = run_both(case, act, gpu)
     assert plan.plan.n_tokens == 1056 and plan.plan.n_chunk_items > 0
     want = oracle_out(case, qh)
-    tol = TOL_CHUNK + (OUT_ROUND if act == torch.float16 else 0.0)
+    tol = emulated_bar(case, qh, want) + (OUT_ROUND if act == torch.float16 else 0.0)
     ea, eb = max_abs(a, want), max_abs(b, want)
     print(f"config3 f16 act={act}: reference-shaped {ea:.3e} ragged {eb:.3e}")
     assert ea < tol and eb < tol
@@ -85,8 +83,9 @@ def test_f16_other_shapes(gpu, q_heads, kv_heads, head_dim):
     a, b, qh, plan = run_both(case, torch.float16, gpu)
     want = oracle_out(case, qh)
     assert plan.plan.n_chunk_items > 0
-    assert max_abs(a, want) < TOL_CHUNK + OUT_ROUND
-    assert max_abs(b, want) < TOL_CHUNK + OUT_ROUND
+    tol = emulated_bar(case, qh, want) + OUT_ROUND
+    assert max_abs(a, want) < tol
+    assert max_abs(b, want) < tol
 
 
 @pytest.mark.parametrize("seed", range(6))
@@ -103,10 +102,11 @@ def test_f16_random_steps(gpu, seed):
     case = make_case(ctx, q_len=q_len, q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim, block_size=bs,
                      num_blocks=int(((ctx + bs - 1) // bs).sum()) + 64, seed=600 + seed, kv_f16=True)
     _, b, qh, plan = run_both(case, torch.float16, gpu, partition_tokens=int(rng.choice([0, 256, 640])))
-    err = max_abs(b, oracle_out(case, qh))
+    want = oracle_out(case, qh)
+    err = max_abs(b, want)
     print(f"seed {seed}: {q_heads}/{kv_heads}x{head_dim} bs {bs} rows {plan.plan.n_tokens} "
           f"parts {plan.plan.n_parts}: max|err| {err:.3e}")
-    assert err < TOL_CHUNK + OUT_ROUND
+    assert err < emulated_bar(case, qh, want) + OUT_ROUND
 
 
 def test_f16_store_then_attend(gpu):
@@ -132,4 +132,5 @@ def test_f16_store_then_attend(gpu):
     torch.cuda.synchronize()
     assert np.array_equal(kc.cpu().numpy().view(np.uint16), case.k_cache.view(np.uint16))
     assert np.array_equal(vc.cpu().numpy().view(np.uint16), case.v_cache.view(np.uint16))
-    assert max_abs(out.float().cpu().numpy(), oracle_out(case, qh)) < TOL_DECODE + OUT_ROUND
+    want = oracle_out(case, qh)
+    assert max_abs(out.float().cpu().numpy(), want) < emulated_bar(case, qh, want) + OUT_ROUND
