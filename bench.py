@@ -25,6 +25,13 @@ weights and K/V (benchmark config 4 shape) and reports decode tok/s at
 Poisson serving workload and the shared-prefix + preemption stress instead
 or as well.
 
+A config2 run also measures the target point and config3 the same way
+(fewer steps) and reports them under "target" and "config3", each with its
+own roofline ("config3" adds the chunk rows' MFMA flops and utilisation).
+"plan.pack_us" is the steady-state host cost of le_plan_step on the step
+(sizing + packing call); the e2e legs report "plan_us_per_step", the C++
+engine's own timing of le_plan_step + le_plan_upload per step.
+
 Prints ONE JSON line. `value` is algorithmic HBM bytes per step / step time:
 K/V of each kv head once (the GQA-shared minimum), q, out, block tables and
 per-row metadata, plus the K/V rows written by the scatter.
@@ -129,6 +136,171 @@ def cpu_baseline(ctx, q_len, kv_bf16: bool, budget_s: float):
                       f"in {el1:.1f} s on 1 thread (value_1_thread)"}
 
 
+def pack_cost_us(slices, kv_dt, reps=200):
+    """Steady-state host cost of le_plan_step on a step's slices (the
+    sized call and the packing call, as the engine makes them each step),
+    timed over `reps` calls through ctypes into a pinned buffer."""
+    import ctypes
+    from llm_engine_amd import _lib, kernels
+    plan = kernels.Plan(slices, Q_HEADS, KV_HEADS, HEAD_DIM, BS, kv_dt)
+    L = _lib.load()
+    arr = (_lib.StepSlice * max(1, len(slices)))()
+    keep = []
+    for i, s in enumerate(slices):
+        b = np.ascontiguousarray(s.blocks, dtype=np.int32)
+        tk = np.ascontiguousarray(s.tokens, dtype=np.int32)
+        keep += [b, tk]
+        arr[i] = _lib.StepSlice(s.seq_key, s.start, s.len, int(s.needs_logits), b.size, b.ctypes.data, tk.ctypes.data)
+    P = _lib.StepPlan()
+    buf = ctypes.c_void_p(plan.host.data_ptr())
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        L.le_plan_step(arr, len(slices), ctypes.byref(plan.cfg), None, 0, ctypes.byref(P))
+        L.le_plan_step(arr, len(slices), ctypes.byref(plan.cfg), buf, int(plan.plan.bytes), ctypes.byref(P))
+    return (time.perf_counter() - t0) / reps * 1e6
+
+
+def attention_leg(workload, kv, L, steps, warmup, partition=0, chunk_partition=0, graph=False,
+                  separate_scatter=False):
+    """The hot path over one workload for L layers per step (see the module
+    docstring); returns the fields of the JSON line for it."""
+    import torch
+    from llm_engine_amd import kernels
+    from gpu_util import slices_of
+    from cases import make_case
+
+    dev = torch.device("cuda:0")
+    kv_dt = torch.bfloat16 if kv == "bf16" else torch.float32
+    act_dt = torch.float32
+    ctx, q_len, pool = workload_shape(workload)
+    case = make_case(ctx, q_len=q_len, num_blocks=pool, seed=2, fill="none")  # tables and rows only
+    kv_dim = KV_HEADS * HEAD_DIM
+    n = int(q_len.sum())
+    g = torch.Generator(device=dev)
+    g.manual_seed(1234)
+    kc = [torch.randn(pool * BS, kv_dim, device=dev, generator=g).to(kv_dt) for _ in range(L)]
+    vc = [torch.randn(pool * BS, kv_dim, device=dev, generator=g).to(kv_dt) for _ in range(L)]
+    qs = [torch.randn(n, Q_HEADS * HEAD_DIM, device=dev, generator=g).to(act_dt) for _ in range(L)]
+    knew = [torch.randn(n, kv_dim, device=dev, generator=g).to(act_dt) for _ in range(L)]
+    vnew = [torch.randn(n, kv_dim, device=dev, generator=g).to(act_dt) for _ in range(L)]
+    outs = [torch.empty_like(qs[0]) for _ in range(L)]
+
+    slices = slices_of(case)
+    plan = kernels.Plan(slices, Q_HEADS, KV_HEADS, HEAD_DIM, BS, kv_dt,
+                        partition_tokens=partition, chunk_partition_tokens=chunk_partition)
+    pack_us = pack_cost_us(slices, kv_dt)
+    plan.upload()
+    torch.cuda.synchronize()
+    slots = plan.dev_array("slots")
+    ws = kernels.new_workspace(plan.workspace_size(), dev)
+    stream = torch.cuda.current_stream()
+    if graph:
+        stream = torch.cuda.Stream()  # capture needs a stream other than the legacy default
+        stream.wait_stream(torch.cuda.current_stream())
+
+    def attn(l, st=None):
+        kernels.ragged_paged_attention(qs[l], kc[l], vc[l], plan, case.scale, out=outs[l],
+                                       workspace=ws, stream=st or stream)
+
+    def eager_step():
+        plan.upload(stream)
+        for l in range(L):
+            if separate_scatter:
+                kernels.store_kv(knew[l], vnew[l], slots, kc[l], vc[l], stream=stream)
+                attn(l)
+            else:  # le_ragged_paged_attention_store: the scatter folded into the attention launch
+                kernels.ragged_paged_attention(qs[l], kc[l], vc[l], plan, case.scale, out=outs[l],
+                                               workspace=ws, stream=stream, k_new=knew[l], v_new=vnew[l])
+
+    step = eager_step
+    if graph:
+        # The whole step (upload + L x (scatter, attention)) as one HIP graph,
+        # replayed per step. Nothing in it allocates or clears memory: the
+        # workspace counters reset themselves.
+        with torch.cuda.stream(stream):
+            eager_step()
+            hg = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(hg, stream=stream):
+                eager_step()
+        step = hg.replay
+
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for _ in range(steps):
+            step()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+
+    kv_size = 2 if kv_dt == torch.bfloat16 else 4
+    attn_b, write_b = algorithmic_bytes(ctx, q_len, kv_size, 4)
+    step_bytes = L * (attn_b + write_b)
+    value = step_bytes / (ms * 1e-3) / 1e9
+
+    # Dominant kernel alone: the attention call per layer, back to back, timed
+    # with events on the stream it is launched on.
+    reps = max(4, steps // 2)
+    attn_loop = lambda: [attn(l) for l in range(L)]
+    if graph:
+        with torch.cuda.stream(stream):
+            agraph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(agraph, stream=stream):
+                attn_loop()
+        attn_loop = agraph.replay
+    a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        attn_loop()
+        a0.record(stream)
+        for _ in range(reps):
+            attn_loop()
+        a1.record(stream)
+    torch.cuda.synchronize()
+    attn_us = a0.elapsed_time(a1) * 1e3 / (reps * L)
+    achieved = attn_b / (attn_us * 1e-6) / 1e9
+    P = plan.plan
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic(workload, kv) if partition == 0 and chunk_partition == 0 else None,
+                "kernel": "le_ragged_paged_attention ("
+                          + ("ragged_kernel: chunk and decode workgroups in one launch"
+                             if P.n_chunk_items and P.n_decode_items else
+                             "chunk_kernel" if P.n_chunk_items else "decode mfma_kernel") + ")",
+                "bytes_per_launch": attn_b, "us_per_launch": round(attn_us, 3)}
+    if workload == "config3":
+        fl = chunk_flops(ctx, q_len)
+        tflops = fl / (attn_us * 1e-6) / 1e12
+        roofline["chunk_flops_per_launch"] = fl
+        roofline["chunk_tflops"] = round(tflops, 1)
+        roofline["mfma_bf16_util"] = round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)
+    res = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": kv, "data": "synthetic",
+        "config": {"workload": f"{workload}: {len(ctx)} seqs, {n} rows, ctx "
+                               f"{'log-uniform [64,4096]' if workload == 'config2' else 'see bench.py'}"
+                               f", Qwen2.5-0.5B GQA 14/2 x 64, block 16, pool {pool} blocks,"
+                               f" {L} layers per step (own KV pool each)",
+                   "kv_dtype": kv, "act_dtype": "f32", "layers": L,
+                   "parallelism": "none (1 GPU)"},
+        "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "decode_rows_per_s": round(n / (ms * 1e-3), 1),
+        "plan": {"rows": P.n_tokens, "decode_items": P.n_decode_items, "chunk_items": P.n_chunk_items,
+                 "parts": P.n_parts, "bytes": int(P.bytes), "pack_us": round(pack_us, 1)},
+        "roofline": roofline,
+    }
+    del kc, vc, qs, knew, vnew, outs, ws, plan, step
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return res
+
+
 def e2e_run(arch, prompts, out_lens, pool_blocks, max_seqs=64, budget=512, arrivals_s=None,
             prefix_caching=False, seed=4, layers=None):
     """One end-to-end run of the engine: scheduler, packing, device model,
@@ -156,7 +328,8 @@ def e2e_run(arch, prompts, out_lens, pool_blocks, max_seqs=64, budget=512, arriv
             "decode_tok_per_s": round(st.decode_step_tokens / st.decode_seconds, 1) if st.decode_seconds else None,
             "decode_ms_per_step": round(1e3 * st.decode_seconds / st.decode_steps, 3) if st.decode_steps else None,
             "ttft_mean_s": round(st.ttft_mean_s, 4), "latency_mean_s": round(st.latency_mean_s, 3),
-            "preemptions": int(st.preemptions), "setup_s": round(setup_s, 1)}
+            "preemptions": int(st.preemptions), "setup_s": round(setup_s, 1),
+            "plan_us_per_step": round(1e6 * st.plan_seconds / st.steps, 1) if st.steps else None}
 
 
 def e2e_leg(which, layers=None):
@@ -206,6 +379,8 @@ def main():
                     help="end-to-end leg after the attention measurement (see e2e_leg)")
     ap.add_argument("--e2e-layers", type=int, default=None, help="model layers (default: all)")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--no-extra-workloads", action="store_true",
+                    help="skip the target and config3 sub-measurements of a config2 run")
     ap.add_argument("--partition", type=int, default=0, help="decode partition tokens (0 = planner's choice)")
     ap.add_argument("--chunk-partition", type=int, default=0,
                     help="chunk-row key partition tokens (0 = planner's choice)")
@@ -228,142 +403,20 @@ def main():
               "sequence with no exchange; multi-GPU runs are not part of it).", file=sys.stderr)
         sys.exit(2)
 
-    import torch
-    from llm_engine_amd import kernels
-    from gpu_util import slices_of
-    from cases import make_case
-
-    dev = torch.device("cuda:0")
-    kv_dt = torch.bfloat16 if args.kv == "bf16" else torch.float32
-    act_dt = torch.float32
-    ctx, q_len, pool = workload_shape(args.workload)
-    case = make_case(ctx, q_len=q_len, num_blocks=pool, seed=2, fill="none")  # tables and rows only
-    kv_dim = KV_HEADS * HEAD_DIM
-    n = int(q_len.sum())
-    g = torch.Generator(device=dev)
-    g.manual_seed(1234)
-    L = args.layers
-    kc = [torch.randn(pool * BS, kv_dim, device=dev, generator=g).to(kv_dt) for _ in range(L)]
-    vc = [torch.randn(pool * BS, kv_dim, device=dev, generator=g).to(kv_dt) for _ in range(L)]
-    qs = [torch.randn(n, Q_HEADS * HEAD_DIM, device=dev, generator=g).to(act_dt) for _ in range(L)]
-    knew = [torch.randn(n, kv_dim, device=dev, generator=g).to(act_dt) for _ in range(L)]
-    vnew = [torch.randn(n, kv_dim, device=dev, generator=g).to(act_dt) for _ in range(L)]
-    outs = [torch.empty_like(qs[0]) for _ in range(L)]
-
-    t0 = time.perf_counter()
-    plan = kernels.Plan(slices_of(case), Q_HEADS, KV_HEADS, HEAD_DIM, BS, kv_dt,
-                        partition_tokens=args.partition, chunk_partition_tokens=args.chunk_partition)
-    pack_us = (time.perf_counter() - t0) * 1e6
-    plan.upload()
-    torch.cuda.synchronize()
-    slots = plan.dev_array("slots")
-    ws = kernels.new_workspace(plan.workspace_size(), dev)
-    stream = torch.cuda.current_stream()
-    if args.graph:
-        stream = torch.cuda.Stream()  # capture needs a stream other than the legacy default
-        stream.wait_stream(torch.cuda.current_stream())
-
-    def attn(l, st=None):
-        kernels.ragged_paged_attention(qs[l], kc[l], vc[l], plan, case.scale, out=outs[l],
-                                       workspace=ws, stream=st or stream)
-
-    def eager_step():
-        plan.upload(stream)
-        for l in range(L):
-            if args.separate_scatter:
-                kernels.store_kv(knew[l], vnew[l], slots, kc[l], vc[l], stream=stream)
-                attn(l)
-            else:  # le_ragged_paged_attention_store: the scatter folded into the attention launch
-                kernels.ragged_paged_attention(qs[l], kc[l], vc[l], plan, case.scale, out=outs[l],
-                                               workspace=ws, stream=stream, k_new=knew[l], v_new=vnew[l])
-
-    step = eager_step
-    if args.graph:
-        # The whole step (upload + 24 x (scatter, attention)) as one HIP graph,
-        # replayed per step. Nothing in it allocates or clears memory: the
-        # workspace counters reset themselves.
-        with torch.cuda.stream(stream):
-            eager_step()
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph, stream=stream):
-                eager_step()
-        step = graph.replay
-
-    with torch.cuda.stream(stream):
-        for _ in range(args.warmup):
-            step()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        e0.record(stream)
-        for _ in range(args.steps):
-            step()
-        e1.record(stream)
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / args.steps
-
-    kv_size = 2 if kv_dt == torch.bfloat16 else 4
-    attn_b, write_b = algorithmic_bytes(ctx, q_len, kv_size, 4)
-    step_bytes = L * (attn_b + write_b)
-    value = step_bytes / (ms * 1e-3) / 1e9
-
-    # Dominant kernel alone: the attention call per layer, back to back, timed
-    # with events on the stream it is launched on.
-    reps = max(4, args.steps // 2)
-    attn_loop = lambda: [attn(l) for l in range(L)]
-    if args.graph:
-        with torch.cuda.stream(stream):
-            agraph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(agraph, stream=stream):
-                attn_loop()
-        attn_loop = agraph.replay
-    a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(stream):
-        attn_loop()
-        a0.record(stream)
-        for _ in range(reps):
-            attn_loop()
-        a1.record(stream)
-    torch.cuda.synchronize()
-    attn_us = a0.elapsed_time(a1) * 1e3 / (reps * L)
-    achieved = attn_b / (attn_us * 1e-6) / 1e9
-    P = plan.plan
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "traffic": measured_traffic(args.workload, args.kv) if args.partition == 0 and args.chunk_partition == 0 else None,
-                "kernel": "le_ragged_paged_attention ("
-                          + ("ragged_kernel: chunk and decode workgroups in one launch"
-                             if P.n_chunk_items and P.n_decode_items else
-                             "chunk_kernel" if P.n_chunk_items else "decode mfma_kernel") + ")",
-                "bytes_per_launch": attn_b, "us_per_launch": round(attn_us, 3)}
-    if args.workload == "config3":
-        fl = chunk_flops(ctx, q_len)
-        roofline["chunk_flops_per_launch"] = fl
-
-    res = {
-        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": args.kv, "data": "synthetic",
-        "config": {"workload": f"{args.workload}: {len(ctx)} seqs, {n} rows, ctx "
-                               f"{'log-uniform [64,4096]' if args.workload == 'config2' else 'see bench.py'}"
-                               f", Qwen2.5-0.5B GQA 14/2 x 64, block 16, pool {pool} blocks,"
-                               f" {L} layers per step (own KV pool each)",
-                   "kv_dtype": args.kv, "act_dtype": "f32", "layers": L,
-                   "parallelism": "none (1 GPU)"},
-        "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
-        "decode_rows_per_s": round(n / (ms * 1e-3), 1),
-        "plan": {"rows": P.n_tokens, "decode_items": P.n_decode_items, "chunk_items": P.n_chunk_items,
-                 "combine_items": P.n_combine_items, "bytes": int(P.bytes), "pack_us": round(pack_us, 1)},
-        "roofline": roofline,
-    }
+    res = attention_leg(args.workload, args.kv, args.layers, args.steps, args.warmup, args.partition,
+                        args.chunk_partition, args.graph, args.separate_scatter)
+    # The north star's target point and the mixed step, measured the same way
+    # (fewer steps), each with its own roofline.
+    if args.workload == "config2" and not args.no_extra_workloads:
+        for extra in ("target", "config3"):
+            sub = attention_leg(extra, "bf16", args.layers, max(10, args.steps // 2), args.warmup)
+            res[extra] = {k: sub[k] for k in ("value", "unit", "ms_per_step", "pct_of_peak", "config", "plan",
+                                               "roofline")}
+    ctx, q_len, _ = workload_shape(args.workload)
     if not args.no_cpu_baseline:
-        res["cpu_baseline"] = cpu_baseline(ctx, q_len, kv_dt == torch.bfloat16, args.cpu_budget)
+        res["cpu_baseline"] = cpu_baseline(ctx, q_len, args.kv == "bf16", args.cpu_budget)
     else:
         res["cpu_baseline"] = None
-    del kc, vc, qs, knew, vnew, outs, ws, plan
-    torch.cuda.empty_cache()
     for leg in (["decode64", "config4", "config5"] if args.e2e == "all" else [args.e2e]):
         if leg != "none":
             res["e2e_" + leg] = e2e_leg(leg, layers=args.e2e_layers)

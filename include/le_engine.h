@@ -73,7 +73,9 @@ typedef struct le_model_desc {
   int32_t tie_word_embeddings;
   int32_t dtype;       /* le_dtype of weights and activations on the device */
   int32_t kv_dtype;    /* le_dtype of the paged K/V cache */
-  int32_t reserved_;
+  int32_t attention;   /* LE_ATTN_RAGGED (0): le_ragged_paged_attention_qkv over the packed
+                          step; LE_ATTN_REFERENCE (1): le_rope_kv_cache_write, then the
+                          reference-shaped le_attention_decode on the packed arrays */
   /* host fp32 weights, row-major, nn.Linear layout [out][in] */
   const float* embed;       /* [vocab][hidden] */
   const float* final_norm;  /* [hidden] */
@@ -91,6 +93,9 @@ typedef struct le_model_desc {
   const float* const* wup;
   const float* const* wdown;     /* [hidden][inter] */
 } le_model_desc;
+
+#define LE_ATTN_RAGGED 0
+#define LE_ATTN_REFERENCE 1
 
 typedef struct le_model le_model;
 
@@ -123,6 +128,7 @@ typedef struct le_run_stats {
   int64_t decode_step_tokens;      /* tokens sampled in those steps */
   double ttft_mean_s;              /* arrival (or start) to first token, mean over sequences */
   double latency_mean_s;           /* arrival (or start) to last token, mean over sequences */
+  double plan_seconds;             /* host time in le_plan_step + le_plan_upload, all steps */
 } le_run_stats;
 
 /* Greedy generation of n_seqs prompts through the scheduler and the model.

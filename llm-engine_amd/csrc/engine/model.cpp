@@ -115,6 +115,7 @@ class Model {
   ~Model();
   void forward(const le_step_slice* slices, int n_slices, int32_t* tokens_out, float* logits_out);
   int num_blocks() const { return num_blocks_; }
+  double plan_seconds() const { return plan_seconds_; }
   int block_size() const { return bs_; }
 
  private:
@@ -124,7 +125,9 @@ class Model {
   void gemm(const void* A, const void* B, void* C, int m, int n, int k, bool c_f32 = false);
 
   le_model_desc d_;
-  bool bf16_, kv_bf16_;
+  bool bf16_;
+  int kv_dt_;  // le_dtype of the caches
+  double plan_seconds_ = 0.0;
   int H_, QD_, KVD_, I_, V_, hd_, nh_, nkv_, bs_, num_blocks_;
   size_t act_;
   hipStream_t stream_ = nullptr;
@@ -142,7 +145,11 @@ class Model {
 
 Model::Model(const le_model_desc& d, int num_blocks, int block_size) : d_(d) {
   bf16_ = d.dtype == LE_BF16;
-  kv_bf16_ = d.kv_dtype == LE_BF16;
+  kv_dt_ = d.kv_dtype;
+  if (d.dtype != LE_F32 && d.dtype != LE_BF16)
+    throw StatusError(LE_EUNSUPPORTED, "model dtype: fp32 or bf16 weights and activations");
+  if (kv_dt_ != LE_F32 && kv_dt_ != LE_BF16 && kv_dt_ != LE_F16) throw std::invalid_argument("kv_dtype");
+  if (d.attention != LE_ATTN_RAGGED && d.attention != LE_ATTN_REFERENCE) throw std::invalid_argument("attention");
   H_ = d.hidden;
   hd_ = d.head_dim;
   nh_ = d.q_heads;
@@ -191,7 +198,7 @@ Model::Model(const le_model_desc& d, int num_blocks, int block_size) : d_(d) {
   }
   cos_ = upload_f32(c.data(), c.size());
   sin_ = upload_f32(s.data(), s.size());
-  const size_t cache_bytes = static_cast<size_t>(num_blocks) * bs_ * KVD_ * (kv_bf16_ ? 2 : 4);
+  const size_t cache_bytes = static_cast<size_t>(num_blocks) * bs_ * KVD_ * (kv_dt_ == LE_F32 ? 4 : 2);
   for (int l = 0; l < d.layers; l++) {
     void *k = nullptr, *v = nullptr;
     hip_ok(hipMalloc(&k, cache_bytes), "hipMalloc kv");
@@ -258,13 +265,15 @@ void Model::gemm(const void* A, const void* B, void* C, int m, int n, int k, boo
 }
 
 void Model::forward(const le_step_slice* slices, int n_slices, int32_t* tokens_out, float* logits_out) {
-  le_plan_config cfg{nh_, nkv_, hd_, bs_, kv_bf16_ ? LE_BF16 : LE_F32, 0, 0, 0, 0, 0};
+  const auto t_plan = std::chrono::steady_clock::now();
+  le_plan_config cfg{nh_, nkv_, hd_, bs_, kv_dt_, 0, 0, 0, 0, 0};
   le_step_plan plan{};
   int st = le_plan_step(slices, n_slices, &cfg, nullptr, 0, &plan);
   if (st != LE_ENOSPACE) le_ok(st, "le_plan_step");
   void* host = plan_host_.get(static_cast<size_t>(plan.bytes));
   le_ok(le_plan_step(slices, n_slices, &cfg, host, plan.bytes, &plan), "le_plan_step");
   le_ok(le_plan_upload(&plan, host, plan_dev_.get(static_cast<size_t>(plan.bytes)), stream_), "le_plan_upload");
+  plan_seconds_ += std::chrono::duration<double>(std::chrono::steady_clock::now() - t_plan).count();
   const int N = plan.n_tokens, R = plan.n_logits;
   if (N == 0) return;
   const int32_t* d_ids = le_plan_dev_array(&plan, plan.off_token_ids);
@@ -279,10 +288,12 @@ void Model::forward(const le_step_slice* slices, int n_slices, int32_t* tokens_o
   void* o = o_.get(n * H_ * act_);
   void* gate_up = gate_up_.get(n * 2 * I_ * act_);
   void* act = act_buf_.get(n * I_ * act_);
-  const size_t ws_bytes = le_ragged_workspace_size(&plan);
+  const bool ref_attn = d_.attention == LE_ATTN_REFERENCE;
+  const size_t ws_bytes =
+      ref_attn ? le_attention_decode_workspace_size(N, nh_, nkv_, hd_) : le_ragged_workspace_size(&plan);
   void* ws = ws_bytes ? ws_.get(ws_bytes, /*zero=*/true, stream_) : nullptr;
   const float scale = 1.0f / std::sqrt(static_cast<float>(hd_));
-  const le_dtype act_dt = bf16_ ? LE_BF16 : LE_F32, kv_dt = kv_bf16_ ? LE_BF16 : LE_F32;
+  const le_dtype act_dt = bf16_ ? LE_BF16 : LE_F32, kv_dt = static_cast<le_dtype>(kv_dt_);
   const int L_n = static_cast<int>(layers_.size());
 
   // Per layer: norm (fused with the previous residual add), one QKV GEMM,
@@ -298,9 +309,24 @@ void Model::forward(const le_step_slice* slices, int n_slices, int32_t* tokens_o
     // on a decode step; otherwise every token's K/V is rotated and written
     // before attention runs, so tokens of one step (a prefill chunk) attend
     // to each other.
-    le_ok(le_ragged_paged_attention_qkv(qkv, act_dt, QKV, L.bqkv, cos_, sin_, d_.max_pos, kc_[l], vc_[l],
-                                        kv_dt, num_blocks_, &plan, scale, attn, q, ws, ws_bytes, stream_),
-          "le_ragged_paged_attention_qkv");
+    if (!ref_attn) {
+      le_ok(le_ragged_paged_attention_qkv(qkv, act_dt, QKV, L.bqkv, cos_, sin_, d_.max_pos, kc_[l], vc_[l],
+                                          kv_dt, num_blocks_, &plan, scale, attn, q, ws, ws_bytes, stream_),
+            "le_ragged_paged_attention_qkv");
+    } else {
+      // the reference's sequence: bias, RoPE and the K/V store, then its
+      // attention launcher over the packed arrays (cuda_model.cu:358-377)
+      const int32_t* pos = le_plan_dev_array(&plan, plan.off_positions);
+      le_ok(le_rope_kv_cache_write(qkv, act_dt, QKV, L.bqkv, pos, le_plan_dev_array(&plan, plan.off_slots), cos_,
+                                   sin_, d_.max_pos, N, nh_, nkv_, hd_, q, kc_[l], vc_[l], kv_dt,
+                                   static_cast<int64_t>(num_blocks_) * bs_, stream_),
+            "le_rope_kv_cache_write");
+      le_ok(le_attention_decode(q, act_dt, kc_[l], vc_[l], kv_dt, le_plan_dev_array(&plan, plan.off_tables),
+                                le_plan_dev_array(&plan, plan.off_table_offset),
+                                le_plan_dev_array(&plan, plan.off_token_seq), pos, attn, N, nh_, nkv_, hd_, bs_, scale,
+                                num_blocks_, ws, ws_bytes, stream_),
+            "le_attention_decode");
+    }
     gemm(attn, L.wo, o, N, H_, QD_);
     hip_ok(residual_rmsnorm(x, o, nullptr, L.post_norm, h, N, H_, d_.eps, true, bf16_, stream_), "residual");
     gemm(h, L.wgate_up, gate_up, N, 2 * I_, H_);
@@ -439,6 +465,7 @@ int le_run_greedy(le_model* m, const le_sched_config* cfg, int prefix_caching, i
     size_t next = 0;
 
     le_run_stats rs{};
+    const double plan_s0 = model.plan_seconds();
     std::vector<double> first_tok(static_cast<size_t>(n_seqs), -1.0), last_tok(static_cast<size_t>(n_seqs), -1.0);
     const auto t0 = std::chrono::steady_clock::now();
     auto elapsed = [&]() { return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count(); };
@@ -497,6 +524,7 @@ int le_run_greedy(le_model* m, const le_sched_config* cfg, int prefix_caching, i
       rs.latency_mean_s /= n_done;
     }
     rs.preemptions = static_cast<int64_t>(sch.stats().preemptions);
+    rs.plan_seconds = model.plan_seconds() - plan_s0;
     for (size_t i = 1; i < held.size(); i += 2) kv.free(held[i]);
     size_t out_off = 0;  // gen_out: max_tokens[i] entries per sequence, back to back
     for (int i = 0; i < n_seqs; i++) {

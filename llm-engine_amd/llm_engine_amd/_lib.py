@@ -110,7 +110,7 @@ class ModelDesc(ctypes.Structure):
                                               "head_dim", "vocab", "max_pos")] + [
         ("eps", ctypes.c_float), ("theta", ctypes.c_float),
         ("tie_word_embeddings", ctypes.c_int32), ("dtype", ctypes.c_int32),
-        ("kv_dtype", ctypes.c_int32), ("reserved_", ctypes.c_int32),
+        ("kv_dtype", ctypes.c_int32), ("attention", ctypes.c_int32),
         ("embed", ctypes.c_void_p), ("final_norm", ctypes.c_void_p), ("lm_head", ctypes.c_void_p),
     ] + [(n, _fpp) for n in ("in_norm", "post_norm", "wq", "wk", "wv", "wo", "bq", "bk", "bv",
                               "wgate", "wup", "wdown")]
@@ -121,7 +121,8 @@ class RunStats(ctypes.Structure):
                 ("decode_tokens", ctypes.c_int64), ("preemptions", ctypes.c_int64),
                 ("seconds", ctypes.c_double), ("decode_seconds", ctypes.c_double),
                 ("decode_steps", ctypes.c_int64), ("decode_step_tokens", ctypes.c_int64),
-                ("ttft_mean_s", ctypes.c_double), ("latency_mean_s", ctypes.c_double)]
+                ("ttft_mean_s", ctypes.c_double), ("latency_mean_s", ctypes.c_double),
+                ("plan_seconds", ctypes.c_double)]
 
 
 # name -> (restype, argtypes). Exactly the symbols include/*.h declare.

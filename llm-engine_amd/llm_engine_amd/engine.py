@@ -13,7 +13,7 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from . import _lib
-from ._lib import LE_BF16, LE_F32, ModelDesc, RunStats, SchedConfig, StepSlice, check
+from ._lib import LE_BF16, LE_F16, LE_F32, ModelDesc, RunStats, SchedConfig, StepSlice, check
 
 ARCHS = {
     # Qwen2.5-0.5B: qkv bias, tied embeddings
@@ -75,13 +75,18 @@ class Model:
     """The device model (le_model_create): weights uploaded once, one K/V cache
     pair per layer of num_blocks * block_size slots."""
 
+    DTYPES = {"f32": LE_F32, "bf16": LE_BF16, "f16": LE_F16}
+
     def __init__(self, w: Weights, num_blocks: int, block_size: int = 16, dtype: str = "f32",
-                 kv_dtype: str | None = None):
+                 kv_dtype: str | None = None, attention: str = "ragged"):
+        """attention: "ragged" (le_ragged_paged_attention_qkv over the packed
+        step) or "reference" (the reference-shaped le_attention_decode)."""
         a = w.arch
         self.arch = a
         self.num_blocks, self.block_size = num_blocks, block_size
-        dt = LE_BF16 if dtype == "bf16" else LE_F32
-        kvdt = dt if kv_dtype is None else (LE_BF16 if kv_dtype == "bf16" else LE_F32)
+        dt = self.DTYPES[dtype]
+        kvdt = dt if kv_dtype is None else self.DTYPES[kv_dtype]
+        attn = {"ragged": 0, "reference": 1}[attention]
         n = a["layers"]
 
         def arr(key):
@@ -92,7 +97,7 @@ class Model:
         self._keep = {k: arr(k) for k in ("in_norm", "post_norm", "wq", "wk", "wv", "wo", "bq", "bk",
                                           "bv", "wgate", "wup", "wdown")}
         d = ModelDesc(a["hidden"], a["inter"], n, a["q_heads"], a["kv_heads"], a["head_dim"],
-                      a["vocab"], a["max_pos"], a["eps"], a["theta"], int(a["tie"]), dt, kvdt, 0,
+                      a["vocab"], a["max_pos"], a["eps"], a["theta"], int(a["tie"]), dt, kvdt, attn,
                       w.embed.ctypes.data, w.final_norm.ctypes.data,
                       None if w.lm_head is None else w.lm_head.ctypes.data)
         for k, v in self._keep.items():

@@ -37,9 +37,14 @@ def run_both(w, prompts, max_tokens, num_blocks, cfg=None, prefix=False, frag=0,
     return gpu, cpu, stats
 
 
-def test_config1_matches_oracle_token_for_token(gpu):
+@pytest.mark.parametrize("attention", ["ragged", "reference"])
+def test_config1_matches_oracle_token_for_token(gpu, attention):
     """Qwen2.5-0.5B (24 layers) random-init fp32, 8 prompts of
-    16..512 tokens, 32 greedy tokens, fragmented 4096-block pool."""
+    16..512 tokens, 32 greedy tokens, fragmented 4096-block pool. Through both
+    attention entries: the ragged plan (le_ragged_paged_attention_qkv) and the
+    reference-shaped launcher (le_attention_decode), which therefore give the
+    same greedy tokens (the reference requires this of its two attention
+    kernels, test_cuda_invariance.cpp:295-344)."""
     from llm_engine_amd.engine import Model, sched_config, synthetic_weights
     import sys
     sys.path.insert(0, str(GOLD))
@@ -47,13 +52,13 @@ def test_config1_matches_oracle_token_for_token(gpu):
     fx = json.loads((GOLD / "config1_tokens.json").read_text())
     w = synthetic_weights(fx["arch"], fx["weight_seed"])
     assert weight_digest(w) == fx["weight_digest"], "weight generator changed; regenerate the fixture"
-    m = Model(w, fx["num_blocks"], 16, dtype="f32")
+    m = Model(w, fx["num_blocks"], 16, dtype="f32", attention=attention)
     toks, stats = m.run_greedy(fx["prompts"], [fx["gen"]] * len(fx["prompts"]),
                                sched_config(max_num_batched_tokens=fx["max_num_batched_tokens"]),
                                fragment_blocks=fx["fragment_blocks"])
     m.close()
-    print(f"config1: {stats.steps} steps, {stats.decode_tokens} tokens in {stats.seconds:.2f}s; "
-          f"oracle min top-2 margins {fx['min_margin']}")
+    print(f"config1 ({attention}): {stats.steps} steps, {stats.decode_tokens} tokens in {stats.seconds:.2f}s, "
+          f"plan {stats.plan_seconds / stats.steps * 1e6:.0f} us/step; oracle min top-2 margins {fx['min_margin']}")
     assert toks == fx["tokens"]
 
 
@@ -80,6 +85,49 @@ def test_small_model_matches_oracle(gpu, case):
         off, _, _ = run_both(w, prompts, [8] * 4, 256, prefix=False)
         assert off == gpu_t
     assert gpu_t == cpu_t
+
+
+@pytest.mark.parametrize("kv", ["f32", "bf16", "f16"])
+def test_attention_entries_give_equal_tokens(gpu, kv):
+    """The reference's invariance test (test_cuda_invariance.cpp:295-344: the
+    GQA kernel and the baseline kernel give identical greedy tokens) for this
+    library's two attention entries: the same model and prompts, chunked
+    prefill and a fragmented pool, through the ragged plan and through the
+    reference-shaped launcher. fp32 K/V: identical tokens. 16-bit K/V: the
+    entries split the work differently (prefill chunks on the chunk tile or
+    row by row), so their logits differ by rounding; tokens are identical up
+    to each sequence's first position whose oracle top-2 margin is below
+    2e-3 (twice the largest logit difference the 16-bit paths show)."""
+    from e2e_util import OracleModel, lockstep
+    from llm_engine_amd.engine import Model, sched_config, synthetic_weights
+    w = synthetic_weights("tinyllama-1.1b", 13, layers=2)
+    prompts = prompts_of(9, (33, 180, 64, 300, 17), w.arch["vocab"])
+    cfg = sched_config(prefill_chunk_size=64)
+    out = {}
+    for attention in ("ragged", "reference"):
+        m = Model(w, 512, 16, dtype="f32", kv_dtype=kv, attention=attention)
+        out[attention], _ = m.run_greedy(prompts, [12] * 5, cfg, fragment_blocks=40)
+        m.close()
+    if kv == "f32":
+        assert out["ragged"] == out["reference"]
+        return
+    m = Model(w, 512, 16, dtype="f32", kv_dtype=kv)
+    kvb = {"bf16": True, "f16": False}[kv]
+    _, rows, _ = lockstep(m, OracleModel(w, 512, kv_bf16=kvb) if kv == "bf16" else OracleModel(w, 512),
+                          prompts, [12] * 5, 512, cfg, fragment_blocks=40)
+    m.close()
+    margins = {}
+    for _, _, margin, _, _, sid in rows:
+        margins.setdefault(sid, []).append(margin)
+    compared = 0
+    for i, (a, b) in enumerate(zip(out["ragged"], out["reference"])):
+        for j, (x, y) in enumerate(zip(a, b)):
+            if margins[i][j] < 2e-3:
+                break
+            assert x == y, (i, j)
+            compared += 1
+    print(f"{kv} K/V: {compared}/{12 * 5} tokens compared equal")
+    assert compared >= 0.5 * 12 * 5
 
 
 def test_second_architecture_group8(gpu):
