@@ -250,7 +250,6 @@ int ragged_attention(const void* q, le_dtype act_dtype, const void* k_new, const
   if (plan->n_chunk_items == 0)
     return hip_status(le::attention_decode(d, act_dtype, kv_dtype, stream));
 
-  if (kv_dtype == LE_F32) return LE_EINVAL;  // chunk items exist only for 16-bit caches
   le::ChunkParams c{};
   c.q = q; c.k_cache = k_cache; c.v_cache = v_cache;
   c.tables = d.tables; c.table_offset = d.table_offset; c.token_pos = d.token_pos;

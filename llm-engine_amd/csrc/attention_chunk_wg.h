@@ -40,10 +40,12 @@
 //     (fp32) and its fp32 (max, sum) with device-coherent
 //     stores; the last partition to arrive (atomic counter per tile and kv
 //     head, reset by it) merges them in partition order, inside the launch.
-// 16-bit operands (q and P rounded to the cache type), fp32 accumulation;
-// fp32 caches never come here (their chunk
-// rows run on the decode kernel for exact fp32 arithmetic).
+// 16-bit caches: 16-bit operands (q and P rounded to the cache type), fp32
+// accumulation. fp32 caches: the same tile on v_mfma_f32_16x16x4_f32 (exact
+// fp32 products), K/V staged 192 keys at a time.
 #include <float.h>
+
+#include <type_traits>
 
 #include "le_common.h"
 #include "le_internal.h"
@@ -56,10 +58,13 @@ namespace {
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * kWave;
 constexpr int kTileKeys = 64;    // keys per MFMA tile
-// Keys staged in LDS at once: 384 for head_dim 64 (110 KB of K and V rows,
-// so a default 384-key partition is one memory round trip), 256 for
-// head_dim 128 (139 KB).
-template <int HD> constexpr int kStageKeys = HD == 64 ? 384 : 256;
+// Keys staged in LDS at once: with a 16-bit cache 384 for head_dim 64 (110 KB
+// of K and V rows, so a default 384-key partition is one memory round trip)
+// and 256 for head_dim 128 (139 KB); with an fp32 cache 192 (104 KB) and 64
+// (68 KB; the registers of 128 keys' staging loads do not fit beside the
+// head_dim 128 accumulators). Always whole 64-key MFMA tiles.
+template <typename KV, int HD>
+constexpr int kStageKeys = sizeof(KV) == 2 ? (HD == 64 ? 384 : 256) : (HD == 64 ? 192 : 64);
 constexpr int kRowsMax = 32;     // query rows per item
 constexpr int kMaxG = 8;         // query heads per kv head
 constexpr int kMaxSplit = 16;    // partitions of one tile the merge stages in LDS
@@ -71,9 +76,9 @@ __device__ __forceinline__ float vmax3(float a, float b, float c) {
   return r;
 }
 
-template <int HD> struct ChunkLds {
-  static constexpr int ROW = HD * 2 + 16;  // bytes per key row of K and of V (padded)
-  static constexpr int K_BYTES = kStageKeys<HD> * ROW;
+template <typename KV, int HD> struct ChunkLds {
+  static constexpr int ROW = HD * static_cast<int>(sizeof(KV)) + 16;  // bytes per key row of K and of V (padded)
+  static constexpr int K_BYTES = kStageKeys<KV, HD> * ROW;
   static constexpr int BYTES = 2 * K_BYTES;  // K rows, then V rows
 };
 
@@ -94,8 +99,8 @@ __device__ __forceinline__ void store4(ACT* p, f32x4 v) {
 }
 
 // LDS of one chunk workgroup.
-template <int HD> struct ChunkSmem {
-  __attribute__((aligned(16))) char lds[ChunkLds<HD>::BYTES];
+template <typename KV, int HD> struct ChunkSmem {
+  __attribute__((aligned(16))) char lds[ChunkLds<KV, HD>::BYTES];
   int last;
 };
 
@@ -178,17 +183,22 @@ __device__ __forceinline__ void merge_tile(const ChunkParams& p, const ChunkItem
 // One chunk workgroup (kThreads threads): chunk item `item`, kv head `kvh`.
 // Shared by the chunk kernel and the fused ragged kernel.
 template <typename ACT, typename KV, int HD>
-__device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm, int item, int kvh) {
-  using M = mma16<KV>;  // K/V element type = the MFMA operand type
+__device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>& sm, int item, int kvh) {
+  // 16-bit caches: the 16x16x32 MFMA of the cache type (q and P rounded to
+  // it). fp32 caches: v_mfma_f32_16x16x4_f32, exact fp32 products.
+  constexpr bool kF32 = std::is_same_v<KV, float>;
+  using M = mma16<std::conditional_t<kF32, bf16_t, KV>>;
   using V8 = typename M::v8;
   using S16 = typename M::scalar;
-  using L = ChunkLds<HD>;
-  constexpr int KS = HD / 32;  // MFMA k-steps over head dims
+  using L = ChunkLds<KV, HD>;
+  constexpr int KS = HD / 32;  // 16-bit MFMA k-steps over head dims
   constexpr int DT = HD / 16;  // 16-dim output tiles
-  constexpr int CPR = HD / 8;  // 16-byte pieces per K/V row
-  constexpr int PIECES = 2 * kStageKeys<HD> * CPR;
+  constexpr int LD = HD / 4;   // fp32: dims per lane group (contiguous), one per MFMA k-step
+  constexpr int CPR = HD * static_cast<int>(sizeof(KV)) / 16;  // 16-byte pieces per K/V row
+  constexpr int PIECES = 2 * kStageKeys<KV, HD> * CPR;
   constexpr int PER = PIECES / kThreads;  // 16-byte loads per thread per stage
   static_assert(PER * kThreads == PIECES && PER % 2 == 0, "staging split");
+  static_assert(kStageKeys<KV, HD> % kTileKeys == 0, "a stage is whole MFMA tiles");
   static_assert(kRowsMax * kMaxG * kMaxSplit * (sizeof(float2) + sizeof(float)) <= L::BYTES,
                 "merge weights fit in the stage's LDS");
 
@@ -239,7 +249,7 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
       const bool bid_ok = bid >= 0 && bid < p.num_cache_blocks;
       okp[k] = rel < n_keys_blk && bid_ok;
       const int64_t slot = (static_cast<int64_t>(bid_ok ? bid : 0) << bs_shift) + (relc & bs_mask);
-      const int64_t off = (slot * kv_stride + kvh * HD + c * 8) * 2;
+      const int64_t off = (slot * kv_stride + kvh * HD) * static_cast<int64_t>(sizeof(KV)) + c * 16;
       kv[0][k] = ld16_stream(kbase + off);
       kv[1][k] = ld16_stream(vbase + off);
     }
@@ -257,36 +267,50 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
   // Query rows first (they are needed last, and a wait for them must not
   // cover the K/V loads issued after them), then the stage's K/V.
   const int pos0 = p.token_pos[tok0];  // the tile's rows are consecutive positions
-  uint4 qraw[2][KS][sizeof(ACT) / 2];  // 8 elements per k-step: 16 bytes (16-bit types) or 32 (fp32)
+  // 16-bit path: this lane's 8 dims per k-step (dims ks*32 + grp*8 ..);
+  // fp32 path: this lane's LD contiguous dims (grp*LD ..). Loaded raw before
+  // the stage's K/V loads are issued, converted after.
+  constexpr int QPIECES = (kF32 ? LD : KS * 8) / 8;  // 8-element pieces per row and lane
+  float qf[2][QPIECES * 8];
+  uint4 qraw[2][QPIECES][sizeof(ACT) / 2];
 #pragma unroll
   for (int rs = 0; rs < 2; rs++) {
     const int r = rs * 16 + col;
     const bool ok = computes && r < nq;
-    const ACT* q = static_cast<const ACT*>(p.q) +
-                   (static_cast<int64_t>(tok0 + (ok ? r : 0)) * p.q_heads + head) * HD + grp * 8;
+    const ACT* q = static_cast<const ACT*>(p.q) + (static_cast<int64_t>(tok0 + (ok ? r : 0)) * p.q_heads + head) * HD;
 #pragma unroll
-    for (int ks = 0; ks < KS; ks++)
+    for (int u = 0; u < QPIECES; u++) {
+      const int d0 = kF32 ? grp * LD + u * 8 : u * 32 + grp * 8;
 #pragma unroll
-      for (int h = 0; h < static_cast<int>(sizeof(ACT) / 2); h++) qraw[rs][ks][h] = ld16(q + ks * 32 + h * (16 / sizeof(ACT)));
+      for (int h = 0; h < static_cast<int>(sizeof(ACT) / 2); h++) qraw[rs][u][h] = ld16(q + d0 + h * (16 / sizeof(ACT)));
+    }
   }
   issue(0);
-  // Q^T operands: this lane's 8 dims per k-step of rows col and 16 + col.
-  V8 qb[2][KS];
 #pragma unroll
   for (int rs = 0; rs < 2; rs++) {
     const bool ok = computes && rs * 16 + col < nq;
 #pragma unroll
-    for (int ks = 0; ks < KS; ks++) {
+    for (int u = 0; u < QPIECES; u++) {
       float f[8];
       if constexpr (sizeof(ACT) == 2) {
-        elem<ACT>::widen(qraw[rs][ks][0], f);
+        elem<ACT>::widen(qraw[rs][u][0], f);
       } else {
-        elem<float>::widen(qraw[rs][ks][0], f);
-        elem<float>::widen(qraw[rs][ks][1], f + 4);
+        elem<float>::widen(qraw[rs][u][0], f);
+        elem<float>::widen(qraw[rs][u][1], f + 4);
       }
 #pragma unroll
-      for (int e = 0; e < 8; e++) qb[rs][ks][e] = static_cast<S16>(ok ? f[e] : 0.f);
+      for (int e = 0; e < 8; e++) qf[rs][u * 8 + e] = ok ? f[e] : 0.f;
     }
+  }
+  // 16-bit path: Q^T operands, this lane's 8 dims per k-step of rows col and 16 + col
+  V8 qb[2][KS];
+  if constexpr (!kF32) {
+#pragma unroll
+    for (int rs = 0; rs < 2; rs++)
+#pragma unroll
+      for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) qb[rs][ks][e] = static_cast<S16>(qf[rs][ks * 8 + e]);
   }
 
   f32x4 acc[2][DT];
@@ -295,8 +319,11 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
 #pragma unroll
     for (int d = 0; d < DT; d++) acc[rs][d] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run[2] = {-FLT_MAX, -FLT_MAX};
-  // lsum[rs][0] of the lanes of group 0 = the row's sum of p (row col); the
-  // other entries stay zero
+  // 16-bit path: lsum[rs][0] of the lanes of group 0 = the row's sum of p
+  // (row col), summed on the MFMA; the other entries stay zero. fp32 path:
+  // lsum[rs][0] of every lane = its share of the row's sum (the keys of its
+  // lane group). Either way the row sum is lsum[rs][0] summed over the four
+  // lane groups.
   f32x4 lsum[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
   const S16 one = static_cast<S16>(col == 0 ? 1.f : 0.f);
   const V8 ones = {one, one, one, one, one, one, one, one};
@@ -308,7 +335,7 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
     if (computes) {
       const int key_end = min(key_begin + n_keys_blk, pos0 + nq);  // past the last row's position: dead
 #pragma unroll 1
-      for (int kt = 0; kt < kStageKeys<HD> / kTileKeys; kt++) {
+      for (int kt = 0; kt < kStageKeys<KV, HD> / kTileKeys; kt++) {
         const int t0 = s0 + kt * kTileKeys;
         if (t0 >= key_end) break;
         const char* kt_lds = lds + kt * kTileKeys * L::ROW;
@@ -319,14 +346,33 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
         for (int rs = 0; rs < 2; rs++)
 #pragma unroll
           for (int i = 0; i < 4; i++) s[rs][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (!kF32) {
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+          for (int i = 0; i < 4; i++)
 #pragma unroll
-          for (int ks = 0; ks < KS; ks++) {
-            const V8 a = *reinterpret_cast<const V8*>(kt_lds + (i * 16 + col) * L::ROW + (ks * 32 + grp * 8) * 2);
+            for (int ks = 0; ks < KS; ks++) {
+              const V8 a = *reinterpret_cast<const V8*>(kt_lds + (i * 16 + col) * L::ROW + (ks * 32 + grp * 8) * 2);
 #pragma unroll
-            for (int rs = 0; rs < 2; rs++) s[rs][i] = M::mma(a, qb[rs][ks], s[rs][i]);
+              for (int rs = 0; rs < 2; rs++) s[rs][i] = M::mma(a, qb[rs][ks], s[rs][i]);
+            }
+        } else {
+          // k-step j: dim grp*LD + j of key col (A) and of row col (B); the
+          // steps and lane groups together cover every dim once
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            float kf[LD];
+#pragma unroll
+            for (int u = 0; u < LD / 4; u++) {
+              const float4 v = *reinterpret_cast<const float4*>(kt_lds + (i * 16 + col) * L::ROW + (grp * LD + u * 4) * 4);
+              kf[u * 4] = v.x; kf[u * 4 + 1] = v.y; kf[u * 4 + 2] = v.z; kf[u * 4 + 3] = v.w;
+            }
+#pragma unroll
+            for (int j = 0; j < LD; j++)
+#pragma unroll
+              for (int rs = 0; rs < 2; rs++)
+                s[rs][i] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[j], qf[rs][j], s[rs][i], 0, 0, 0);
           }
+        }
         // ---- causal mask, online softmax per row (log2 domain) ----
         // A tile wholly below the diagonal and inside the range needs no
         // mask: every row's position is at least pos0. The max runs on raw
@@ -377,37 +423,65 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<HD>& sm
             for (int j = 0; j < 4; j++)
               s[rs][i][j] = __builtin_amdgcn_exp2f(fmaf(s[rs][i][j], p.scale_log2, -m_run[rs]));
         }
-        // ---- O^T += V^T . P^T over the tile's 64 keys (2 k-steps of 32) ----
+        if constexpr (!kF32) {
+          // ---- O^T += V^T . P^T over the tile's 64 keys (2 k-steps of 32) ----
 #pragma unroll
-        for (int kk = 0; kk < 2; kk++) {
-          V8 pb[2];
+          for (int kk = 0; kk < 2; kk++) {
+            V8 pb[2];
 #pragma unroll
-          for (int rs = 0; rs < 2; rs++)
+            for (int rs = 0; rs < 2; rs++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-              pb[rs][j] = static_cast<S16>(s[rs][2 * kk][j]);
-              pb[rs][4 + j] = static_cast<S16>(s[rs][2 * kk + 1][j]);
+              for (int j = 0; j < 4; j++) {
+                pb[rs][j] = static_cast<S16>(s[rs][2 * kk][j]);
+                pb[rs][4 + j] = static_cast<S16>(s[rs][2 * kk + 1][j]);
+              }
+            // lane (col, grp) addresses key row kk*32 + 4*grp + col/4 (then +16)
+            // at dims 16*d + 4*(col%4), and receives dim 16*d + col of four
+            // keys: the keys P^T holds for that group.
+            const char* r_lo = vt_lds + (kk * 32 + grp * 4 + (col >> 2)) * L::ROW + (col & 3) * 8;
+            const char* r_hi = r_lo + 16 * L::ROW;
+#pragma unroll
+            for (int d = 0; d < DT; d++) {
+              const typename M::v4 lo = lds_read_tr16<KV>(r_lo + d * 32);
+              const typename M::v4 hi = lds_read_tr16<KV>(r_hi + d * 32);
+              const V8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+              for (int rs = 0; rs < 2; rs++) acc[rs][d] = M::mma(a, pb[rs], acc[rs][d]);
             }
-          // lane (col, grp) addresses key row kk*32 + 4*grp + col/4 (then +16)
-          // at dims 16*d + 4*(col%4), and receives dim 16*d + col of four
-          // keys: the keys P^T holds for that group.
-          const char* r_lo = vt_lds + (kk * 32 + grp * 4 + (col >> 2)) * L::ROW + (col & 3) * 8;
-          const char* r_hi = r_lo + 16 * L::ROW;
+            // row sums on the MFMA: a V^T row of ones (lanes of column 0)
 #pragma unroll
-          for (int d = 0; d < DT; d++) {
-            const typename M::v4 lo = lds_read_tr16<KV>(r_lo + d * 32);
-            const typename M::v4 hi = lds_read_tr16<KV>(r_hi + d * 32);
-            const V8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-#pragma unroll
-            for (int rs = 0; rs < 2; rs++) acc[rs][d] = M::mma(a, pb[rs], acc[rs][d]);
+            for (int rs = 0; rs < 2; rs++) lsum[rs] = M::mma(ones, pb[rs], lsum[rs]);
           }
-          // row sums on the MFMA: a V^T row of ones (lanes of column 0)
+        } else {
+          // ---- O^T += V^T . P^T: k-step (i, r) covers keys 16i + 4*grp + r,
+          // exactly the scores this lane's S^T accumulators hold, so P^T is
+          // the accumulator as is; V^T reads single floats of the row-major
+          // V rows (the 16-byte row pad spreads the lane groups' rows over
+          // the banks) ----
 #pragma unroll
-          for (int rs = 0; rs < 2; rs++) lsum[rs] = M::mma(ones, pb[rs], lsum[rs]);
+          for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+              const float* vrow = reinterpret_cast<const float*>(vt_lds + (i * 16 + grp * 4 + r) * L::ROW);
+#pragma unroll
+              for (int d = 0; d < DT; d++) {
+                const float a = vrow[d * 16 + col];
+#pragma unroll
+                for (int rs = 0; rs < 2; rs++)
+                  acc[rs][d] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, s[rs][i][r], acc[rs][d], 0, 0, 0);
+              }
+            }
+#pragma unroll
+          for (int rs = 0; rs < 2; rs++) {
+            float ls = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) ls += (s[rs][i][0] + s[rs][i][1]) + (s[rs][i][2] + s[rs][i][3]);
+            lsum[rs][0] += ls;
+          }
         }
       }
     }
-    rel0 += kStageKeys<HD>;
+    rel0 += kStageKeys<KV, HD>;
     if (rel0 >= n_keys_blk) break;
     __syncthreads();  // the stage is no longer read
     issue(rel0);

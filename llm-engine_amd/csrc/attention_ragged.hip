@@ -25,7 +25,7 @@ constexpr int kRaggedThreads = chk::kThreads;
 constexpr int kDecodeWaves = kRaggedThreads / kWave;
 
 template <typename KV, int HD> union RaggedSmem {
-  chk::ChunkSmem<HD> c;
+  chk::ChunkSmem<KV, HD> c;
   dec::DecodeSmem<KV, HD, kDecodeWaves> d;
 };
 
@@ -58,7 +58,7 @@ hipError_t attention_ragged(const DecodeParams& d, const ChunkParams& c, int act
     return hipErrorInvalidValue;
   const dim3 grid(static_cast<unsigned>(n));
   return with_dtype(act_dtype, [&](auto a) {
-    return with_dtype16(kv_dtype, [&](auto k) {
+    return with_dtype(kv_dtype, [&](auto k) {
       using ACT = decltype(a);
       using KV = decltype(k);
       if (c.head_dim == 64) ragged_kernel<ACT, KV, 64><<<grid, kRaggedThreads, 0, s>>>(d, c);

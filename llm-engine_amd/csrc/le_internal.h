@@ -126,7 +126,7 @@ struct ChunkParams {
 
 hipError_t attention_chunk(const ChunkParams& p, int act_dtype, int kv_dtype, hipStream_t stream);
 
-// A mixed step's chunk rows and decode rows (16-bit cache, plan items) in one
+// A mixed step's chunk rows and decode rows (plan items) in one
 // launch: chunk workgroups first, then decode workgroups.
 hipError_t attention_ragged(const DecodeParams& d, const ChunkParams& c, int act_dtype, int kv_dtype,
                             hipStream_t stream);

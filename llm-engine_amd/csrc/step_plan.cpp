@@ -12,14 +12,13 @@
 //
 // Work lists. A row whose slice has length 1 is a decode row: its context
 // 0..pos is cut into partitions of ~partition_tokens (whole blocks, equal
-// shares) and each partition becomes one DecodeItem. With a bf16 cache, the
-// rows of a longer slice (a prefill chunk) are cut into tiles of chunk_q_tile
-// consecutive positions; each tile's keys 0..last position are cut into
-// partitions of ~chunk_partition_tokens, one ChunkItem each, run on MFMA.
-// (fp16 caches are planned like bf16 ones.)
-// With an fp32 cache, chunk rows are decode rows (exact fp32 products on the
-// fp32 MFMA). Split rows of either kind are merged inside their launch by
-// the last partition to finish.
+// shares) and each partition becomes one DecodeItem. The rows of a longer
+// slice (a prefill chunk) are cut into tiles of chunk_q_tile consecutive
+// positions; each tile's keys 0..last position are cut into partitions of
+// ~chunk_partition_tokens, one ChunkItem each, run on MFMA tiles (16-bit
+// operands with a bf16/fp16 cache, fp32 operands with an fp32 cache). Split
+// rows of either kind are merged inside their launch by the last partition
+// to finish.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -143,7 +142,7 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
     // 16.3 us, 1024 17.1 us, 512 18.0 us).
     int64_t ctx = 0;
     for (int i = 0; i < n_slices; i++)
-      if (slices[i].len == 1 || cfg.kv_dtype == LE_F32)
+      if (slices[i].len == 1)
         for (int r = 0; r < slices[i].len; r++) ctx += slices[i].start + r + 1;
     const int64_t per_kvh = std::max<int64_t>(1, kTargetItems / cfg.kv_heads);
     int64_t part = (ctx + per_kvh - 1) / per_kvh;
@@ -153,16 +152,18 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
     // of the launch; splitting the decode rows further only adds merges
     // (config 3: 22.7 us with the rule above, 22.4 us with 2048 tokens).
     bool chunk_rows = false;
-    for (int i = 0; i < n_slices; i++) chunk_rows |= slices[i].len > 1 && cfg.kv_dtype != LE_F32;
+    for (int i = 0; i < n_slices; i++) chunk_rows |= slices[i].len > 1;
     if (chunk_rows) part = std::max<int64_t>(part, kMixedStepPartition);
     cfg.partition_tokens = static_cast<int32_t>(std::min<int64_t>(part, kMaxAutoPartition));
   }
   if (cfg.chunk_q_tile <= 0) cfg.chunk_q_tile = kDefaultChunkTile;
-  if (cfg.chunk_partition_tokens <= 0) cfg.chunk_partition_tokens = kDefaultChunkPartition;
+  // one LDS stage per partition: 384 keys of a 16-bit cache, 192 of fp32
+  if (cfg.chunk_partition_tokens <= 0)
+    cfg.chunk_partition_tokens = cfg.kv_dtype == LE_F32 ? kDefaultChunkPartition / 2 : kDefaultChunkPartition;
   if (cfg.chunk_q_tile != 16 && cfg.chunk_q_tile != 32) return LE_EUNSUPPORTED;  // MFMA row tiles
   const int dec_pb = round_to_blocks(cfg.partition_tokens, bs);
   const int chk_pb = round_to_blocks(cfg.chunk_partition_tokens, bs);
-  const bool mfma_chunks = cfg.kv_dtype != LE_F32;  // 16-bit caches: chunk rows on MFMA tiles
+  const bool mfma_chunks = true;  // chunk rows on MFMA tiles, every cache type
   const int max_decode_parts = std::max(1, kMaxMergeEntries / (cfg.q_heads / cfg.kv_heads));
 
   // ---- sizes, and validation of every slice against its table ----
