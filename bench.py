@@ -161,7 +161,7 @@ def pack_cost_us(slices, kv_dt, reps=200):
 
 
 def attention_leg(workload, kv, L, steps, warmup, partition=0, chunk_partition=0, graph=False,
-                  separate_scatter=False):
+                  separate_scatter=False, flags=0):
     """The hot path over one workload for L layers per step (see the module
     docstring); returns the fields of the JSON line for it."""
     import torch
@@ -187,7 +187,7 @@ def attention_leg(workload, kv, L, steps, warmup, partition=0, chunk_partition=0
 
     slices = slices_of(case)
     plan = kernels.Plan(slices, Q_HEADS, KV_HEADS, HEAD_DIM, BS, kv_dt,
-                        partition_tokens=partition, chunk_partition_tokens=chunk_partition)
+                        partition_tokens=partition, chunk_partition_tokens=chunk_partition, flags=flags)
     pack_us = pack_cost_us(slices, kv_dt)
     plan.upload()
     torch.cuda.synchronize()
@@ -382,6 +382,7 @@ def main():
     ap.add_argument("--no-extra-workloads", action="store_true",
                     help="skip the target and config3 sub-measurements of a config2 run")
     ap.add_argument("--partition", type=int, default=0, help="decode partition tokens (0 = planner's choice)")
+    ap.add_argument("--flags", type=int, default=0, help="le_plan_config.flags (e.g. 4 = LE_PLAN_WORK_QUEUE)")
     ap.add_argument("--chunk-partition", type=int, default=0,
                     help="chunk-row key partition tokens (0 = planner's choice)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -404,7 +405,7 @@ def main():
         sys.exit(2)
 
     res = attention_leg(args.workload, args.kv, args.layers, args.steps, args.warmup, args.partition,
-                        args.chunk_partition, args.graph, args.separate_scatter)
+                        args.chunk_partition, args.graph, args.separate_scatter, args.flags)
     # The north star's target point and the mixed step, measured the same way
     # (fewer steps), each with its own roofline.
     if args.workload == "config2" and not args.no_extra_workloads:
