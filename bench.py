@@ -302,7 +302,7 @@ def attention_leg(workload, kv, L, steps, warmup, partition=0, chunk_partition=0
 
 
 def e2e_run(arch, prompts, out_lens, pool_blocks, max_seqs=64, budget=512, arrivals_s=None,
-            prefix_caching=False, seed=4, layers=None):
+            prefix_caching=False, seed=4, layers=None, decode_graph=False):
     """One end-to-end run of the engine: scheduler, packing, device model,
     device greedy. Random-init weights N(0, 0.02) held as bf16 on the device,
     bf16 K/V cache, block 16, chunked prefill budget `budget` tokens/step."""
@@ -310,12 +310,13 @@ def e2e_run(arch, prompts, out_lens, pool_blocks, max_seqs=64, budget=512, arriv
     t0 = time.perf_counter()
     w = synthetic_weights(arch, seed, layers=layers)
     L = w.arch["layers"]
-    m = Model(w, pool_blocks, 16, dtype="bf16", kv_dtype="bf16")
+    m = Model(w, pool_blocks, 16, dtype="bf16", kv_dtype="bf16", decode_graph=decode_graph)
     del w
     setup_s = time.perf_counter() - t0
     cfg = sched_config(max_num_seqs=max_seqs, max_num_batched_tokens=budget, prefill_chunk_size=budget)
     m.run_greedy([p[:64] for p in prompts[:4]], [4] * 4, cfg)  # warm-up: code objects, rocBLAS
     toks, st = m.run_greedy(prompts, out_lens, cfg, prefix_caching=prefix_caching, arrival_s=arrivals_s)
+    replays = m.graph_replays
     m.close()
     gen_total = sum(len(t) for t in toks)
     if gen_total != sum(out_lens):
@@ -329,7 +330,8 @@ def e2e_run(arch, prompts, out_lens, pool_blocks, max_seqs=64, budget=512, arriv
             "decode_ms_per_step": round(1e3 * st.decode_seconds / st.decode_steps, 3) if st.decode_steps else None,
             "ttft_mean_s": round(st.ttft_mean_s, 4), "latency_mean_s": round(st.latency_mean_s, 3),
             "preemptions": int(st.preemptions), "setup_s": round(setup_s, 1),
-            "plan_us_per_step": round(1e6 * st.plan_seconds / st.steps, 1) if st.steps else None}
+            "plan_us_per_step": round(1e6 * st.plan_seconds / st.steps, 1) if st.steps else None,
+            "decode_graph": decode_graph, "graph_replays": replays}
 
 
 def e2e_leg(which, layers=None):
@@ -338,7 +340,8 @@ def e2e_leg(which, layers=None):
       decode64  closed loop: 64 requests at t=0, prompts U[128, 1024], 256 greedy
                 tokens each, at most 64 running; decode tok/s = tokens sampled in
                 steps with no prefill / their wall time (host scheduling, packing,
-                upload, all layers, greedy read-back)
+                upload, all layers, greedy read-back); run eagerly, then again
+                with decode steps replayed from HIP graphs ("with_decode_graph")
       config4   256 requests, Poisson arrivals at 8/s, prompts U[128, 1024],
                 outputs U[64, 256], at most 64 running, budget 512
       config5   128 requests sharing a 512-token prefix (prefix caching on) plus
@@ -350,7 +353,10 @@ def e2e_leg(which, layers=None):
         V = 32000
         prompts = [rng.integers(0, V, int(x)).astype(np.int32) for x in rng.integers(128, 1025, size=n)]
         if which == "decode64":
-            return e2e_run("tinyllama-1.1b", prompts, [256] * n, 5120, layers=layers)
+            eager = e2e_run("tinyllama-1.1b", prompts, [256] * n, 5120, layers=layers)
+            graph = e2e_run("tinyllama-1.1b", prompts, [256] * n, 5120, layers=layers, decode_graph=True)
+            return eager | {"with_decode_graph": {k: graph[k] for k in (
+                "decode_tok_per_s", "decode_ms_per_step", "tok_per_s", "graph_replays", "plan_us_per_step")}}
         outs = rng.integers(64, 257, size=n).tolist()
         arr = np.cumsum(rng.exponential(1.0 / 8.0, size=n)).tolist()
         return e2e_run("tinyllama-1.1b", prompts, outs, 5120, arrivals_s=arr, layers=layers) | \

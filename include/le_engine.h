@@ -104,6 +104,16 @@ typedef struct le_model le_model;
 le_model* le_model_create(const le_model_desc* desc, int num_blocks, int block_size, int* status);
 void le_model_destroy(le_model* m);
 
+/* Decode steps (one row per sequence, every row sampled, no logits copied
+ * back) replayed from HIP graphs: per row count, the first step runs eagerly,
+ * the second is captured (plan upload, every layer's GEMMs and kernels, the
+ * greedy selection and the token copy), later ones replay it with the new
+ * plan packed in a fixed layout (le_plan_config.table_capacity). Results are
+ * those of the eager path. Off by default. le_model_graph_replays counts the
+ * replays so far. */
+int le_model_set_decode_graph(le_model* m, int enable);
+int64_t le_model_graph_replays(const le_model* m);
+
 /* One step: slices in scheduler order. tokens_out receives the greedy token
  * of every slice with needs_logits (first maximum wins); logits_out, if not
  * NULL, receives their fp32 logits [n_logits][vocab]. */

@@ -153,7 +153,13 @@ typedef struct le_plan_config {
   int32_t chunk_q_tile;        /* query rows per chunk tile (16 or 32); 0 = default (32) */
   int32_t chunk_partition_tokens; /* key partition of chunk tiles; 0 = default */
   int32_t flags;               /* LE_PLAN_* bits below; 0 = the defaults */
-  int32_t reserved_;           /* must be 0 */
+  int32_t table_capacity;      /* 0: tables packed exactly. > 0: a fixed layout for a step of
+                                  decode rows only, so launches captured in a HIP graph can be
+                                  replayed for later steps with the same number of rows: every
+                                  sequence's table gets table_capacity entries, every row
+                                  partition_tokens-sized partitions (partition_tokens must be
+                                  given), and the work lists, partials and every array offset
+                                  depend only on the row count (le_plan_fixed_key) */
 } le_plan_config;
 
 /* le_plan_config.flags. Both select slower, equivalent launches; the tests

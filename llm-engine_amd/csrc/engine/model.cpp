@@ -16,6 +16,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstring>
+#include <map>
 #include <memory>
 #include <new>
 #include <stdexcept>
@@ -30,6 +31,9 @@
 
 namespace le::engine {
 namespace {
+
+// Decode partition of graph-replayed steps (fixed, so the layout is too).
+constexpr int kGraphPartition = 1024;
 
 }  // namespace
 
@@ -60,10 +64,17 @@ uint16_t to_bf16(float f) {  // round to nearest even, inf/nan unrounded (tensor
   return static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
 }
 
+// Bumped whenever a step buffer moves: captured decode graphs hold the old
+// addresses and are captured again.
+struct Generation {
+  uint64_t value = 0;
+};
+
 // Device buffer that grows on demand and is then reused across steps.
 struct DevBuf {
   void* p = nullptr;
   size_t cap = 0;
+  Generation* gen = nullptr;
   DevBuf() = default;
   DevBuf(const DevBuf&) = delete;
   DevBuf& operator=(const DevBuf&) = delete;
@@ -74,6 +85,7 @@ struct DevBuf {
       p = nullptr;
       hip_ok(hipMalloc(&p, bytes), "hipMalloc");
       cap = bytes;
+      if (gen) gen->value++;
       if (zero) hip_ok(hipMemsetAsync(p, 0, bytes, s), "hipMemsetAsync");
     }
     return p;
@@ -83,6 +95,7 @@ struct DevBuf {
 struct HostBuf {
   void* p = nullptr;
   size_t cap = 0;
+  Generation* gen = nullptr;
   HostBuf() = default;
   HostBuf(const HostBuf&) = delete;
   HostBuf& operator=(const HostBuf&) = delete;
@@ -93,6 +106,7 @@ struct HostBuf {
       p = nullptr;
       hip_ok(hipHostMalloc(&p, bytes, hipHostMallocDefault), "hipHostMalloc");
       cap = bytes;
+      if (gen) gen->value++;
     }
     return p;
   }
@@ -114,6 +128,8 @@ class Model {
   Model(const le_model_desc& d, int num_blocks, int block_size);
   ~Model();
   void forward(const le_step_slice* slices, int n_slices, int32_t* tokens_out, float* logits_out);
+  void set_decode_graph(bool on) { graph_on_ = on; }
+  int64_t graph_replays() const { return graph_replays_; }
   int num_blocks() const { return num_blocks_; }
   double plan_seconds() const { return plan_seconds_; }
   int block_size() const { return bs_; }
@@ -123,6 +139,10 @@ class Model {
   void* upload_parts(const std::vector<std::pair<const float*, size_t>>& parts, bool as_bf16);
   float* upload_f32(const float* host, size_t n) { return static_cast<float*>(upload(host, n, false)); }
   void gemm(const void* A, const void* B, void* C, int m, int n, int k, bool c_f32 = false);
+  // The device work of a step on stream_, from the plan upload to the token
+  // read-back into the pinned tokens buffer (nothing synchronises).
+  void enqueue_step(le_step_plan& plan, const void* host_plan, float* logits_out);
+  bool forward_graph(const le_step_slice* slices, int n_slices, int32_t* tokens_out);
 
   le_model_desc d_;
   bool bf16_;
@@ -141,6 +161,18 @@ class Model {
   std::vector<void*> kc_, vc_;
   DevBuf x_, h_, qkv_, q_, attn_, o_, gate_up_, act_buf_, logits_, tokens_, plan_dev_, ws_;
   HostBuf plan_host_, tokens_host_;
+  // Decode graphs: per row count, the whole decode step captured once (after
+  // one eager run of the same layout) and replayed while the buffers stay.
+  struct DecodeGraph {
+    hipGraphExec_t exec = nullptr;
+    int64_t plan_bytes = 0;
+    uint64_t gen = 0;
+    bool warm = false;
+  };
+  Generation gen_;
+  bool graph_on_ = false, graph_failed_ = false;
+  int64_t graph_replays_ = 0;
+  std::map<int, DecodeGraph> graphs_;
 };
 
 Model::Model(const le_model_desc& d, int num_blocks, int block_size) : d_(d) {
@@ -162,6 +194,9 @@ Model::Model(const le_model_desc& d, int num_blocks, int block_size) : d_(d) {
   num_blocks_ = num_blocks;
   act_ = bf16_ ? 2 : 4;
   if (nh_ % nkv_ != 0 || hd_ % 2 != 0) throw std::invalid_argument("head layout");
+  for (DevBuf* b : {&x_, &h_, &qkv_, &q_, &attn_, &o_, &gate_up_, &act_buf_, &logits_, &tokens_, &plan_dev_, &ws_})
+    b->gen = &gen_;
+  for (HostBuf* b : {&plan_host_, &tokens_host_}) b->gen = &gen_;
   hip_ok(hipStreamCreate(&stream_), "hipStreamCreate");
   blas_ok(rocblas_create_handle(&blas_), "rocblas_create_handle");
   blas_ok(rocblas_set_stream(blas_, stream_), "rocblas_set_stream");
@@ -215,6 +250,8 @@ Model::Model(const le_model_desc& d, int num_blocks, int block_size) : d_(d) {
 
 Model::~Model() {
   (void)hipStreamSynchronize(stream_);
+  for (auto& [n, g] : graphs_)
+    if (g.exec) (void)hipGraphExecDestroy(g.exec);
   for (void* p : owned_) (void)hipFree(p);
   if (blas_) rocblas_destroy_handle(blas_);
   if (stream_) (void)hipStreamDestroy(stream_);
@@ -265,6 +302,7 @@ void Model::gemm(const void* A, const void* B, void* C, int m, int n, int k, boo
 }
 
 void Model::forward(const le_step_slice* slices, int n_slices, int32_t* tokens_out, float* logits_out) {
+  if (graph_on_ && !graph_failed_ && !logits_out && forward_graph(slices, n_slices, tokens_out)) return;
   const auto t_plan = std::chrono::steady_clock::now();
   le_plan_config cfg{nh_, nkv_, hd_, bs_, kv_dt_, 0, 0, 0, 0, 0};
   le_step_plan plan{};
@@ -272,10 +310,84 @@ void Model::forward(const le_step_slice* slices, int n_slices, int32_t* tokens_o
   if (st != LE_ENOSPACE) le_ok(st, "le_plan_step");
   void* host = plan_host_.get(static_cast<size_t>(plan.bytes));
   le_ok(le_plan_step(slices, n_slices, &cfg, host, plan.bytes, &plan), "le_plan_step");
-  le_ok(le_plan_upload(&plan, host, plan_dev_.get(static_cast<size_t>(plan.bytes)), stream_), "le_plan_upload");
   plan_seconds_ += std::chrono::duration<double>(std::chrono::steady_clock::now() - t_plan).count();
+  if (plan.n_tokens == 0) return;
+  enqueue_step(plan, host, logits_out);
+  hip_ok(hipStreamSynchronize(stream_), "step sync");
+  if (tokens_out && plan.n_logits > 0)
+    std::memcpy(tokens_out, tokens_host_.p, static_cast<size_t>(plan.n_logits) * 4);
+}
+
+// A decode step (one row per sequence, every row sampled) replayed from a
+// captured HIP graph: the plan is packed in the fixed layout for its row
+// count (every table table_capacity entries, fixed partitions, fixed work
+// lists), so the graph captured for that row count stays valid while the
+// contexts grow; only the plan's contents change, in the same pinned buffer
+// the graph's upload node reads. Returns false when the step is not a
+// decode step (the caller runs it eagerly). Each row count runs once
+// eagerly first, so every buffer has its size and rocBLAS its kernels
+// before the capture.
+bool Model::forward_graph(const le_step_slice* slices, int n_slices, int32_t* tokens_out) {
+  if (n_slices <= 0) return false;
+  for (int i = 0; i < n_slices; i++)
+    if (slices[i].len != 1 || !slices[i].needs_logits) return false;
+  const auto t_plan = std::chrono::steady_clock::now();
+  const int cap_blocks = (d_.max_pos + bs_ - 1) / bs_;
+  le_plan_config cfg{nh_, nkv_, hd_, bs_, kv_dt_, kGraphPartition, 0, 0, 0, cap_blocks};
+  le_step_plan plan{};
+  int st = le_plan_step(slices, n_slices, &cfg, nullptr, 0, &plan);
+  if (st != LE_ENOSPACE) return false;  // e.g. a table longer than max_pos allows: run eagerly
+  DecodeGraph& g = graphs_[n_slices];
+  void* host = plan_host_.get(static_cast<size_t>(plan.bytes));
+  le_ok(le_plan_step(slices, n_slices, &cfg, host, plan.bytes, &plan), "le_plan_step");
+  plan_seconds_ += std::chrono::duration<double>(std::chrono::steady_clock::now() - t_plan).count();
+  if (!g.warm || g.plan_bytes != plan.bytes) {  // first step of this layout: eager
+    if (g.exec) (void)hipGraphExecDestroy(g.exec);
+    g = DecodeGraph{};
+    enqueue_step(plan, host, nullptr);
+    hip_ok(hipStreamSynchronize(stream_), "step sync");
+    g.warm = true;
+    g.plan_bytes = plan.bytes;
+  } else {
+    if (!g.exec || g.gen != gen_.value) {
+      if (g.exec) (void)hipGraphExecDestroy(g.exec);
+      g.exec = nullptr;
+      const uint64_t gen0 = gen_.value;
+      hipGraph_t graph = nullptr;
+      hip_ok(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+      try {
+        enqueue_step(plan, host, nullptr);
+      } catch (...) {
+        (void)hipStreamEndCapture(stream_, &graph);
+        if (graph) (void)hipGraphDestroy(graph);
+        throw;
+      }
+      const hipError_t ec = hipStreamEndCapture(stream_, &graph);
+      const hipError_t ei = ec == hipSuccess ? hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0) : ec;
+      if (graph) (void)hipGraphDestroy(graph);
+      if (ei != hipSuccess || gen_.value != gen0) {  // not capturable here: run every step eagerly
+        if (g.exec) (void)hipGraphExecDestroy(g.exec);
+        g.exec = nullptr;
+        graph_failed_ = true;
+        (void)hipGetLastError();
+        enqueue_step(plan, host, nullptr);
+        hip_ok(hipStreamSynchronize(stream_), "step sync");
+        if (tokens_out) std::memcpy(tokens_out, tokens_host_.p, static_cast<size_t>(n_slices) * 4);
+        return true;
+      }
+      g.gen = gen_.value;
+    }
+    hip_ok(hipGraphLaunch(g.exec, stream_), "hipGraphLaunch");
+    hip_ok(hipStreamSynchronize(stream_), "step sync");
+    graph_replays_++;
+  }
+  if (tokens_out) std::memcpy(tokens_out, tokens_host_.p, static_cast<size_t>(n_slices) * 4);
+  return true;
+}
+
+void Model::enqueue_step(le_step_plan& plan, const void* host_plan, float* logits_out) {
+  le_ok(le_plan_upload(&plan, host_plan, plan_dev_.get(static_cast<size_t>(plan.bytes)), stream_), "le_plan_upload");
   const int N = plan.n_tokens, R = plan.n_logits;
-  if (N == 0) return;
   const int32_t* d_ids = le_plan_dev_array(&plan, plan.off_token_ids);
   const int32_t* d_rows = le_plan_dev_array(&plan, plan.off_logit_rows);
   const size_t n = static_cast<size_t>(N);
@@ -349,12 +461,9 @@ void Model::forward(const le_step_slice* slices, int n_slices, int32_t* tokens_o
     if (logits_out)
       hip_ok(hipMemcpyAsync(logits_out, logits, static_cast<size_t>(R) * V_ * 4, hipMemcpyDeviceToHost,
                             stream_), "logits");
-    hip_ok(hipStreamSynchronize(stream_), "step sync");
-    if (tokens_out) std::memcpy(tokens_out, htok, static_cast<size_t>(R) * 4);
-  } else {
-    hip_ok(hipStreamSynchronize(stream_), "step sync");
   }
 }
+
 
 }  // namespace le::engine
 
@@ -395,6 +504,14 @@ le_model* le_model_create(const le_model_desc* desc, int num_blocks, int block_s
 }
 
 void le_model_destroy(le_model* m) { delete m; }
+
+int le_model_set_decode_graph(le_model* m, int enable) {
+  if (!m) return LE_EINVAL;
+  m->impl->set_decode_graph(enable != 0);
+  return LE_OK;
+}
+
+int64_t le_model_graph_replays(const le_model* m) { return m ? m->impl->graph_replays() : 0; }
 
 int le_argmax_rows(const float* logits, int rows, int vocab, int32_t* out, hipStream_t stream) {
   if (rows < 0 || vocab <= 0) return LE_EINVAL;

@@ -129,10 +129,13 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
   if (cfg.block_size <= 0 || cfg.q_heads <= 0 || cfg.kv_heads <= 0 || cfg.head_dim <= 0)
     return LE_EINVAL;
   if (cfg.kv_dtype != LE_F32 && cfg.kv_dtype != LE_BF16 && cfg.kv_dtype != LE_F16) return LE_EINVAL;
-  if ((cfg.flags & ~(LE_PLAN_WRITE_THROUGH | LE_PLAN_TWO_LAUNCHES)) != 0 || cfg.reserved_ != 0)
+  if ((cfg.flags & ~(LE_PLAN_WRITE_THROUGH | LE_PLAN_TWO_LAUNCHES)) != 0 || cfg.table_capacity < 0)
     return LE_EINVAL;
+  // Fixed layout (table_capacity > 0): decode rows only, a given partition.
+  const bool fixed = cfg.table_capacity > 0;
+  if (fixed && cfg.partition_tokens <= 0) return LE_EINVAL;
   const int bs = cfg.block_size;
-  if (cfg.partition_tokens <= 0) {
+  if (!fixed && cfg.partition_tokens <= 0) {
     // Size decode partitions so the step has about kTargetItems workgroups,
     // about one per CU. Each workgroup pays a fixed chain of dependent memory
     // round trips (block ids, then K/V; partial store, arrival counter, merge)
@@ -177,6 +180,8 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
   for (int i = 0; i < n_slices; i++) {
     const le_step_slice& s = slices[i];
     if (s.len <= 0 || s.start < 0 || s.num_blocks < 0 || !s.tokens) return LE_EINVAL;
+    if (fixed && s.len != 1) return LE_EUNSUPPORTED;
+    if (fixed && s.num_blocks > cfg.table_capacity) return LE_EINVAL;
     if (s.num_blocks > 0 && !s.blocks) return LE_EINVAL;
     const int last = s.start + s.len - 1;
     if (last / bs >= s.num_blocks) return LE_EINVAL;  // a position without a block
@@ -199,6 +204,10 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
     max_pos = std::max(max_pos, last);
   }
   if (n_tok > INT32_MAX / 2) return LE_EUNSUPPORTED;
+  // Fixed layout: every row owns parts_cap partial slots and every table
+  // table_capacity entries, whatever its current length.
+  const int parts_cap = fixed ? std::min((cfg.table_capacity + dec_pb - 1) / dec_pb, max_decode_parts) : 0;
+  if (fixed) n_table = static_cast<int64_t>(n_seqs) * cfg.table_capacity;
 
   // Table offset of each distinct sequence in the concatenated tables.
   std::vector<int32_t> seq_table_off(static_cast<size_t>(n_seqs));
@@ -206,7 +215,7 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
     int32_t o = 0;
     for (int s = 0; s < n_seqs; s++) {
       seq_table_off[s] = o;
-      o += slices[seq_first_slice[s]].num_blocks;
+      o += fixed ? cfg.table_capacity : slices[seq_first_slice[s]].num_blocks;
     }
   }
 
@@ -257,12 +266,13 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
             d.table_off = seq_table_off[slice_seq[i]];
             d.blk_begin = static_cast<int32_t>(static_cast<int64_t>(j) * nb / J);
             d.blk_end = static_cast<int32_t>(static_cast<int64_t>(j + 1) * nb / J);
-            d.part = J > 1 ? parts + j : -1;
-            d.part_begin = parts;
+            const int32_t first = fixed ? (t + r) * parts_cap : parts;
+            d.part = J > 1 ? first + j : -1;
+            d.part_begin = first;
             d.n_parts = J;
             dec.push_back(d);
           }
-          if (J > 1) parts += J;
+          if (J > 1 && !fixed) parts += J;
         }
       }
       t += s.len;
@@ -272,7 +282,10 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
   // Longest work first: workgroups start over a couple of microseconds in
   // launch order, so the items on the critical path (most keys) go first.
   // Merges do not depend on the order (partials are addressed by index).
-  if (parts > 0) {
+  bool split = parts > 0;  // chunk or decode partials (fixed layout: decode rows checked below)
+  for (const auto& d : dec) split |= d.part >= 0;
+  if (fixed) parts = static_cast<int32_t>(n_tok) * parts_cap;
+  if (split) {
     dec = place_decode_items(dec);
   } else {
     std::stable_sort(dec.begin(), dec.end(), [](const le::DecodeItem& a, const le::DecodeItem& b) {
@@ -287,6 +300,18 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
     std::stable_sort(chk.begin(), chk.end(), [](const le::ChunkItem& a, const le::ChunkItem& b) {
       return a.blk_end - a.blk_begin > b.blk_end - b.blk_begin;
     });
+  }
+
+  if (fixed) {
+    // one item count for every step of this row count: rows * parts_cap
+    // items dealt into eight bins, each bin at most one row's partitions
+    // longer than the mean, padded to that with empty items
+    const size_t cap_items = kXcds * ((static_cast<size_t>(n_tok) * parts_cap + kXcds - 1) / kXcds + parts_cap);
+    if (dec.size() > cap_items) return LE_EUNSUPPORTED;
+    le::DecodeItem pad{};
+    pad.token = -1;
+    pad.part = -1;
+    dec.resize(cap_items, pad);
   }
 
   // ---- layout: every array 256-byte aligned in one buffer ----
@@ -326,6 +351,7 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
   int32_t ids_stride = 0;
   for (const auto& d : dec) ids_stride = std::max(ids_stride, d.blk_end - d.blk_begin);
   for (const auto& c : chk) ids_stride = std::max(ids_stride, c.blk_end - c.blk_begin);
+  if (fixed) ids_stride = std::max(dec_pb, (cfg.table_capacity + parts_cap - 1) / parts_cap);
   ids_stride = (ids_stride + 3) / 4 * 4;
   P.decode_ids_stride = ids_stride;
   P.off_decode_ids = take(static_cast<int64_t>(dec.size() + chk.size()) * ids_stride * 4);
@@ -353,7 +379,9 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
     const le_step_slice& f = slices[seq_first_slice[s]];
     table_offset[s] = nt;
     if (f.num_blocks) std::memcpy(tables + nt, f.blocks, sizeof(int32_t) * f.num_blocks);
-    nt += f.num_blocks;
+    const int32_t width = fixed ? cfg.table_capacity : f.num_blocks;
+    for (int32_t j = f.num_blocks; j < width; j++) tables[nt + j] = -1;
+    nt += width;
   }
   int32_t t = 0, r = 0;
   cu_q[0] = 0;

@@ -51,7 +51,7 @@ class PlanConfig(ctypes.Structure):
         ("chunk_q_tile", ctypes.c_int32),
         ("chunk_partition_tokens", ctypes.c_int32),
         ("flags", ctypes.c_int32),
-        ("reserved_", ctypes.c_int32),
+        ("table_capacity", ctypes.c_int32),
     ]
 
 
@@ -169,6 +169,8 @@ SIGNATURES = {
     "le_model_create": (ctypes.c_void_p, [ctypes.POINTER(ModelDesc), ctypes.c_int, ctypes.c_int,
                                           ctypes.POINTER(ctypes.c_int)]),
     "le_model_destroy": (None, [ctypes.c_void_p]),
+    "le_model_set_decode_graph": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
+    "le_model_graph_replays": (ctypes.c_int64, [ctypes.c_void_p]),
     "le_model_forward": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(StepSlice), ctypes.c_int,
                                         ctypes.c_void_p, ctypes.c_void_p]),
     "le_run_greedy": (ctypes.c_int, [

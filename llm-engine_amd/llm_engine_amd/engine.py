@@ -78,9 +78,11 @@ class Model:
     DTYPES = {"f32": LE_F32, "bf16": LE_BF16, "f16": LE_F16}
 
     def __init__(self, w: Weights, num_blocks: int, block_size: int = 16, dtype: str = "f32",
-                 kv_dtype: str | None = None, attention: str = "ragged"):
+                 kv_dtype: str | None = None, attention: str = "ragged", decode_graph: bool = False):
         """attention: "ragged" (le_ragged_paged_attention_qkv over the packed
-        step) or "reference" (the reference-shaped le_attention_decode)."""
+        step) or "reference" (the reference-shaped le_attention_decode).
+        decode_graph: replay decode steps from captured HIP graphs
+        (le_model_set_decode_graph)."""
         a = w.arch
         self.arch = a
         self.num_blocks, self.block_size = num_blocks, block_size
@@ -107,6 +109,12 @@ class Model:
         if not self._h:
             raise _lib.LeError("le_model_create", st.value or _lib.LE_EINVAL)
         self._keep = None  # weights are on the device now
+        if decode_graph:
+            check("le_model_set_decode_graph", _lib.load().le_model_set_decode_graph(self._h, 1))
+
+    @property
+    def graph_replays(self) -> int:
+        return int(_lib.load().le_model_graph_replays(self._h))
 
     def close(self):
         if getattr(self, "_h", None):

@@ -167,9 +167,9 @@ class Plan:
     def __init__(self, slices: list[Slice], q_heads: int, kv_heads: int, head_dim: int,
                  block_size: int, kv_dtype: torch.dtype, partition_tokens: int = 0,
                  chunk_partition_tokens: int = 0, device="cuda", pin: bool = True, chunk_q_tile: int = 0,
-                 flags: int = 0):
+                 flags: int = 0, table_capacity: int = 0):
         self.cfg = PlanConfig(q_heads, kv_heads, head_dim, block_size, _dt(kv_dtype),
-                              partition_tokens, chunk_q_tile, chunk_partition_tokens, flags, 0)
+                              partition_tokens, chunk_q_tile, chunk_partition_tokens, flags, table_capacity)
         keep = []
         arr = (StepSlice * max(1, len(slices)))()
         for i, s in enumerate(slices):

@@ -151,7 +151,10 @@ def check_work_lists(plan, slices, bs=16):
     for it in chk:
         if it[4] >= 0:
             owned += [int(it[4]) + r * int(it[5]) for r in range(int(it[1]))]
-    assert sorted(owned) == list(range(P.n_parts))
+    if P.cfg.table_capacity > 0:  # fixed layout: each row owns a fixed slot range, some unused
+        assert len(set(owned)) == len(owned) and all(0 <= o < P.n_parts for o in owned)
+    else:
+        assert sorted(owned) == list(range(P.n_parts))
 
 
 TRACES = np.load(ROOT / "tests" / "golden" / "schedule_ref.npz")
@@ -262,3 +265,36 @@ def test_noalloc_rejects_steps_beyond_its_scratch():
     empty = Plan([], 14, 2, 64, 16, torch.bfloat16, device="cpu", pin=False)
     assert L.le_ragged_paged_attention_noalloc(nul, 0, nul, nul, 1, 100, ctypes.byref(empty.plan), 0.125,
                                                nul, nul) == _lib.LE_OK
+
+
+def test_fixed_layout_is_constant_across_decode_steps():
+    """table_capacity > 0: a decode step's plan has one layout for a given row
+    count (every array offset, the item and partial counts, the id stride),
+    however the contexts grow, so launches captured in a HIP graph replay
+    for later steps; the values are still the reference packing's."""
+    from llm_engine_amd.kernels import Slice
+    rng = np.random.default_rng(7)
+    cap, n = 128, 24
+    blocks = [rng.permutation(5000)[:cap].astype(np.int32) for _ in range(n)]
+    ctx = rng.integers(1, 1500, n)
+    layout = None
+    for step in range(40):
+        c = ctx + step * 13  # crosses block and partition boundaries
+        sl = [Slice(100 + i, int(c[i]) - 1, 1, True, blocks[i][:(int(c[i]) + 15) // 16],
+                    np.arange(int(c[i]), dtype=np.int32)) for i in range(n)]
+        plan = _plan(sl, partition_tokens=512, table_capacity=cap)
+        P = plan.plan
+        key = (P.bytes, P.n_decode_items, P.n_parts, P.decode_ids_stride, P.n_table) + tuple(
+            getattr(P, f) for f, _ in type(P)._fields_ if f.startswith("off_"))
+        layout = layout or key
+        assert key == layout, step
+        want = oracle.pack_step([(s.seq_key, s.start, s.len, s.needs_logits, s.blocks, s.tokens) for s in sl], 16)
+        for f in ("token_ids", "positions", "slots", "token_seq", "logit_rows"):
+            assert np.array_equal(plan.host_array(f), getattr(want, f)), f
+        tab = plan.host_array("tables").reshape(n, cap)
+        for i, s in enumerate(sl):
+            assert np.array_equal(tab[i, :len(s.blocks)], s.blocks) and (tab[i, len(s.blocks):] == -1).all()
+        assert list(plan.host_array("table_offset")) == [i * cap for i in range(n)]
+        check_work_lists(plan, sl)
+    with pytest.raises(ValueError):  # prefill chunks have no fixed layout
+        _plan([Slice(1, 0, 5, True, blocks[0][:1], np.zeros(5, np.int32))], partition_tokens=512, table_capacity=cap)

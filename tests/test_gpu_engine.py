@@ -37,14 +37,15 @@ def run_both(w, prompts, max_tokens, num_blocks, cfg=None, prefix=False, frag=0,
     return gpu, cpu, stats
 
 
-@pytest.mark.parametrize("attention", ["ragged", "reference"])
-def test_config1_matches_oracle_token_for_token(gpu, attention):
+@pytest.mark.parametrize("attention,graph", [("ragged", False), ("reference", False), ("ragged", True)])
+def test_config1_matches_oracle_token_for_token(gpu, attention, graph):
     """Qwen2.5-0.5B (24 layers) random-init fp32, 8 prompts of
     16..512 tokens, 32 greedy tokens, fragmented 4096-block pool. Through both
     attention entries: the ragged plan (le_ragged_paged_attention_qkv) and the
     reference-shaped launcher (le_attention_decode), which therefore give the
     same greedy tokens (the reference requires this of its two attention
-    kernels, test_cuda_invariance.cpp:295-344)."""
+    kernels, test_cuda_invariance.cpp:295-344). And with decode steps replayed
+    from captured HIP graphs (fixed-layout plans)."""
     from llm_engine_amd.engine import Model, sched_config, synthetic_weights
     import sys
     sys.path.insert(0, str(GOLD))
@@ -52,14 +53,17 @@ def test_config1_matches_oracle_token_for_token(gpu, attention):
     fx = json.loads((GOLD / "config1_tokens.json").read_text())
     w = synthetic_weights(fx["arch"], fx["weight_seed"])
     assert weight_digest(w) == fx["weight_digest"], "weight generator changed; regenerate the fixture"
-    m = Model(w, fx["num_blocks"], 16, dtype="f32", attention=attention)
+    m = Model(w, fx["num_blocks"], 16, dtype="f32", attention=attention, decode_graph=graph)
     toks, stats = m.run_greedy(fx["prompts"], [fx["gen"]] * len(fx["prompts"]),
                                sched_config(max_num_batched_tokens=fx["max_num_batched_tokens"]),
                                fragment_blocks=fx["fragment_blocks"])
-    m.close()
-    print(f"config1 ({attention}): {stats.steps} steps, {stats.decode_tokens} tokens in {stats.seconds:.2f}s, "
+    replays = m.graph_replays
+    print(f"config1 ({attention}, graph {graph}: {replays} replays): {stats.steps} steps, {stats.decode_tokens} tokens in {stats.seconds:.2f}s, "
           f"plan {stats.plan_seconds / stats.steps * 1e6:.0f} us/step; oracle min top-2 margins {fx['min_margin']}")
+    m.close()
     assert toks == fx["tokens"]
+    if graph:
+        assert replays > 10
 
 
 @pytest.mark.parametrize("case", ["fragmented_multi", "chunked16", "preempt", "prefix"])
