@@ -162,12 +162,15 @@ typedef struct le_plan_config {
                                   depend only on the row count (le_plan_fixed_key) */
 } le_plan_config;
 
-/* le_plan_config.flags. Both select slower, equivalent launches; the tests
- * use them to check that every launch shape gives the same result. */
+/* le_plan_config.flags. The first two select slower, equivalent launches;
+ * the tests use them to check that every launch shape gives the same result. */
 #define LE_PLAN_WRITE_THROUGH 1 /* split rows exchange partials through write-through
                                    stores, without relying on the XCD placement */
 #define LE_PLAN_TWO_LAUNCHES 2  /* a mixed step runs its decode and chunk rows as two
                                    launches instead of one */
+#define LE_PLAN_SIMULATE_MISPLACEMENT 4 /* fault injection for tests of the placement
+                                   guard (le_xcd_misplacements): workgroups whose linear
+                                   id / 8 is odd act as if they ran off their planned XCD */
 
 typedef struct le_step_plan {
   le_plan_config cfg;
@@ -211,10 +214,10 @@ static inline const int32_t* le_plan_dev_array(const le_step_plan* plan, int64_t
  * (3)(4) Ragged paged attention over a packed step.
  * Decode rows (slices of length 1) run the bandwidth kernel: one workgroup per
  * (row, kv head, context partition), each K/V row read once for the whole
- * GQA group. Prefill-chunk rows run the MFMA kernel with a bf16 cache
- * (causal mask by absolute position against the cached prefix), and the
- * bandwidth kernel row by row with an fp32 cache. Split rows are merged
- * inside their launch. The result equals le_attention_decode on the same step.
+ * GQA group. Prefill-chunk rows run the MFMA tile kernel (bf16 / fp16 tiles
+ * for 16-bit caches, fp32 tiles for an fp32 cache), with a causal mask by
+ * absolute position against the cached prefix. Split rows are merged inside
+ * their launch. The result equals le_attention_decode on the same step.
  * ------------------------------------------------------------------------ */
 size_t le_ragged_workspace_size(const le_step_plan* plan);
 
@@ -243,6 +246,30 @@ size_t le_noalloc_scratch_bytes(void);
 int le_ragged_paged_attention_noalloc(const void* q, le_dtype act_dtype, const void* k_cache,
                                       const void* v_cache, le_dtype kv_dtype, int64_t num_cache_blocks,
                                       const le_step_plan* plan, float scale, void* out, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * XCD placement guard. No counterpart in the reference (its GPU has one L2).
+ * A plan launch places all partitions of a split row on one XCD, assuming
+ * the device sends workgroup i to XCD i % 8, and the partitions then exchange
+ * their partials through that XCD's L2 with plain stores. The assumption is
+ * probed once per device (first plan launch with split rows, outside stream
+ * capture); if it fails, partials are stored write-through and placement
+ * plays no part. Every workgroup of a split row also checks its own XCD
+ * (HW_REG_XCC_ID) when it arrives: one that is elsewhere writes its L2 back
+ * before arriving (so a merge on the planned XCD sees its partial) and is
+ * counted, and a merge that is itself elsewhere, and so cannot see partials
+ * left in the planned XCD's L2, writes NaN over its outputs instead of a
+ * wrong value. So results are correct or NaN, never silently wrong.
+ *
+ * le_xcd_misplacements reads and clears the current device's count of
+ * workgroups found off their planned XCD (synchronises `stream`); a nonzero
+ * count switches the device to write-through partials for the rest of the
+ * process. le_xcd_placement_recheck forgets the probe result of the current
+ * device, so the next plan launch probes again: call it after changing the
+ * device's compute partitioning or the CU masks of the streams in use.
+ * ------------------------------------------------------------------------ */
+int le_xcd_misplacements(hipStream_t stream, int64_t* count);
+void le_xcd_placement_recheck(void);
 
 /* ------------------------------------------------------------------------
  * (2)+(3) The scatter and the attention of a step in one call.

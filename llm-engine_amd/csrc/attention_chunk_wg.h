@@ -546,11 +546,23 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
       }
     }
   }
+  const bool misplaced = misplaced_wg(p.l2_local, p.lin);
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are performed
+  if (misplaced) {  // ... and written back from this L2
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __builtin_amdgcn_s_waitcnt(0);
+  }
   __syncthreads();                // ... and every other thread's
   int32_t* counter = p.parts.counters + static_cast<int64_t>(tok0) * p.kv_heads + kvh;
-  if (tid == 0)
-    last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == it.part_stride - 1;
+  if (tid == 0) {
+    if (misplaced) __hip_atomic_fetch_add(p.parts.misplaced, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int seen = __hip_atomic_fetch_add(counter, misplaced ? 1 + kMisplacedArrival : 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+    // A merge off the planned XCD cannot see partials left in the planned
+    // XCD's L2: it poisons the tile's output instead of returning a wrong one.
+    const bool is_last = arrivals(seen) == it.part_stride - 1;
+    last = !is_last ? 0 : (misplaced && misplaced_arrivals(seen) < it.part_stride - 1 ? 2 : 1);
+  }
   __syncthreads();
   if (!last) return;
 
@@ -560,7 +572,13 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
   const int base = it.part0 - it.part;
   // Rounds of loads as wide as the tile's partition count (up to 6 for hd
   // 64), so no load is issued twice.
-  if constexpr (HD == 64) {
+  if (last == 2) {
+    for (int i = tid; i < nq * G * HD; i += kThreads) {
+      const int r = i / (G * HD), j = i - r * (G * HD);
+      elem<ACT>::store1(static_cast<ACT*>(p.out) + (static_cast<int64_t>(tok0 + r) * p.q_heads + kvh * G) * HD + j,
+                        __builtin_nanf(""));
+    }
+  } else if constexpr (HD == 64) {
     if (J <= 4) merge_tile<ACT, HD, 4>(p, it, acc_rsrc, ml, rec_tile, base, J, G, kvh, nq, tok0);
     else merge_tile<ACT, HD, 6>(p, it, acc_rsrc, ml, rec_tile, base, J, G, kvh, nq, tok0);
   } else {

@@ -282,12 +282,23 @@ __device__ __forceinline__ void arrive_and_merge(const DecodeParams& p, const Wo
   const int n4 = G * HD / 4;
   const int64_t head0 = static_cast<int64_t>(w.token) * p.q_heads + kvh * G;
   float* ml = reinterpret_cast<float*>(p.parts.ml);
+  const bool off = misplaced_wg(p.l2_local, p.lin);
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are performed
+  if (off) {  // ... and written back from this L2
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __builtin_amdgcn_s_waitcnt(0);
+  }
   __syncthreads();                // ... and every other thread's
   int32_t* counter = p.parts.counters + static_cast<int64_t>(w.token) * p.kv_heads + kvh;
-  if (tid == 0)
-    *flag = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-            w.n_parts - 1;
+  if (tid == 0) {
+    if (off) __hip_atomic_fetch_add(p.parts.misplaced, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int seen = __hip_atomic_fetch_add(counter, off ? 1 + kMisplacedArrival : 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+    // A merge off the planned XCD cannot see partials left in the planned
+    // XCD's L2: it poisons the output instead of returning a wrong one.
+    const bool last = arrivals(seen) == w.n_parts - 1;
+    *flag = !last ? 0 : (off && misplaced_arrivals(seen) < w.n_parts - 1 ? 2 : 1);
+  }
   __syncthreads();
   if (!*flag) return;
   // Every other partition incremented the counter after its partial was
@@ -297,10 +308,14 @@ __device__ __forceinline__ void arrive_and_merge(const DecodeParams& p, const Wo
   const __amdgpu_buffer_rsrc_t r = coherent_rsrc(p.parts.acc + rbase * HD);
   // Batches as wide as the row's partition count (up to kMergeBatch), so no
   // load is issued twice.
-  if (np <= kMergeBatch / 2)
+  if (*flag == 2) {
+    ACT* out = static_cast<ACT*>(p.out) + head0 * HD;
+    for (int i = tid; i < G * HD; i += NTHR) elem<ACT>::store1(out + i, __builtin_nanf(""));
+  } else if (np <= kMergeBatch / 2) {
     merge_parts<ACT, HD, NTHR, kMergeBatch / 2>(p, r, ml, rbase, np, n4, head0);
-  else
+  } else {
     merge_parts<ACT, HD, NTHR, kMergeBatch>(p, r, ml, rbase, np, n4, head0);
+  }
   if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 

@@ -225,6 +225,28 @@ __device__ __forceinline__ f32x4v ld_coherent16(__amdgpu_buffer_rsrc_t r, uint32
 __device__ __forceinline__ void st_coherent16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, f32x4v v) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4raw, v), r, byte_off, 0, kCachePolicySc1);
 }
+// Split rows of a plan launch are placed so that all partitions of a row run
+// on one XCD, assuming workgroup i (linear id `lin` over the grid) runs on XCD
+// i % 8; their partials then go through that XCD's L2 with plain stores.
+// Each split-row workgroup checks the assumption when it arrives (the check
+// overlaps the wait for its partial stores). l2_local: 0 off, 1 on, 2 on with
+// fault injection (workgroups with an odd lin / 8 count as misplaced).
+__device__ __forceinline__ bool misplaced_wg(int l2_local, int lin) {
+  if (l2_local == 0) return false;
+  unsigned v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  const bool injected = l2_local == 2 && ((lin / 8) & 1);
+  return injected || (v & 0xf) != static_cast<unsigned>(lin % 8);
+}
+// A misplaced workgroup writes its L2 back (agent-scope release) before it
+// arrives, so a merge on the planned XCD sees its partial; a merge that is
+// itself misplaced cannot see partials left in the planned XCD's L2 and
+// writes NaN instead. Arrival counters count partitions in their low 16 bits
+// and misplaced partitions in the high bits.
+constexpr int kMisplacedArrival = 1 << 16;
+__device__ __forceinline__ int arrivals(int counter) { return counter & (kMisplacedArrival - 1); }
+__device__ __forceinline__ int misplaced_arrivals(int counter) { return counter >> 16; }
+
 // A plain 16-byte store (write-back into the XCD's L2), for data that only
 // workgroups on the same XCD read back.
 __device__ __forceinline__ void st_l2_16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, f32x4v v) {

@@ -129,7 +129,7 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
   if (cfg.block_size <= 0 || cfg.q_heads <= 0 || cfg.kv_heads <= 0 || cfg.head_dim <= 0)
     return LE_EINVAL;
   if (cfg.kv_dtype != LE_F32 && cfg.kv_dtype != LE_BF16 && cfg.kv_dtype != LE_F16) return LE_EINVAL;
-  if ((cfg.flags & ~(LE_PLAN_WRITE_THROUGH | LE_PLAN_TWO_LAUNCHES)) != 0 || cfg.table_capacity < 0)
+  if ((cfg.flags & ~(LE_PLAN_WRITE_THROUGH | LE_PLAN_TWO_LAUNCHES | LE_PLAN_SIMULATE_MISPLACEMENT)) != 0 || cfg.table_capacity < 0)
     return LE_EINVAL;
   // Fixed layout (table_capacity > 0): decode rows only, a given partition.
   const bool fixed = cfg.table_capacity > 0;

@@ -24,6 +24,7 @@ LE_BF16 = 1
 LE_F16 = 2
 LE_PLAN_WRITE_THROUGH = 1
 LE_PLAN_TWO_LAUNCHES = 2
+LE_PLAN_SIMULATE_MISPLACEMENT = 4
 
 c_i32p = ctypes.POINTER(ctypes.c_int32)
 
@@ -184,6 +185,8 @@ SIGNATURES = {
         ctypes.c_int64, ctypes.POINTER(StepPlan), ctypes.c_float, ctypes.c_void_p,
         ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "le_noalloc_scratch_bytes": (ctypes.c_size_t, []),
+    "le_xcd_misplacements": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64)]),
+    "le_xcd_placement_recheck": (None, []),
     "le_ragged_paged_attention_noalloc": (ctypes.c_int, [
         ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
         ctypes.c_int64, ctypes.POINTER(StepPlan), ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p]),

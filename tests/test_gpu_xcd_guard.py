@@ -1,0 +1,73 @@
+"""The XCD placement guard of split rows (le_xcd_misplacements).
+
+Split rows of a plan launch exchange partials through one XCD's L2, placed
+on the assumption that workgroup i runs on XCD i % 8. A workgroup that finds
+itself elsewhere writes its L2 back before it arrives, and a merge that would
+need partials left in another XCD's L2 writes NaN instead of a wrong value. The
+LE_PLAN_SIMULATE_MISPLACEMENT flag forces the condition from the host (the
+kernels treat every workgroup whose linear id / 8 is odd as misplaced), so
+the guard's paths run while every kernel still exits normally."""
+import numpy as np
+import pytest
+import torch
+
+from cases import make_case
+from gpu_util import device_q, slices_of, to_dev_cache
+from llm_engine_amd._lib import LE_PLAN_SIMULATE_MISPLACEMENT, LE_PLAN_WRITE_THROUGH
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(gpu):
+    from llm_engine_amd import kernels
+    # split decode rows (long contexts, 256-token partitions) and split chunk tiles
+    ctx = [3000, 2600, 2100, 1800, 900, 1500] + [1200] * 24
+    q_len = [200, 1, 1, 1, 130, 1] + [1] * 24
+    case = make_case(ctx, q_len=q_len, num_blocks=4096, seed=71, kv_bf16=True)
+    q, _ = device_q(case, torch.float32, gpu)
+    kc, vc = to_dev_cache(case.k_cache, gpu), to_dev_cache(case.v_cache, gpu)
+
+    def run(flags):
+        plan = kernels.Plan(slices_of(case), case.q_heads, case.kv_heads, case.head_dim, case.block_size,
+                            kc.dtype, partition_tokens=256, flags=flags).upload()
+        assert plan.plan.n_parts > 0 and plan.plan.n_chunk_items > 0
+        ws = kernels.new_workspace(plan.workspace_size(), gpu)
+        out = kernels.ragged_paged_attention(q, kc, vc, plan, case.scale, workspace=ws)
+        torch.cuda.synchronize()
+        assert int(ws[:256 * 1024].count_nonzero().item()) == 0  # counters left at zero
+        return out.float().cpu().numpy()
+
+    return case, run
+
+
+def test_misplaced_partials_are_correct_or_nan(gpu):
+    from llm_engine_amd import kernels
+    case, run = _setup(gpu)
+    kernels.xcd_placement_recheck()
+    ref = run(LE_PLAN_WRITE_THROUGH)          # placement plays no part
+    l2 = run(0)
+    if kernels.xcd_misplacements() != 0:
+        pytest.skip("this device does not hold the XCD placement; the guard's L2 path is off")
+    assert np.array_equal(l2, ref)            # same partials, same merge order
+
+    sim = run(LE_PLAN_SIMULATE_MISPLACEMENT)
+    misses = kernels.xcd_misplacements()      # reads, clears, switches to write-through
+    groups = sim.reshape(sim.shape[0], case.kv_heads, -1)
+    nan = np.isnan(groups).all(axis=2)
+    ok = (groups == ref.reshape(groups.shape)).all(axis=2)
+    print(f"misplaced workgroups {misses}; (row, kv head) groups poisoned {int(nan.sum())} "
+          f"of {nan.size}, exact {int(ok.sum())}")
+    # Which groups are poisoned depends on arrival order (a misplaced
+    # partition writes its L2 back first, so it tends to arrive last and
+    # merge); that every group is exact or all NaN does not.
+    assert misses > 0
+    assert np.all(nan | ok)                   # every group is right or all NaN, never wrong
+
+    # after a nonzero count the device stores write-through: the simulation is inert
+    assert np.array_equal(run(LE_PLAN_SIMULATE_MISPLACEMENT), ref)
+    assert kernels.xcd_misplacements() == 0
+
+    # a recheck probes again and restores the L2 exchange
+    kernels.xcd_placement_recheck()
+    assert np.array_equal(run(0), ref)
+    assert kernels.xcd_misplacements() == 0
