@@ -9,8 +9,8 @@
  * reports. Exceptions never cross this boundary.
  *
  * Attention workspaces: zero-fill a workspace once, before its first use;
- * every launch leaves it that way again. Its first 256 KiB hold arrival
- * counters (one per (row, kv head); at most 65536 of them, else
+ * every launch leaves it that way again. Its first 512 KiB hold arrival
+ * counters (64-bit, one per (row, kv head); at most 65536 of them, else
  * LE_EUNSUPPORTED) at the same place for every plan, then the split-K
  * partials, so one workspace of the largest size needed can serve steps of
  * any shape. Launches that share a workspace must be ordered on one stream.
@@ -170,7 +170,7 @@ typedef struct le_plan_config {
                                    launches instead of one */
 #define LE_PLAN_SIMULATE_MISPLACEMENT 4 /* fault injection for tests of the placement
                                    guard (le_xcd_misplacements): workgroups whose linear
-                                   id / 8 is odd act as if they ran off their planned XCD */
+                                   id / 8 is odd report another XCD */
 
 typedef struct le_step_plan {
   le_plan_config cfg;
@@ -249,21 +249,21 @@ int le_ragged_paged_attention_noalloc(const void* q, le_dtype act_dtype, const v
 
 /* ------------------------------------------------------------------------
  * XCD placement guard. No counterpart in the reference (its GPU has one L2).
- * A plan launch places all partitions of a split row on one XCD, assuming
- * the device sends workgroup i to XCD i % 8, and the partitions then exchange
- * their partials through that XCD's L2 with plain stores. The assumption is
- * probed once per device (first plan launch with split rows, outside stream
- * capture); if it fails, partials are stored write-through and placement
- * plays no part. Every workgroup of a split row also checks its own XCD
- * (HW_REG_XCC_ID) when it arrives: one that is elsewhere writes its L2 back
- * before arriving (so a merge on the planned XCD sees its partial) and is
- * counted, and a merge that is itself elsewhere, and so cannot see partials
- * left in the planned XCD's L2, writes NaN over its outputs instead of a
- * wrong value. So results are correct or NaN, never silently wrong.
+ * A plan launch places all partitions of a split row on one XCD: the
+ * device deals a launch's workgroups to its 8 XCDs round robin, so
+ * workgroups whose ids are equal modulo 8 share an XCD (wherever the deal
+ * starts), and the partitions exchange their partials through that XCD's L2
+ * with plain stores. The dealing is probed once per device (first plan
+ * launch with split rows, outside stream capture); if it is not round robin,
+ * partials are stored write-through and placement plays no part. Every
+ * partition also reports its XCD (HW_REG_XCC_ID, relative to its id) when it
+ * arrives, and the last to arrive merges only if all partitions shared its
+ * XCD; otherwise it writes NaN over its outputs instead of a wrong value and
+ * counts the event. So results are correct or NaN, never silently wrong.
  *
- * le_xcd_misplacements reads and clears the current device's count of
- * workgroups found off their planned XCD (synchronises `stream`); a nonzero
- * count switches the device to write-through partials for the rest of the
+ * le_xcd_misplacements reads and clears the current device's count of split
+ * rows found spread over XCDs (synchronises `stream`); a nonzero count
+ * switches the device to write-through partials for the rest of the
  * process. le_xcd_placement_recheck forgets the probe result of the current
  * device, so the next plan launch probes again: call it after changing the
  * device's compute partitioning or the CU masks of the streams in use.

@@ -42,10 +42,10 @@ size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 // every plan, so a workspace reused across steps of different shapes never
 // finds an earlier step's partials where this step's counters are: the
 // counters are zero at every launch because every launch leaves them zero.
-constexpr size_t kCounterRegion = 256 * 1024;  // 65536 (row, kv head) counters
+constexpr size_t kCounterRegion = 512 * 1024;  // 65536 (row, kv head) 64-bit counters
 size_t counter_bytes(int64_t, int) { return kCounterRegion; }
 bool counters_fit(int64_t n_rows, int kv_heads) {
-  return static_cast<size_t>(n_rows) * kv_heads * sizeof(int32_t) <= kCounterRegion;
+  return static_cast<size_t>(n_rows) * kv_heads * sizeof(uint64_t) <= kCounterRegion;
 }
 
 size_t partial_bytes(int64_t n_parts, int64_t n_rows, int q_heads, int kv_heads, int head_dim) {
@@ -58,7 +58,7 @@ le::PartialLayout carve_partials(void* ws, int64_t n_parts, int64_t n_rows, int 
                                  int kv_heads, int head_dim) {
   le::PartialLayout L;
   char* b = static_cast<char*>(ws);
-  L.counters = reinterpret_cast<int32_t*>(b);
+  L.counters = reinterpret_cast<unsigned long long*>(b);
   b += counter_bytes(n_rows, kv_heads);
   L.acc = reinterpret_cast<float*>(b);
   b += align256(static_cast<size_t>(n_parts) * q_heads * head_dim * sizeof(float));

@@ -546,22 +546,18 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
       }
     }
   }
-  const bool misplaced = misplaced_wg(p.l2_local, p.lin);
+  const int rot = p.l2_local ? xcd_rotation(p.l2_local, p.lin) : 0;
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are performed
-  if (misplaced) {  // ... and written back from this L2
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __builtin_amdgcn_s_waitcnt(0);
-  }
   __syncthreads();                // ... and every other thread's
-  int32_t* counter = p.parts.counters + static_cast<int64_t>(tok0) * p.kv_heads + kvh;
+  arrival_t* counter = p.parts.counters + static_cast<int64_t>(tok0) * p.kv_heads + kvh;
   if (tid == 0) {
-    if (misplaced) __hip_atomic_fetch_add(p.parts.misplaced, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int seen = __hip_atomic_fetch_add(counter, misplaced ? 1 + kMisplacedArrival : 1, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-    // A merge off the planned XCD cannot see partials left in the planned
-    // XCD's L2: it poisons the tile's output instead of returning a wrong one.
-    const bool is_last = arrivals(seen) == it.part_stride - 1;
-    last = !is_last ? 0 : (misplaced && misplaced_arrivals(seen) < it.part_stride - 1 ? 2 : 1);
+    const arrival_t mine = arrival_token(rot);
+    const arrival_t seen = __hip_atomic_fetch_add(counter, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool is_last = arrival_count(seen) == it.part_stride - 1;
+    // partials left in another XCD's L2 are out of reach: poison the tile
+    const bool apart = is_last && p.l2_local && !arrivals_colocated(seen + mine, rot);
+    if (apart) __hip_atomic_fetch_add(p.parts.misplaced, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = !is_last ? 0 : (apart ? 2 : 1);
   }
   __syncthreads();
   if (!last) return;
@@ -584,7 +580,7 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
   } else {
     merge_tile<ACT, HD, 3>(p, it, acc_rsrc, ml, rec_tile, base, J, G, kvh, nq, tok0);
   }
-  if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) __hip_atomic_store(counter, arrival_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 }  // namespace
 }  // namespace chk

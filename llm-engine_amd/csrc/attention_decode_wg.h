@@ -282,22 +282,18 @@ __device__ __forceinline__ void arrive_and_merge(const DecodeParams& p, const Wo
   const int n4 = G * HD / 4;
   const int64_t head0 = static_cast<int64_t>(w.token) * p.q_heads + kvh * G;
   float* ml = reinterpret_cast<float*>(p.parts.ml);
-  const bool off = misplaced_wg(p.l2_local, p.lin);
+  const int rot = p.l2_local ? xcd_rotation(p.l2_local, p.lin) : 0;
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are performed
-  if (off) {  // ... and written back from this L2
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    __builtin_amdgcn_s_waitcnt(0);
-  }
   __syncthreads();                // ... and every other thread's
-  int32_t* counter = p.parts.counters + static_cast<int64_t>(w.token) * p.kv_heads + kvh;
+  arrival_t* counter = p.parts.counters + static_cast<int64_t>(w.token) * p.kv_heads + kvh;
   if (tid == 0) {
-    if (off) __hip_atomic_fetch_add(p.parts.misplaced, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int seen = __hip_atomic_fetch_add(counter, off ? 1 + kMisplacedArrival : 1, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-    // A merge off the planned XCD cannot see partials left in the planned
-    // XCD's L2: it poisons the output instead of returning a wrong one.
-    const bool last = arrivals(seen) == w.n_parts - 1;
-    *flag = !last ? 0 : (off && misplaced_arrivals(seen) < w.n_parts - 1 ? 2 : 1);
+    const arrival_t mine = arrival_token(rot);
+    const arrival_t seen = __hip_atomic_fetch_add(counter, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = arrival_count(seen) == w.n_parts - 1;
+    // partials left in another XCD's L2 are out of reach: poison the output
+    const bool apart = last && p.l2_local && !arrivals_colocated(seen + mine, rot);
+    if (apart) __hip_atomic_fetch_add(p.parts.misplaced, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag = !last ? 0 : (apart ? 2 : 1);
   }
   __syncthreads();
   if (!*flag) return;
@@ -316,7 +312,7 @@ __device__ __forceinline__ void arrive_and_merge(const DecodeParams& p, const Wo
   } else {
     merge_parts<ACT, HD, NTHR, kMergeBatch>(p, r, ml, rbase, np, n4, head0);
   }
-  if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) __hip_atomic_store(counter, arrival_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------

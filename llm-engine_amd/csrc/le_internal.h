@@ -13,9 +13,9 @@ namespace le {
 struct PartialLayout {
   float* acc;         // [n_parts][q_heads][head_dim]
   float2* ml;         // [n_parts][q_heads]  (m, l)
-  int32_t* counters;  // [n_rows][kv_heads] arrivals; zero between launches
-  // Device-wide count of split-row workgroups that ran off the XCD the plan
-  // placed them on (only touched when that happens; see xcd_misplacements).
+  unsigned long long* counters;  // [n_rows][kv_heads] arrivals; zero between launches
+  // Device-wide count of split-row merges that found their partitions on
+  // different XCDs (only touched when that happens; see xcd_misplacements).
   int32_t* misplaced;
 };
 
@@ -96,7 +96,7 @@ struct DecodeParams {
   // With items: every partition of a split row runs on one XCD (the plan's
   // placement, confirmed on this device by xcd_placement_holds), so partials
   // go through that XCD's L2 with plain stores. 0 off, 1 on,
-  // kL2LocalSimulateMisses: on, with fault injection (misplaced_wg).
+  // kL2LocalSimulateMisses: on, with fault injection (xcd_rotation).
   int l2_local;
   int lin;  // set by the kernel: the workgroup's linear id in its grid
 };
@@ -110,17 +110,18 @@ bool xcd_placement_holds(hipStream_t stream);
 // error), which launches with l2_local pass to their kernels.
 int32_t* xcd_miss_counter();
 
-// Reads and clears the current device's misplacement counter (synchronises
-// `stream`). A nonzero count turns the L2 exchange off for the device: from
-// then on split rows store write-through, as when the probe fails.
+// Reads and clears the current device's misplacement counter (split rows
+// whose partitions were found on different XCDs; synchronises `stream`). A
+// nonzero count turns the L2 exchange off for the device: from then on split
+// rows store write-through, as when the probe fails.
 hipError_t xcd_misplacements(hipStream_t stream, int64_t* count);
 
 // Forgets the current device's probe result: the next plan launch with split
 // rows probes the placement again.
 void xcd_placement_recheck();
 
-// l2_local value that makes the kernels treat every workgroup whose linear id
-// / 8 is odd as off its planned XCD (fault injection for the guard's tests).
+// l2_local value that makes every workgroup whose linear id / 8 is odd
+// report another XCD rotation (fault injection for the guard's tests).
 constexpr int kL2LocalSimulateMisses = 2;
 
 hipError_t attention_decode(const DecodeParams& p, int act_dtype, int kv_dtype, hipStream_t stream);

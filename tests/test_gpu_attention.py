@@ -235,7 +235,7 @@ def test_workspace_reused_across_plans(gpu):
             print(f"rep {rep} rows {plan.plan.n_tokens} parts {plan.plan.n_parts} "
                   f"chunk items {plan.plan.n_chunk_items}: max|err| {err:.3e}")
             assert within(out.float().cpu().numpy(), oracle_out(case, qh), tol_for(case, qh))
-    assert int(ws[:256 * 1024].count_nonzero().item()) == 0  # counters left at zero
+    assert int(ws[:512 * 1024].count_nonzero().item()) == 0  # counters left at zero
 
 
 @pytest.mark.parametrize("q_heads,kv_heads,head_dim", [(32, 4, 64), (8, 8, 64), (16, 2, 128), (4, 1, 128)])
