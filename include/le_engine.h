@@ -114,12 +114,6 @@ void le_model_destroy(le_model* m);
 int le_model_set_decode_graph(le_model* m, int enable);
 int64_t le_model_graph_replays(const le_model* m);
 
-/* bf16 models: projections of steps with at most 64 rows run on
- * le_weight_gemm (the gate|up projection fused with the SiLU product); larger
- * steps, unsupported shapes and fp32 models use rocBLAS. On by default;
- * enable = 0 sends every GEMM to rocBLAS (and the SiLU product to its own
- * kernel). */
-int le_model_set_weight_gemm(le_model* m, int enable);
 
 /* One step: slices in scheduler order. tokens_out receives the greedy token
  * of every slice with needs_logits (first maximum wins); logits_out, if not
@@ -135,23 +129,6 @@ int le_model_forward(le_model* m, const le_step_slice* slices, int n_slices, int
  * NaN is never chosen past element 0, and a row whose element 0 is NaN (or
  * with no greater value) gives 0. One launch for all rows. */
 int le_argmax_rows(const float* logits, int rows, int vocab, int32_t* out, hipStream_t stream);
-
-/* ---- decode-step projections (reference: the cuBLAS GEMMs of
- *      CudaModel::forward, cuda_model.cu:535-540) ----
- * out[m][n] = x[m][k] . w[n][k]^T: x and w bf16, row-major (w in nn.Linear
- * layout), fp32 accumulation, out bf16 or fp32. For the few rows of a decode
- * step: 1 <= m <= 64, k % 128 == 0, n % 64 == 0 (else LE_EUNSUPPORTED). The
- * weight bytes are the cost: each w row is read once, k split over
- * workgroups when n alone gives too few. silu = 1: w = [gate; up] (n rows,
- * n / 2 % 32 == 0) and out[m][n / 2] = silu(x . gate^T) * (x . up^T) (bf16;
- * both products rounded to bf16 first, as the unfused SiLU kernel reads
- * them). The workspace (le_weight_gemm_workspace_size bytes, 0 when no k
- * split is used) must be zero-filled once; every launch leaves it zeroed.
- * Split partials are summed in a fixed order: results do not depend on
- * timing. */
-size_t le_weight_gemm_workspace_size(int m, int k, int n, int silu);
-int le_weight_gemm(const void* x, int m, int k, const void* w, int n, int silu, void* out, le_dtype out_dtype,
-                   void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 /* ---- serving loop (reference: greedy_run, test_cuda_invariance.cpp:90-143,
  *      and Engine::run_loop, engine.cpp:246) ---- */

@@ -27,7 +27,6 @@
 #include "le_engine.h"
 #include "llm_engine_amd.h"
 #include "model_kernels.h"
-#include "weight_gemm.h"
 #include "scheduler.h"
 
 namespace le::engine {
@@ -130,7 +129,6 @@ class Model {
   ~Model();
   void forward(const le_step_slice* slices, int n_slices, int32_t* tokens_out, float* logits_out);
   void set_decode_graph(bool on) { graph_on_ = on; }
-  void set_weight_gemm(bool on) { weight_gemm_on_ = on; }
   int64_t graph_replays() const { return graph_replays_; }
   int num_blocks() const { return num_blocks_; }
   double plan_seconds() const { return plan_seconds_; }
@@ -141,12 +139,6 @@ class Model {
   void* upload_parts(const std::vector<std::pair<const float*, size_t>>& parts, bool as_bf16);
   float* upload_f32(const float* host, size_t n) { return static_cast<float*>(upload(host, n, false)); }
   void gemm(const void* A, const void* B, void* C, int m, int n, int k, bool c_f32 = false);
-  // act = silu(A . gate^T) * (A . up^T) with B = [gate; up] ([2 * I_][k]);
-  // gate_up is the scratch of the unfused form.
-  void gate_up_silu(const void* A, const void* B, void* gate_up, void* act, int m, int k);
-  bool use_weight_gemm(int m, int n, int k, bool silu) const {
-    return bf16_ && weight_gemm_on_ && weight_gemm_supported(m, k, n, silu);
-  }
   // The device work of a step on stream_, from the plan upload to the token
   // read-back into the pinned tokens buffer (nothing synchronises).
   void enqueue_step(le_step_plan& plan, const void* host_plan, float* logits_out);
@@ -179,11 +171,6 @@ class Model {
   };
   Generation gen_;
   bool graph_on_ = false, graph_failed_ = false;
-  // Decode-sized GEMMs (m <= 64, bf16) on the weight-streaming kernel; its
-  // workspace is sized at creation for the largest projection.
-  bool weight_gemm_on_ = true;
-  void* gemm_ws_ = nullptr;
-  size_t gemm_ws_bytes_ = 0;
   int64_t graph_replays_ = 0;
   std::map<int, DecodeGraph> graphs_;
 };
@@ -258,17 +245,6 @@ Model::Model(const le_model_desc& d, int num_blocks, int block_size) : d_(d) {
     kc_.push_back(k);
     vc_.push_back(v);
   }
-  if (bf16_) {
-    const int shapes[][3] = {{QD_ + 2 * KVD_, H_, 0}, {H_, QD_, 0}, {2 * I_, H_, 1}, {H_, I_, 0}, {V_, H_, 0}};
-    for (const auto& sh : shapes)
-      for (int m = 1; m <= kMaxGemmRows; m++)
-        gemm_ws_bytes_ = std::max(gemm_ws_bytes_, weight_gemm_workspace(m, sh[1], sh[0], sh[2] != 0, 0));
-    if (gemm_ws_bytes_) {
-      hip_ok(hipMalloc(&gemm_ws_, gemm_ws_bytes_), "hipMalloc gemm workspace");
-      owned_.push_back(gemm_ws_);
-      hip_ok(hipMemsetAsync(gemm_ws_, 0, gemm_ws_bytes_, stream_), "memset gemm workspace");
-    }
-  }
   hip_ok(hipStreamSynchronize(stream_), "sync");
 }
 
@@ -310,10 +286,6 @@ void* Model::upload_parts(const std::vector<std::pair<const float*, size_t>>& pa
 // C[m][n] = A[m][k] * B[n][k]^T in row-major terms. rocBLAS is column-major,
 // so it computes C^T = B * A^T: B with op T first, A with op N second.
 void Model::gemm(const void* A, const void* B, void* C, int m, int n, int k, bool c_f32) {
-  if (use_weight_gemm(m, n, k, false)) {
-    hip_ok(weight_gemm(A, m, k, B, n, false, C, c_f32, gemm_ws_, gemm_ws_bytes_, 0, stream_), "weight_gemm");
-    return;
-  }
   const float one = 1.f, zero = 0.f;
   if (!bf16_) {
     blas_ok(rocblas_sgemm(blas_, rocblas_operation_transpose, rocblas_operation_none, n, m, k, &one,
@@ -327,15 +299,6 @@ void Model::gemm(const void* A, const void* B, void* C, int m, int n, int k, boo
                           B, rocblas_datatype_bf16_r, k, A, rocblas_datatype_bf16_r, k, &zero, C, ct, n,
                           C, ct, n, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0),
           "rocblas_gemm_ex");
-}
-
-void Model::gate_up_silu(const void* A, const void* B, void* gate_up, void* act, int m, int k) {
-  if (use_weight_gemm(m, 2 * I_, k, true)) {
-    hip_ok(weight_gemm(A, m, k, B, 2 * I_, true, act, false, gemm_ws_, gemm_ws_bytes_, 0, stream_), "weight_gemm");
-    return;
-  }
-  gemm(A, B, gate_up, m, 2 * I_, k);
-  hip_ok(silu_mul_split(gate_up, act, m, I_, bf16_, stream_), "silu_mul");
 }
 
 void Model::forward(const le_step_slice* slices, int n_slices, int32_t* tokens_out, float* logits_out) {
@@ -478,7 +441,8 @@ void Model::enqueue_step(le_step_plan& plan, const void* host_plan, float* logit
     }
     gemm(attn, L.wo, o, N, H_, QD_);
     hip_ok(residual_rmsnorm(x, o, nullptr, L.post_norm, h, N, H_, d_.eps, true, bf16_, stream_), "residual");
-    gate_up_silu(h, L.wgate_up, gate_up, act, N, H_);
+    gemm(h, L.wgate_up, gate_up, N, 2 * I_, H_);
+    hip_ok(silu_mul_split(gate_up, act, N, I_, bf16_, stream_), "silu_mul");
     gemm(act, L.wdown, o, N, H_, I_);
     if (l + 1 < L_n)
       hip_ok(residual_rmsnorm(x, o, nullptr, layers_[l + 1].in_norm, h, N, H_, d_.eps, true, bf16_, stream_),
@@ -549,26 +513,6 @@ int le_model_set_decode_graph(le_model* m, int enable) {
 
 int64_t le_model_graph_replays(const le_model* m) { return m ? m->impl->graph_replays() : 0; }
 
-int le_model_set_weight_gemm(le_model* m, int enable) {
-  if (!m) return LE_EINVAL;
-  m->impl->set_weight_gemm(enable != 0);
-  return LE_OK;
-}
-
-size_t le_weight_gemm_workspace_size(int m, int k, int n, int silu) {
-  return le::engine::weight_gemm_workspace(m, k, n, silu != 0, 0);
-}
-
-int le_weight_gemm(const void* x, int m, int k, const void* w, int n, int silu, void* out, le_dtype out_dtype,
-                   void* workspace, size_t workspace_bytes, hipStream_t stream) {
-  if (!x || !w || !out || (out_dtype != LE_BF16 && out_dtype != LE_F32)) return LE_EINVAL;
-  if (!le::engine::weight_gemm_supported(m, k, n, silu != 0) || (silu && out_dtype != LE_BF16))
-    return LE_EUNSUPPORTED;
-  if (workspace_bytes < le::engine::weight_gemm_workspace(m, k, n, silu != 0, 0)) return LE_EINVAL;
-  const hipError_t e = le::engine::weight_gemm(x, m, k, w, n, silu != 0, out, out_dtype == LE_F32, workspace,
-                                               workspace_bytes, 0, stream);
-  return e == hipSuccess ? LE_OK : static_cast<int>(e);
-}
 
 int le_argmax_rows(const float* logits, int rows, int vocab, int32_t* out, hipStream_t stream) {
   if (rows < 0 || vocab <= 0) return LE_EINVAL;

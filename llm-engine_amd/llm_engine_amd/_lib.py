@@ -172,11 +172,6 @@ SIGNATURES = {
     "le_model_destroy": (None, [ctypes.c_void_p]),
     "le_model_set_decode_graph": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
     "le_model_graph_replays": (ctypes.c_int64, [ctypes.c_void_p]),
-    "le_model_set_weight_gemm": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
-    "le_weight_gemm_workspace_size": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
-    "le_weight_gemm": (ctypes.c_int, [
-        ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
-        ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "le_model_forward": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(StepSlice), ctypes.c_int,
                                         ctypes.c_void_p, ctypes.c_void_p]),
     "le_run_greedy": (ctypes.c_int, [

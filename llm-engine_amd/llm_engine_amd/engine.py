@@ -78,14 +78,11 @@ class Model:
     DTYPES = {"f32": LE_F32, "bf16": LE_BF16, "f16": LE_F16}
 
     def __init__(self, w: Weights, num_blocks: int, block_size: int = 16, dtype: str = "f32",
-                 kv_dtype: str | None = None, attention: str = "ragged", decode_graph: bool = False,
-                 weight_gemm: bool = True):
+                 kv_dtype: str | None = None, attention: str = "ragged", decode_graph: bool = False):
         """attention: "ragged" (le_ragged_paged_attention_qkv over the packed
         step) or "reference" (the reference-shaped le_attention_decode).
         decode_graph: replay decode steps from captured HIP graphs
-        (le_model_set_decode_graph). weight_gemm: bf16 steps of at most 64
-        rows project on le_weight_gemm (le_model_set_weight_gemm); False
-        sends every GEMM to rocBLAS."""
+        (le_model_set_decode_graph)."""
         a = w.arch
         self.arch = a
         self.num_blocks, self.block_size = num_blocks, block_size
@@ -114,8 +111,6 @@ class Model:
         self._keep = None  # weights are on the device now
         if decode_graph:
             check("le_model_set_decode_graph", _lib.load().le_model_set_decode_graph(self._h, 1))
-        if not weight_gemm:
-            check("le_model_set_weight_gemm", _lib.load().le_model_set_weight_gemm(self._h, 0))
 
     @property
     def graph_replays(self) -> int:

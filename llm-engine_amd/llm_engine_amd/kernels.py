@@ -106,29 +106,6 @@ def argmax_rows(logits: torch.Tensor, stream=None) -> torch.Tensor:
     return out
 
 
-def weight_gemm_workspace_size(m: int, k: int, n: int, silu: bool = False) -> int:
-    return int(_lib.load().le_weight_gemm_workspace_size(m, k, n, 1 if silu else 0))
-
-
-def weight_gemm(x: torch.Tensor, w: torch.Tensor, silu: bool = False, out_dtype=torch.bfloat16,
-                workspace: torch.Tensor | None = None, stream=None) -> torch.Tensor:
-    """x [m, k] . w[n, k]^T on le_weight_gemm (bf16 operands, m <= 64). silu:
-    w = [gate; up] and the result is silu(x . gate^T) * (x . up^T), [m, n/2]."""
-    _req(x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and x.is_cuda and w.is_cuda, "bf16 cuda x, w")
-    _req(x.dim() == 2 and w.dim() == 2 and x.shape[1] == w.shape[1] and x.is_contiguous() and w.is_contiguous(),
-         "x [m, k], w [n, k], contiguous")
-    m, k = x.shape
-    n = w.shape[0]
-    out = torch.empty(m, n // 2 if silu else n, dtype=out_dtype, device=x.device)
-    need = weight_gemm_workspace_size(m, k, n, silu)
-    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
-        workspace = torch.zeros(need, dtype=torch.uint8, device=x.device)
-    nbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
-    check("le_weight_gemm", _lib.load().le_weight_gemm(_p(x), m, k, _p(w), n, 1 if silu else 0, _p(out),
-                                                       _dt(out_dtype), _p(workspace), nbytes, _stream(stream)))
-    return out
-
-
 def new_workspace(nbytes: int, device="cuda") -> torch.Tensor:
     """A workspace for the attention calls: zero-filled once, as the ABI requires
     (the kernels leave its arrival counters at zero after every launch)."""
