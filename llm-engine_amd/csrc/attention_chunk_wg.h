@@ -37,9 +37,10 @@
 //     kp <= pos[t]; masked scores are -inf and the running max starts at
 //     -FLT_MAX, so fully masked tiles add zero;
 //   * a tile whose keys were split stores each partition's normalised output
-//     (fp32) and its fp32 (max, sum) with device-coherent
-//     stores; the last partition to arrive (atomic counter per tile and kv
-//     head, reset by it) merges them in partition order, inside the launch.
+//     (fp16 with a bf16 cache, fp32 otherwise) and its fp32 (max, sum) with
+//     device-coherent stores; the last partition to arrive (atomic counter
+//     per tile and kv head, reset by it) merges them in partition order,
+//     inside the launch.
 // 16-bit caches: 16-bit operands (q and P rounded to the cache type), fp32
 // accumulation. fp32 caches: the same tile on v_mfma_f32_16x16x4_f32 (exact
 // fp32 products), K/V staged 192 keys at a time.
@@ -111,7 +112,17 @@ template <typename KV, int HD> struct ChunkSmem {
 // folded in partition order into a running (max, sum) with rescaling. With at
 // most kMJ partitions the whole merge is one memory round trip, with no LDS
 // phase or barrier.
-template <typename ACT, int HD, int kMJ>
+// Split tiles of a bf16 cache carry their partials as fp16: the tile already
+// rounds its softmax weights to bf16 (2^-9), and a normalised partial is a
+// convex combination of V rows, so rounding it to fp16 moves the merged output
+// by at most 2^-11 max|V|; it halves the partial store and the merge's loads.
+// The price is the fp16 range, the reference's own cache range: a partial
+// element past 65504 (only possible with |V| > 65504 in the cache) becomes
+// inf, so the row's output comes back inf or NaN, never a wrong finite value.
+// fp16 and fp32 caches keep fp32 partials.
+template <typename KV> constexpr bool kHalfPartials = std::is_same_v<KV, bf16_t>;
+
+template <typename ACT, int HD, int kMJ, bool kHalf>
 __device__ __forceinline__ void merge_tile(const ChunkParams& p, const ChunkItem& it, __amdgpu_buffer_rsrc_t acc_rsrc,
                                            float* ml, int64_t rec_tile, int base, int J, int G, int kvh, int nq,
                                            int tok0) {
@@ -137,18 +148,34 @@ __device__ __forceinline__ void merge_tile(const ChunkParams& p, const ChunkItem
     }
     for (int j0 = 0; j0 < J; j0 += kMJ) {
       f32x4 x[kMG][kMJ][2];
+      uint4 xh[kMG][kMJ];
       float mj[kMG][kMJ], lj[kMG][kMJ];
 #pragma unroll
       for (int gi = 0; gi < kMG; gi++)
 #pragma unroll
         for (int jj = 0; jj < kMJ; jj++) {
           const int64_t rec = rec_base[gi] + static_cast<int64_t>(min(j0 + jj, J - 1)) * p.q_heads;
-          const uint32_t off = static_cast<uint32_t>(((rec - rec_tile) * HD + d8[gi] * 8) * 4);
-          x[gi][jj][0] = ld_coherent16(acc_rsrc, off);
-          x[gi][jj][1] = ld_coherent16(acc_rsrc, off + 16);
+          if constexpr (kHalf) {
+            xh[gi][jj] = ld_coherent16u(acc_rsrc, static_cast<uint32_t>(((rec - rec_tile) * HD + d8[gi] * 8) * 2));
+          } else {
+            const uint32_t off = static_cast<uint32_t>(((rec - rec_tile) * HD + d8[gi] * 8) * 4);
+            x[gi][jj][0] = ld_coherent16(acc_rsrc, off);
+            x[gi][jj][1] = ld_coherent16(acc_rsrc, off + 16);
+          }
           mj[gi][jj] = ld_dev(ml + rec * 2);
           lj[gi][jj] = ld_dev(ml + rec * 2 + 1);
         }
+      if constexpr (kHalf) {
+#pragma unroll
+        for (int gi = 0; gi < kMG; gi++)
+#pragma unroll
+          for (int jj = 0; jj < kMJ; jj++) {
+            float f[8];
+            elem<f16_t>::widen(xh[gi][jj], f);
+            x[gi][jj][0] = f32x4{f[0], f[1], f[2], f[3]};
+            x[gi][jj][1] = f32x4{f[4], f[5], f[6], f[7]};
+          }
+      }
 #pragma unroll
       for (int gi = 0; gi < kMG; gi++)
 #pragma unroll
@@ -523,17 +550,25 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
       const int r = rs * 16 + col;
       if (r < nq) {
         const int64_t rec = static_cast<int64_t>(it.part0 + r * it.part_stride) * p.q_heads + head;
-        // the partition's normalised output, fp32, in the record's natural
+        // the partition's normalised output (fp16 or fp32), in the record's natural
         // layout (a row with no live key in the partition stores zeros and
         // l = 0): lane (col, grp) holds dims d*16 + grp*4 .. +4 of each
         // output tile d
         const float inv = l_tot[rs] > 0.f ? 1.f / l_tot[rs] : 0.f;
 #pragma unroll
         for (int d = 0; d < DT; d++) {
-          const uint32_t off = static_cast<uint32_t>(((rec - rec_tile) * HD + d * 16 + grp * 4) * 4);
-          const f32x4v v = __builtin_bit_cast(f32x4v, acc[rs][d] * inv);
-          if (p.l2_local) st_l2_16(acc_rsrc, off, v);
-          else st_coherent16(acc_rsrc, off, v);
+          const f32x4 o = acc[rs][d] * inv;
+          if constexpr (kHalfPartials<KV>) {
+            const uint32_t off = static_cast<uint32_t>(((rec - rec_tile) * HD + d * 16 + grp * 4) * 2);
+            const uint2 v = make_uint2(pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3]));
+            if (p.l2_local) st_l2_8(acc_rsrc, off, v);
+            else st_coherent8(acc_rsrc, off, v);
+          } else {
+            const uint32_t off = static_cast<uint32_t>(((rec - rec_tile) * HD + d * 16 + grp * 4) * 4);
+            const f32x4v v = __builtin_bit_cast(f32x4v, o);
+            if (p.l2_local) st_l2_16(acc_rsrc, off, v);
+            else st_coherent16(acc_rsrc, off, v);
+          }
         }
         if (grp == 0) {
           if (p.l2_local) {
@@ -575,10 +610,10 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
                         __builtin_nanf(""));
     }
   } else if constexpr (HD == 64) {
-    if (J <= 4) merge_tile<ACT, HD, 4>(p, it, acc_rsrc, ml, rec_tile, base, J, G, kvh, nq, tok0);
-    else merge_tile<ACT, HD, 6>(p, it, acc_rsrc, ml, rec_tile, base, J, G, kvh, nq, tok0);
+    if (J <= 4) merge_tile<ACT, HD, 4, kHalfPartials<KV>>(p, it, acc_rsrc, ml, rec_tile, base, J, G, kvh, nq, tok0);
+    else merge_tile<ACT, HD, 6, kHalfPartials<KV>>(p, it, acc_rsrc, ml, rec_tile, base, J, G, kvh, nq, tok0);
   } else {
-    merge_tile<ACT, HD, 3>(p, it, acc_rsrc, ml, rec_tile, base, J, G, kvh, nq, tok0);
+    merge_tile<ACT, HD, 3, kHalfPartials<KV>>(p, it, acc_rsrc, ml, rec_tile, base, J, G, kvh, nq, tok0);
   }
   if (tid == 0) __hip_atomic_store(counter, arrival_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

@@ -93,4 +93,14 @@ def emulated_bar(case: AttnCase, q_f32: np.ndarray, want: np.ndarray | None = No
     if want is None:
         want = oracle_out(case, q_f32)
     chunk = np.array([case.seq_qlen[s] > 1 for s in case.token_seq])
-    return factor * float(np.abs(emulate(case, q_f32, dt, chunk) - want).max())
+    bar = factor * float(np.abs(emulate(case, q_f32, dt, chunk) - want).max())
+    if dt == "bf16" and chunk.any():
+        # split chunk tiles of a bf16 cache carry normalised partials as fp16:
+        # each is a convex combination of V rows, rounded with relative error
+        # <= 2^-11, and the merge is a convex combination of them
+        bar += 2.0 ** -11 * float(np.abs(_widen_cache(case.v_cache)).max())
+    return bar
+
+
+def _widen_cache(c: np.ndarray) -> np.ndarray:
+    return oracle.bf16_to_f32(c) if c.dtype == np.uint16 else c.astype(np.float32)

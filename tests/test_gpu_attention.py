@@ -208,6 +208,33 @@ def test_mixed_step_two_launches(gpu):
         assert within(got, want, tol_for(case, qh))
 
 
+def test_split_chunk_partials_beyond_fp16_range(gpu):
+    """Split chunk tiles of a bf16 cache carry fp16 partials, so the fp16
+    range (the reference's own cache range) bounds them. With V scaled by
+    2^20 (exact in bf16, |V| far past 65504), every output element must be
+    either within the bar or not finite: an overflow is loud, never a wrong
+    finite value. Rows whose partials stayed in range (decode rows, unsplit
+    tiles) stay exact to the bar."""
+    import dataclasses
+    import oracle
+    ctx = [900, 700, 1500, 300]
+    q_len = [300, 1, 200, 1]
+    base = make_case(ctx, q_len=q_len, num_blocks=1024, seed=83, kv_bf16=True)
+    v = oracle.bf16_to_f32(base.v_cache) * np.float32(2.0 ** 20)
+    case = dataclasses.replace(base, v_cache=oracle.f32_to_bf16(v))
+    got, qh, plan = run_ragged(case, torch.float32, gpu, partition_tokens=256, chunk_partition_tokens=256)
+    assert plan.plan.n_chunk_items > 0 and plan.plan.n_parts > 0
+    want = oracle_out(case, qh)
+    tol = tol_for(case, qh)
+    ok = np.abs(got.astype(np.float64) - want) <= tol
+    loud = ~np.isfinite(got)
+    print(f"|V| up to {np.abs(v).max():.3g}: {int(loud.sum())} of {got.size} outputs not finite")
+    assert bool(np.all(ok | loud))
+    assert loud.any()  # the split tiles' partials did overflow
+    decode = np.repeat(np.array([case.seq_qlen[s] == 1 for s in case.token_seq]), 1)
+    assert bool(np.all(ok[decode]))
+
+
 def test_workspace_reused_across_plans(gpu):
     """One workspace serves steps of different shapes (as the engine uses it):
     a step with few rows and many split partials, then a larger mixed step
