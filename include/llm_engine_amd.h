@@ -159,7 +159,7 @@ typedef struct le_plan_config {
                                   sequence's table gets table_capacity entries, every row
                                   partition_tokens-sized partitions (partition_tokens must be
                                   given), and the work lists, partials and every array offset
-                                  depend only on the row count (le_plan_fixed_key) */
+                                  depend only on the row count */
 } le_plan_config;
 
 /* le_plan_config.flags. The first two select slower, equivalent launches;
