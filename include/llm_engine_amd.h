@@ -170,7 +170,7 @@ typedef struct le_plan_config {
                                    launches instead of one */
 #define LE_PLAN_SIMULATE_MISPLACEMENT 4 /* fault injection for tests of the placement
                                    guard (le_xcd_misplacements): workgroups whose linear
-                                   id / 8 is odd report another XCD */
+                                   bits 3 and 4 differ report another XCD */
 
 typedef struct le_step_plan {
   le_plan_config cfg;

@@ -235,13 +235,13 @@ __device__ __forceinline__ void st_coherent16(__amdgpu_buffer_rsrc_t r, uint32_t
 // arrive merges only if every arrival had its own rotation; otherwise some
 // partial sits in another XCD's L2, and it writes NaN instead of a wrong
 // result (and counts the event). l2_local: 0 off (write-through partials, no
-// check), 1 on, 2 on with fault injection (workgroups with an odd lin / 8
+// check), 1 on, 2 on with fault injection (workgroups whose lin bits 3 and 4 differ
 // report another rotation).
 __device__ __forceinline__ int xcd_rotation(int l2_local, int lin) {
   unsigned v;
   asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
   int rot = (static_cast<int>(v & 7) - lin) & 7;
-  if (l2_local == 2 && ((lin / 8) & 1)) rot ^= 1;
+  if (l2_local == 2 && (((lin >> 3) ^ (lin >> 4)) & 1)) rot ^= 1;
   return rot;
 }
 // 64-bit arrival counters: the number of arrivals in bits 0..10, the sum of

@@ -120,7 +120,7 @@ hipError_t xcd_misplacements(hipStream_t stream, int64_t* count);
 // rows probes the placement again.
 void xcd_placement_recheck();
 
-// l2_local value that makes every workgroup whose linear id / 8 is odd
+// l2_local value that makes every workgroup whose bits 3 and 4 of the linear id differ
 // report another XCD rotation (fault injection for the guard's tests).
 constexpr int kL2LocalSimulateMisses = 2;
 

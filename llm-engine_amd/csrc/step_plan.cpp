@@ -81,7 +81,11 @@ std::vector<Item> place_on_xcds(const std::vector<Item>& items, Same same_group,
     groups.push_back(g);
     i = j;
   }
-  std::stable_sort(groups.begin(), groups.end(), [](const Group& a, const Group& b) { return a.longest > b.longest; });
+  // longest first; among equally long, the groups with more partitions (the
+  // longer merge) first: low ids are dispatched first
+  std::stable_sort(groups.begin(), groups.end(), [](const Group& a, const Group& b) {
+    return a.longest != b.longest ? a.longest > b.longest : a.n > b.n;
+  });
   std::vector<std::vector<Item>> bins(kXcds);
   int64_t load[kXcds] = {};
   for (const Group& g : groups) {

@@ -5,7 +5,7 @@ on the assumption that workgroups whose ids are equal modulo 8 share an XCD.
 Each partition reports its XCD when it arrives, and a merge whose partitions
 were spread over XCDs writes NaN instead of a wrong value. The
 LE_PLAN_SIMULATE_MISPLACEMENT flag forces the condition from the host (the
-kernels make every workgroup whose linear id / 8 is odd report another XCD),
+kernels make every workgroup whose bits 3 and 4 of the linear id differ report another XCD),
 so the guard's paths run while every kernel still exits normally."""
 import numpy as np
 import pytest
