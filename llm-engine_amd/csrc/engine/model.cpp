@@ -24,6 +24,7 @@
 #include <thread>
 #include <vector>
 
+#include "../le_internal.h"
 #include "le_engine.h"
 #include "llm_engine_amd.h"
 #include "model_kernels.h"
@@ -129,6 +130,8 @@ class Model {
   ~Model();
   void forward(const le_step_slice* slices, int n_slices, int32_t* tokens_out, float* logits_out);
   void set_decode_graph(bool on) { graph_on_ = on; }
+  void set_plan_flags(int flags) { plan_flags_ = flags; graphs_clear(); }
+  int64_t placement_reruns() const { return placement_reruns_; }
   int64_t graph_replays() const { return graph_replays_; }
   int num_blocks() const { return num_blocks_; }
   double plan_seconds() const { return plan_seconds_; }
@@ -143,6 +146,14 @@ class Model {
   // read-back into the pinned tokens buffer (nothing synchronises).
   void enqueue_step(le_step_plan& plan, const void* host_plan, float* logits_out);
   bool forward_graph(const le_step_slice* slices, int n_slices, int32_t* tokens_out);
+  // After a step's sync: true if some split row's partitions were found on
+  // different XCDs during the step (the misplacement counter, copied back
+  // with the tokens, is nonzero). Such a merge wrote NaN instead of its
+  // output, so the caller runs the step again: the counter is read and
+  // cleared, which switches the device to write-through partials, and the
+  // captured graphs (which hold the L2 exchange) are dropped.
+  bool step_poisoned();
+  void graphs_clear();
 
   le_model_desc d_;
   bool bf16_;
@@ -160,7 +171,10 @@ class Model {
   std::vector<Layer> layers_;
   std::vector<void*> kc_, vc_;
   DevBuf x_, h_, qkv_, q_, attn_, o_, gate_up_, act_buf_, logits_, tokens_, plan_dev_, ws_;
-  HostBuf plan_host_, tokens_host_;
+  HostBuf plan_host_, tokens_host_, miss_host_;
+  int32_t* miss_dev_ = nullptr;  // the device's misplacement counter (static device array)
+  int plan_flags_ = 0;
+  int64_t placement_reruns_ = 0;
   // Decode graphs: per row count, the whole decode step captured once (after
   // one eager run of the same layout) and replayed while the buffers stay.
   struct DecodeGraph {
@@ -196,7 +210,7 @@ Model::Model(const le_model_desc& d, int num_blocks, int block_size) : d_(d) {
   if (nh_ % nkv_ != 0 || hd_ % 2 != 0) throw std::invalid_argument("head layout");
   for (DevBuf* b : {&x_, &h_, &qkv_, &q_, &attn_, &o_, &gate_up_, &act_buf_, &logits_, &tokens_, &plan_dev_, &ws_})
     b->gen = &gen_;
-  for (HostBuf* b : {&plan_host_, &tokens_host_}) b->gen = &gen_;
+  for (HostBuf* b : {&plan_host_, &tokens_host_, &miss_host_}) b->gen = &gen_;
   hip_ok(hipStreamCreate(&stream_), "hipStreamCreate");
   blas_ok(rocblas_create_handle(&blas_), "rocblas_create_handle");
   blas_ok(rocblas_set_stream(blas_, stream_), "rocblas_set_stream");
@@ -245,13 +259,30 @@ Model::Model(const le_model_desc& d, int num_blocks, int block_size) : d_(d) {
     kc_.push_back(k);
     vc_.push_back(v);
   }
+  miss_dev_ = le::xcd_miss_counter();
+  if (miss_dev_) *static_cast<int32_t*>(miss_host_.get(4)) = 0;
   hip_ok(hipStreamSynchronize(stream_), "sync");
+}
+
+void Model::graphs_clear() {
+  for (auto& [n, g] : graphs_)
+    if (g.exec) (void)hipGraphExecDestroy(g.exec);
+  graphs_.clear();
+}
+
+bool Model::step_poisoned() {
+  if (!miss_dev_ || *static_cast<const int32_t*>(miss_host_.p) == 0) return false;
+  int64_t n = 0;
+  hip_ok(le::xcd_misplacements(stream_, &n), "xcd_misplacements");
+  *static_cast<int32_t*>(miss_host_.p) = 0;
+  graphs_clear();
+  placement_reruns_++;
+  return true;
 }
 
 Model::~Model() {
   (void)hipStreamSynchronize(stream_);
-  for (auto& [n, g] : graphs_)
-    if (g.exec) (void)hipGraphExecDestroy(g.exec);
+  graphs_clear();
   for (void* p : owned_) (void)hipFree(p);
   if (blas_) rocblas_destroy_handle(blas_);
   if (stream_) (void)hipStreamDestroy(stream_);
@@ -304,7 +335,7 @@ void Model::gemm(const void* A, const void* B, void* C, int m, int n, int k, boo
 void Model::forward(const le_step_slice* slices, int n_slices, int32_t* tokens_out, float* logits_out) {
   if (graph_on_ && !graph_failed_ && !logits_out && forward_graph(slices, n_slices, tokens_out)) return;
   const auto t_plan = std::chrono::steady_clock::now();
-  le_plan_config cfg{nh_, nkv_, hd_, bs_, kv_dt_, 0, 0, 0, 0, 0};
+  le_plan_config cfg{nh_, nkv_, hd_, bs_, kv_dt_, 0, 0, 0, plan_flags_, 0};
   le_step_plan plan{};
   int st = le_plan_step(slices, n_slices, &cfg, nullptr, 0, &plan);
   if (st != LE_ENOSPACE) le_ok(st, "le_plan_step");
@@ -314,6 +345,10 @@ void Model::forward(const le_step_slice* slices, int n_slices, int32_t* tokens_o
   if (plan.n_tokens == 0) return;
   enqueue_step(plan, host, logits_out);
   hip_ok(hipStreamSynchronize(stream_), "step sync");
+  if (step_poisoned()) {  // once: the device now stores partials write-through
+    enqueue_step(plan, host, logits_out);
+    hip_ok(hipStreamSynchronize(stream_), "step sync");
+  }
   if (tokens_out && plan.n_logits > 0)
     std::memcpy(tokens_out, tokens_host_.p, static_cast<size_t>(plan.n_logits) * 4);
 }
@@ -333,7 +368,7 @@ bool Model::forward_graph(const le_step_slice* slices, int n_slices, int32_t* to
     if (slices[i].len != 1 || !slices[i].needs_logits) return false;
   const auto t_plan = std::chrono::steady_clock::now();
   const int cap_blocks = (d_.max_pos + bs_ - 1) / bs_;
-  le_plan_config cfg{nh_, nkv_, hd_, bs_, kv_dt_, kGraphPartition, 0, 0, 0, cap_blocks};
+  le_plan_config cfg{nh_, nkv_, hd_, bs_, kv_dt_, kGraphPartition, 0, 0, plan_flags_, cap_blocks};
   le_step_plan plan{};
   int st = le_plan_step(slices, n_slices, &cfg, nullptr, 0, &plan);
   if (st != LE_ENOSPACE) return false;  // e.g. a table longer than max_pos allows: run eagerly
@@ -346,8 +381,13 @@ bool Model::forward_graph(const le_step_slice* slices, int n_slices, int32_t* to
     g = DecodeGraph{};
     enqueue_step(plan, host, nullptr);
     hip_ok(hipStreamSynchronize(stream_), "step sync");
-    g.warm = true;
-    g.plan_bytes = plan.bytes;
+    if (step_poisoned()) {
+      enqueue_step(plan, host, nullptr);
+      hip_ok(hipStreamSynchronize(stream_), "step sync");
+    }
+    DecodeGraph& g2 = graphs_[n_slices];  // step_poisoned may have cleared the map
+    g2.warm = true;
+    g2.plan_bytes = plan.bytes;
   } else {
     if (!g.exec || g.gen != gen_.value) {
       if (g.exec) (void)hipGraphExecDestroy(g.exec);
@@ -372,6 +412,10 @@ bool Model::forward_graph(const le_step_slice* slices, int n_slices, int32_t* to
         (void)hipGetLastError();
         enqueue_step(plan, host, nullptr);
         hip_ok(hipStreamSynchronize(stream_), "step sync");
+        if (step_poisoned()) {
+          enqueue_step(plan, host, nullptr);
+          hip_ok(hipStreamSynchronize(stream_), "step sync");
+        }
         if (tokens_out) std::memcpy(tokens_out, tokens_host_.p, static_cast<size_t>(n_slices) * 4);
         return true;
       }
@@ -380,6 +424,10 @@ bool Model::forward_graph(const le_step_slice* slices, int n_slices, int32_t* to
     hip_ok(hipGraphLaunch(g.exec, stream_), "hipGraphLaunch");
     hip_ok(hipStreamSynchronize(stream_), "step sync");
     graph_replays_++;
+    if (step_poisoned()) {  // the graphs are gone: run this step eagerly
+      enqueue_step(plan, host, nullptr);
+      hip_ok(hipStreamSynchronize(stream_), "step sync");
+    }
   }
   if (tokens_out) std::memcpy(tokens_out, tokens_host_.p, static_cast<size_t>(n_slices) * 4);
   return true;
@@ -462,6 +510,9 @@ void Model::enqueue_step(le_step_plan& plan, const void* host_plan, float* logit
       hip_ok(hipMemcpyAsync(logits_out, logits, static_cast<size_t>(R) * V_ * 4, hipMemcpyDeviceToHost,
                             stream_), "logits");
   }
+  // every step, sampled or not: a poisoned merge also poisons the K/V that
+  // later layers wrote
+  if (miss_dev_) hip_ok(hipMemcpyAsync(miss_host_.p, miss_dev_, 4, hipMemcpyDeviceToHost, stream_), "misplacements");
 }
 
 
@@ -512,6 +563,15 @@ int le_model_set_decode_graph(le_model* m, int enable) {
 }
 
 int64_t le_model_graph_replays(const le_model* m) { return m ? m->impl->graph_replays() : 0; }
+
+int le_model_set_plan_flags(le_model* m, int32_t flags) {
+  if (!m) return LE_EINVAL;
+  if ((flags & ~(LE_PLAN_WRITE_THROUGH | LE_PLAN_TWO_LAUNCHES | LE_PLAN_SIMULATE_MISPLACEMENT)) != 0) return LE_EINVAL;
+  m->impl->set_plan_flags(flags);
+  return LE_OK;
+}
+
+int64_t le_model_placement_reruns(const le_model* m) { return m ? m->impl->placement_reruns() : 0; }
 
 
 int le_argmax_rows(const float* logits, int rows, int vocab, int32_t* out, hipStream_t stream) {

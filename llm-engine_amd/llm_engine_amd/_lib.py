@@ -172,6 +172,8 @@ SIGNATURES = {
     "le_model_destroy": (None, [ctypes.c_void_p]),
     "le_model_set_decode_graph": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
     "le_model_graph_replays": (ctypes.c_int64, [ctypes.c_void_p]),
+    "le_model_set_plan_flags": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32]),
+    "le_model_placement_reruns": (ctypes.c_int64, [ctypes.c_void_p]),
     "le_model_forward": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(StepSlice), ctypes.c_int,
                                         ctypes.c_void_p, ctypes.c_void_p]),
     "le_run_greedy": (ctypes.c_int, [

@@ -116,6 +116,15 @@ class Model:
     def graph_replays(self) -> int:
         return int(_lib.load().le_model_graph_replays(self._h))
 
+    def set_plan_flags(self, flags: int) -> None:
+        """le_plan_config.flags for the model's plans (le_model_set_plan_flags)."""
+        check("le_model_set_plan_flags", _lib.load().le_model_set_plan_flags(self._h, int(flags)))
+
+    @property
+    def placement_reruns(self) -> int:
+        """Steps run again because a split row's partitions were spread over XCDs."""
+        return int(_lib.load().le_model_placement_reruns(self._h))
+
     def close(self):
         if getattr(self, "_h", None):
             _lib.load().le_model_destroy(self._h)

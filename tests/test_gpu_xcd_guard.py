@@ -70,3 +70,38 @@ def test_misplaced_partials_are_correct_or_nan(gpu):
     kernels.xcd_placement_recheck()
     assert np.array_equal(run(0), ref)
     assert kernels.xcd_misplacements() == 0
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_engine_reruns_a_poisoned_step(gpu, graph):
+    """The device model copies the misplacement counter back with every step;
+    a step whose merges were poisoned runs again (on write-through partials)
+    before its tokens are used. With the fault injection on from the first
+    step, config 1 must still give the fixture's tokens, after at least one
+    re-run."""
+    import json
+    import sys
+    from pathlib import Path
+    from llm_engine_amd import kernels
+    from llm_engine_amd.engine import Model, sched_config, synthetic_weights
+    gold = Path(__file__).resolve().parent / "golden"
+    sys.path.insert(0, str(gold))
+    from make_config1 import weight_digest
+    fx = json.loads((gold / "config1_tokens.json").read_text())
+    w = synthetic_weights(fx["arch"], fx["weight_seed"])
+    assert weight_digest(w) == fx["weight_digest"]
+    kernels.xcd_placement_recheck()
+    kernels.xcd_misplacements()
+    m = Model(w, fx["num_blocks"], 16, dtype="f32", decode_graph=graph)
+    m.set_plan_flags(LE_PLAN_SIMULATE_MISPLACEMENT)
+    toks, _ = m.run_greedy(fx["prompts"], [fx["gen"]] * len(fx["prompts"]),
+                           sched_config(max_num_batched_tokens=fx["max_num_batched_tokens"]),
+                           fragment_blocks=fx["fragment_blocks"])
+    reruns = m.placement_reruns
+    m.close()
+    kernels.xcd_placement_recheck()  # the re-run switched the device to write-through
+    print(f"graph {graph}: {reruns} re-run step(s)")
+    if reruns == 0:
+        pytest.skip("no split row in this run took the L2 exchange (device not on the L2 path)")
+    assert reruns >= 1
+    assert toks == fx["tokens"]
