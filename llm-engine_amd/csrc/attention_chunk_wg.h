@@ -326,7 +326,7 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
         elem<float>::widen(qraw[rs][u][1], f + 4);
       }
 #pragma unroll
-      for (int e = 0; e < 8; e++) qf[rs][u * 8 + e] = ok ? f[e] : 0.f;
+      for (int e = 0; e < 8; e++) qf[rs][u * 8 + e] = ok ? f[e] * p.scale_log2 : 0.f;
     }
   }
   // 16-bit path: Q^T operands, this lane's 8 dims per k-step of rows col and 16 + col
@@ -346,6 +346,13 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
 #pragma unroll
     for (int d = 0; d < DT; d++) acc[rs][d] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run[2] = {-FLT_MAX, -FLT_MAX};
+  // The S^T accumulators start at -sbase (per row): scores come out of the
+  // MFMA as s - sbase, already in log2 units (q carries scale * log2(e)).
+  // sbase is the running max once the row has a live key (0 before), so on
+  // tiles that do not move the max, p = exp2(s - sbase) with no vector-ALU
+  // work before the exp2.
+  float sbase[2] = {0.f, 0.f};
+  f32x4 nbase[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};  // -sbase, the MFMA's C operand
   // 16-bit path: lsum[rs][0] of the lanes of group 0 = the row's sum of p
   // (row col), summed on the MFMA; the other entries stay zero. fp32 path:
   // lsum[rs][0] of every lane = its share of the row's sum (the keys of its
@@ -361,18 +368,15 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
     const int s0 = key_begin + rel0;
     if (computes) {
       const int key_end = min(key_begin + n_keys_blk, pos0 + nq);  // past the last row's position: dead
-#pragma unroll 1
-      for (int kt = 0; kt < kStageKeys<KV, HD> / kTileKeys; kt++) {
-        const int t0 = s0 + kt * kTileKeys;
-        if (t0 >= key_end) break;
+      // Tiles of the stage with a live key.
+      const int nt = min(kStageKeys<KV, HD> / kTileKeys, (key_end - s0 + kTileKeys - 1) / kTileKeys);
+      // ---- S^T of tile kt: 64 keys x 32 rows, less the rows' current base ----
+      auto scores = [&](int kt, f32x4 (&s)[2][4]) {
         const char* kt_lds = lds + kt * kTileKeys * L::ROW;
-        const char* vt_lds = lds + L::K_BYTES + kt * kTileKeys * L::ROW;
-        // ---- S^T: 64 keys x 32 rows ----
-        f32x4 s[2][4];
 #pragma unroll
         for (int rs = 0; rs < 2; rs++)
 #pragma unroll
-          for (int i = 0; i < 4; i++) s[rs][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+          for (int i = 0; i < 4; i++) s[rs][i] = nbase[rs];
         if constexpr (!kF32) {
 #pragma unroll
           for (int i = 0; i < 4; i++)
@@ -400,55 +404,64 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
                 s[rs][i] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[j], qf[rs][j], s[rs][i], 0, 0, 0);
           }
         }
+      };
+      auto soft_pv = [&](int kt, f32x4 (&s)[2][4]) {
+        const int t0 = s0 + kt * kTileKeys;
+        const char* vt_lds = lds + L::K_BYTES + kt * kTileKeys * L::ROW;
         // ---- causal mask, online softmax per row (log2 domain) ----
         // A tile wholly below the diagonal and inside the range needs no
-        // mask: every row's position is at least pos0. The max runs on raw
-        // scores (the scale is positive) and the scale enters once, in
-        // exp2(s * scale - m). Arguments of exp2 are <= 0, so the raw
-        // hardware exp2 (whose results below 2^-126 flush to zero) suffices.
+        // mask: every row's position is at least pos0. Arguments of exp2 are
+        // at most kRescaleSlack, so the raw hardware exp2 (whose results
+        // below 2^-126 flush to zero) suffices.
         const bool full = t0 + kTileKeys - 1 <= pos0 && t0 + kTileKeys <= key_end;
 #pragma unroll
         for (int rs = 0; rs < 2; rs++) {
           if (!full) {
+            // key t0 + 16i + 4grp + j is live iff 16i + j <= lim: one
+            // per-lane limit against compile-time offsets
             const int r = rs * 16 + col;
             const int qpos = r < nq ? pos0 + r : -1;
+            const int lim = min(qpos, key_end - 1) - t0 - grp * 4;
 #pragma unroll
             for (int i = 0; i < 4; i++)
 #pragma unroll
-              for (int j = 0; j < 4; j++) {
-                const int kp = t0 + i * 16 + grp * 4 + j;
-                if (!(kp <= qpos && kp < key_end)) s[rs][i][j] = -INFINITY;
-              }
+              for (int j = 0; j < 4; j++)
+                if (i * 16 + j > lim) s[rs][i][j] = -INFINITY;
           }
-          float mt = vmax3(s[rs][0][0], s[rs][0][1], s[rs][0][2]);
-          mt = vmax3(mt, s[rs][0][3], s[rs][1][0]);
-          mt = vmax3(mt, s[rs][1][1], s[rs][1][2]);
-          mt = vmax3(mt, s[rs][1][3], s[rs][2][0]);
-          mt = vmax3(mt, s[rs][2][1], s[rs][2][2]);
-          mt = vmax3(mt, s[rs][2][3], s[rs][3][0]);
-          mt = vmax3(mt, s[rs][3][1], s[rs][3][2]);
-          mt = fmaxf(mt, s[rs][3][3]);
-          mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
-          mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+          // a tree of v_max3 (depth 3) over the lane's 16 scores
+          const float m0 = vmax3(s[rs][0][0], s[rs][0][1], s[rs][0][2]);
+          const float m1 = vmax3(s[rs][0][3], s[rs][1][0], s[rs][1][1]);
+          const float m2 = vmax3(s[rs][1][2], s[rs][1][3], s[rs][2][0]);
+          const float m3 = vmax3(s[rs][2][1], s[rs][2][2], s[rs][2][3]);
+          const float m4 = vmax3(s[rs][3][0], s[rs][3][1], s[rs][3][2]);
+          float mt = vmax2(vmax3(m0, m1, m2), vmax3(m3, m4, s[rs][3][3]));
+          mt = rows_max(mt);
           // The running max moves only when the tile's max passes it by more
           // than kRescaleSlack (log2 units): probabilities then stay below
-          // 2^kRescaleSlack, and the accumulators are rescaled only on the
-          // tiles where some row of the wave moved its max.
-          const float cand = mt * p.scale_log2;
+          // 2^kRescaleSlack, and the accumulators are rescaled and the
+          // scores shifted to the new base only on the tiles where some row
+          // of the wave moved its max (always on a row's first live tile).
+          // A row that does not move keeps sbase == m_run, or has only
+          // masked (-inf) scores so far.
+          const float cand = mt + sbase[rs];
           const bool grow = cand > m_run[rs] + kRescaleSlack;
           if (__builtin_amdgcn_ballot_w64(grow)) {
             const float m_new = grow ? cand : m_run[rs];
             const float alpha = __builtin_amdgcn_exp2f(m_run[rs] - m_new);
+            const float shift = grow ? m_new - sbase[rs] : 0.f;
             m_run[rs] = m_new;
+            sbase[rs] = grow ? m_new : sbase[rs];
+            nbase[rs] = f32x4{-sbase[rs], -sbase[rs], -sbase[rs], -sbase[rs]};
 #pragma unroll
             for (int d = 0; d < DT; d++) acc[rs][d] *= alpha;
             lsum[rs] *= alpha;
+#pragma unroll
+            for (int i = 0; i < 4; i++) s[rs][i] -= shift;
           }
 #pragma unroll
           for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-              s[rs][i][j] = __builtin_amdgcn_exp2f(fmaf(s[rs][i][j], p.scale_log2, -m_run[rs]));
+            for (int j = 0; j < 4; j++) s[rs][i][j] = __builtin_amdgcn_exp2f(s[rs][i][j]);
         }
         if constexpr (!kF32) {
           // ---- O^T += V^T . P^T over the tile's 64 keys (2 k-steps of 32) ----
@@ -506,6 +519,12 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
             lsum[rs][0] += ls;
           }
         }
+      };
+#pragma unroll 1
+      for (int kt = 0; kt < nt; kt++) {
+        f32x4 sa[2][4];
+        scores(kt, sa);
+        soft_pv(kt, sa);
       }
     }
     rel0 += kStageKeys<KV, HD>;
@@ -518,8 +537,7 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
   float l_tot[2];
 #pragma unroll
   for (int rs = 0; rs < 2; rs++) {
-    l_tot[rs] = lsum[rs][0] + __shfl_xor(lsum[rs][0], 16, kWave);
-    l_tot[rs] += __shfl_xor(l_tot[rs], 32, kWave);
+    l_tot[rs] = rows_sum(lsum[rs][0]);
   }
   if (it.part0 < 0) {
     if (computes) {

@@ -187,6 +187,29 @@ __device__ __forceinline__ float group_max(float v) {
   return v;
 }
 
+// Max / sum over the four 16-lane rows of a wave (lanes i, i^16, i^32 and
+// i^48), every lane ending with the result. gfx950's row swaps
+// (v_permlane32_swap, v_permlane16_swap: the two halves, then the odd and
+// even rows, of two registers exchanged) are VALU moves; a shuffle through
+// ds_bpermute is an LDS round trip that the wave waits for.
+__device__ __forceinline__ float vmax2(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float rows_max(float v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = vmax2(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return vmax2(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float rows_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // Whole-wave reductions: DPP inside each 16-lane row, then the four row
 // results are read as scalars. The result is wave-uniform.
 __device__ __forceinline__ float wave_max(float v) {
