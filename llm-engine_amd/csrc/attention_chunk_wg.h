@@ -378,14 +378,21 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
 #pragma unroll
           for (int i = 0; i < 4; i++) s[rs][i] = nbase[rs];
         if constexpr (!kF32) {
+          // the tile's K fragments, then row tile 0's products before row
+          // tile 1's: the softmax of row tile 0 starts while row tile 1's
+          // products are still in the MFMA pipe
+          V8 ka[4][KS];
 #pragma unroll
           for (int i = 0; i < 4; i++)
 #pragma unroll
-            for (int ks = 0; ks < KS; ks++) {
-              const V8 a = *reinterpret_cast<const V8*>(kt_lds + (i * 16 + col) * L::ROW + (ks * 32 + grp * 8) * 2);
+            for (int ks = 0; ks < KS; ks++)
+              ka[i][ks] = *reinterpret_cast<const V8*>(kt_lds + (i * 16 + col) * L::ROW + (ks * 32 + grp * 8) * 2);
 #pragma unroll
-              for (int rs = 0; rs < 2; rs++) s[rs][i] = M::mma(a, qb[rs][ks], s[rs][i]);
-            }
+          for (int rs = 0; rs < 2; rs++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+              for (int ks = 0; ks < KS; ks++) s[rs][i] = M::mma(ka[i][ks], qb[rs][ks], s[rs][i]);
         } else {
           // k-step j: dim grp*LD + j of key col (A) and of row col (B); the
           // steps and lane groups together cover every dim once
@@ -414,8 +421,7 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
         // at most kRescaleSlack, so the raw hardware exp2 (whose results
         // below 2^-126 flush to zero) suffices.
         const bool full = t0 + kTileKeys - 1 <= pos0 && t0 + kTileKeys <= key_end;
-#pragma unroll
-        for (int rs = 0; rs < 2; rs++) {
+        auto softmax = [&](int rs) {
           if (!full) {
             // key t0 + 16i + 4grp + j is live iff 16i + j <= lim: one
             // per-lane limit against compile-time offsets
@@ -435,17 +441,18 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
           const float m3 = vmax3(s[rs][2][1], s[rs][2][2], s[rs][2][3]);
           const float m4 = vmax3(s[rs][3][0], s[rs][3][1], s[rs][3][2]);
           float mt = vmax2(vmax3(m0, m1, m2), vmax3(m3, m4, s[rs][3][3]));
-          mt = rows_max(mt);
           // The running max moves only when the tile's max passes it by more
           // than kRescaleSlack (log2 units): probabilities then stay below
           // 2^kRescaleSlack, and the accumulators are rescaled and the
           // scores shifted to the new base only on the tiles where some row
           // of the wave moved its max (always on a row's first live tile).
           // A row that does not move keeps sbase == m_run, or has only
-          // masked (-inf) scores so far.
-          const float cand = mt + sbase[rs];
-          const bool grow = cand > m_run[rs] + kRescaleSlack;
-          if (__builtin_amdgcn_ballot_w64(grow)) {
+          // masked (-inf) scores so far. The test runs on each lane's own
+          // 16 scores; only when some lane passes it is the row's maximum
+          // over its four lanes formed.
+          if (__builtin_amdgcn_ballot_w64(mt + sbase[rs] > m_run[rs] + kRescaleSlack)) {
+            const float cand = rows_max(mt) + sbase[rs];
+            const bool grow = cand > m_run[rs] + kRescaleSlack;
             const float m_new = grow ? cand : m_run[rs];
             const float alpha = __builtin_amdgcn_exp2f(m_run[rs] - m_new);
             const float shift = grow ? m_new - sbase[rs] : 0.f;
@@ -462,37 +469,49 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
           for (int i = 0; i < 4; i++)
 #pragma unroll
             for (int j = 0; j < 4; j++) s[rs][i][j] = __builtin_amdgcn_exp2f(s[rs][i][j]);
-        }
+        };
         if constexpr (!kF32) {
           // ---- O^T += V^T . P^T over the tile's 64 keys (2 k-steps of 32) ----
+          // V^T operands for both row tiles, read once: lane (col, grp)
+          // addresses key row kk*32 + 4*grp + col/4 (then +16) at dims
+          // 16*d + 4*(col%4), and receives dim 16*d + col of four keys: the
+          // keys P^T holds for that group.
+          V8 va[2][DT];
 #pragma unroll
           for (int kk = 0; kk < 2; kk++) {
-            V8 pb[2];
-#pragma unroll
-            for (int rs = 0; rs < 2; rs++)
-#pragma unroll
-              for (int j = 0; j < 4; j++) {
-                pb[rs][j] = static_cast<S16>(s[rs][2 * kk][j]);
-                pb[rs][4 + j] = static_cast<S16>(s[rs][2 * kk + 1][j]);
-              }
-            // lane (col, grp) addresses key row kk*32 + 4*grp + col/4 (then +16)
-            // at dims 16*d + 4*(col%4), and receives dim 16*d + col of four
-            // keys: the keys P^T holds for that group.
             const char* r_lo = vt_lds + (kk * 32 + grp * 4 + (col >> 2)) * L::ROW + (col & 3) * 8;
             const char* r_hi = r_lo + 16 * L::ROW;
 #pragma unroll
             for (int d = 0; d < DT; d++) {
               const typename M::v4 lo = lds_read_tr16<KV>(r_lo + d * 32);
               const typename M::v4 hi = lds_read_tr16<KV>(r_hi + d * 32);
-              const V8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-#pragma unroll
-              for (int rs = 0; rs < 2; rs++) acc[rs][d] = M::mma(a, pb[rs], acc[rs][d]);
+              va[kk][d] = V8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             }
-            // row sums on the MFMA: a V^T row of ones (lanes of column 0)
-#pragma unroll
-            for (int rs = 0; rs < 2; rs++) lsum[rs] = M::mma(ones, pb[rs], lsum[rs]);
           }
+          auto pv = [&](int rs) {
+#pragma unroll
+            for (int kk = 0; kk < 2; kk++) {
+              V8 pb;
+#pragma unroll
+              for (int j = 0; j < 4; j++) {
+                pb[j] = static_cast<S16>(s[rs][2 * kk][j]);
+                pb[4 + j] = static_cast<S16>(s[rs][2 * kk + 1][j]);
+              }
+#pragma unroll
+              for (int d = 0; d < DT; d++) acc[rs][d] = M::mma(va[kk][d], pb, acc[rs][d]);
+              // row sums on the MFMA: a V^T row of ones (lanes of column 0)
+              lsum[rs] = M::mma(ones, pb, lsum[rs]);
+            }
+          };
+          // row tile 1's softmax runs while row tile 0's products are in
+          // the MFMA pipe
+          softmax(0);
+          pv(0);
+          softmax(1);
+          pv(1);
         } else {
+          softmax(0);
+          softmax(1);
           // ---- O^T += V^T . P^T: k-step (i, r) covers keys 16i + 4*grp + r,
           // exactly the scores this lane's S^T accumulators hold, so P^T is
           // the accumulator as is; V^T reads single floats of the row-major
