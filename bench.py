@@ -402,8 +402,16 @@ def main():
         y = torch.empty_like(x)
         for _ in range(3):
             y.copy_(x)
+        # two kernels that do one thing each, to check the copy's factors:
+        # a reduction reads the 256 MiB and writes 8 bytes, a fill writes
+        # them and reads nothing
+        for _ in range(3):
+            x.sum(dtype=torch.int64)
+        for _ in range(3):
+            y.fill_(2)
         torch.cuda.synchronize()
-        print(json.dumps({"calibration": "copy", "bytes_read": x.numel(), "bytes_written": y.numel()}))
+        print(json.dumps({"calibration": "copy, read-only sum, write-only fill", "bytes_read": x.numel(),
+                          "bytes_written": y.numel()}))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (the decode path shards by "

@@ -88,6 +88,44 @@ def make_case(ctx, q_heads=14, kv_heads=2, head_dim=64, block_size=16, num_block
                     q_len.astype(np.int32))
 
 
+def make_shared_prefix_case(suffix, prefix_blocks=32, q_len=None, num_blocks=16384, seed=0,
+                            kv_bf16=False, q_heads=14, kv_heads=2, head_dim=64, block_size=16) -> AttnCase:
+    """Config 5's cache state: every sequence's table starts with the same
+    prefix_blocks refcounted blocks (one shared prefix), then suffix[s] tokens
+    in blocks of its own, all drawn from a random permutation of the pool
+    (fragmented). Rows as make_case: the last q_len[s] positions."""
+    rng = np.random.default_rng(seed)
+    suffix = np.asarray(suffix, dtype=np.int64)
+    S = len(suffix)
+    ctx = prefix_blocks * block_size + suffix
+    q_len = np.ones(S, dtype=np.int64) if q_len is None else np.asarray(q_len, dtype=np.int64)
+    assert np.all(q_len >= 1) and np.all(q_len <= ctx)
+    own = (suffix + block_size - 1) // block_size
+    assert prefix_blocks + int(own.sum()) <= num_blocks, "pool too small"
+    perm = rng.permutation(num_blocks).astype(np.int32)
+    shared, rest = perm[:prefix_blocks], perm[prefix_blocks:]
+    tables, o = [], 0
+    for s in range(S):
+        tables.append(np.concatenate([shared, rest[o:o + int(own[s])]]))
+        o += int(own[s])
+    table_len = np.array([len(t) for t in tables], dtype=np.int32)
+    table_offset = np.concatenate([[0], np.cumsum(table_len)[:-1]]).astype(np.int32)
+    kv_dim = kv_heads * head_dim
+    k = rng.standard_normal((num_blocks * block_size, kv_dim), dtype=np.float32)
+    v = rng.standard_normal((num_blocks * block_size, kv_dim), dtype=np.float32)
+    if kv_bf16:
+        import oracle  # test infrastructure: host RNE rounding identical to tensor.h
+        k, v = oracle.f32_to_bf16(k), oracle.f32_to_bf16(v)
+    N = int(q_len.sum())
+    q = rng.standard_normal((N, q_heads * head_dim), dtype=np.float32)
+    token_seq = np.repeat(np.arange(S, dtype=np.int32), q_len)
+    seq_start = (ctx - q_len).astype(np.int32)
+    token_pos = np.concatenate([np.arange(seq_start[s], ctx[s]) for s in range(S)]).astype(np.int32)
+    return AttnCase(q_heads, kv_heads, head_dim, block_size, num_blocks, q, k, v,
+                    np.concatenate(tables).astype(np.int32), table_offset, table_len, token_seq, token_pos,
+                    seq_start, q_len.astype(np.int32))
+
+
 def fragment_like_reference(num_blocks: int, n_single: int = 40):
     """Free-list order after the reference's fragmentation recipe
     (test_cuda_invariance.cpp:98-105): allocate n_single one-block sequences

@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 import torch
 
-from cases import loguniform_ctx, make_case
+from cases import loguniform_ctx, make_case, make_shared_prefix_case
 from gpu_util import device_q, emulated_bar, i32, max_abs, oracle_out, slices_of, to_dev_cache
 from llm_engine_amd._lib import LE_PLAN_TWO_LAUNCHES, LE_PLAN_WRITE_THROUGH
 
@@ -187,6 +187,33 @@ def test_mixed_step_config3(gpu, act, kv_bf16):
     err = max_abs(got, want)
     print(f"config3 act={act} kv_bf16={kv_bf16}: max|err|={err:.3e}")
     assert within(got, want, tol_for(case, qh), act)
+
+
+@pytest.mark.parametrize("kv_bf16", [False, True])
+@pytest.mark.parametrize("mixed", [False, True])
+def test_config5_shared_prefix_full_contexts(gpu, kv_bf16, mixed):
+    """Config 5's attention step at full size: 128 sequences whose tables
+    start with the same 32 refcounted prefix blocks (a 512-token shared
+    prefix) and go on in blocks of their own, contexts up to 8192 (four
+    sequences at 8192, the rest 512 + U[64, 3300]), all in a fragmented
+    16384-block pool. Decode rows only, or (mixed) with four sequences
+    prefilling a 256-row chunk right after the shared prefix, whose causal
+    rows read the shared blocks through the MFMA chunk tiles."""
+    rng = np.random.default_rng(55)
+    suffix = np.concatenate([[7680] * 4, rng.integers(64, 3301, size=124)])
+    q_len = None
+    if mixed:
+        suffix[4:8] = 256
+        q_len = np.ones(128, dtype=np.int64)
+        q_len[4:8] = 256
+    case = make_shared_prefix_case(suffix, q_len=q_len, seed=55, kv_bf16=kv_bf16)
+    assert int(case.table_len.max()) == 512
+    got, qh, plan = run_ragged(case, torch.float32, gpu)
+    assert (plan.plan.n_chunk_items > 0) == mixed
+    want = oracle_out(case, qh)
+    err = max_abs(got, want)
+    print(f"config5 full contexts kv_bf16={kv_bf16} mixed={mixed}: {case.n_tokens} rows, max|err|={err:.3e}")
+    assert within(got, want, tol_for(case, qh))
 
 
 def test_mixed_step_two_launches(gpu):
