@@ -138,7 +138,7 @@ template <typename ACT> struct QRope {
 // synchronises the workgroup before any K/V load issued after it, so those
 // read the row back from the cache like every other key (no other workgroup
 // reads its lines in this launch). A first tile loaded before the store is
-// loaded again in that workgroup.
+// loaded again in that workgroup if it holds the new row's key.
 __device__ __forceinline__ bool stores_new_row(const DecodeParams& p, const Work& w) {
   return p.k_new != nullptr && (w.part < 0 || w.part == w.part_begin + w.n_parts - 1);
 }
@@ -776,14 +776,18 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
         tab[i] = (bid >= 0 && bid < p.num_cache_blocks) ? bid : -1;
       }
     }
-    if (p.k_new != nullptr) __builtin_amdgcn_s_waitcnt(0);  // the new row is stored
+    // The workgroup that stores its row's new K/V waits for the store before
+    // the barrier, so no wave's later load of that slot precedes it. Only
+    // this workgroup reads those lines in the launch: the others do not wait.
+    if (stores_new_row(p, w)) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     const int key_end = min(sb1 << bs_shift, w.pos + 1);
     int key0 = (sb0 << bs_shift) + wave * T::kKeys;
     if (key0 >= key_end) continue;
-    // the early first tile stands unless this workgroup stored the new row
-    // after issuing it
-    if (!early || stores_new_row(p, w))
+    // The early first tile stands unless it holds the key this workgroup
+    // stored after issuing it (a partition shorter than the waves' first
+    // tiles); the other slots' lines are not touched by the store.
+    if (!early || (stores_new_row(p, w) && w.pos < key0 + T::kKeys))
       T::load(ra, kc, vc, key0, key_end, kv_stride, bs_shift, tab, sb0, col);
     if constexpr (kPipe) {
       // The next tile's loads are issued unconditionally (clamped to valid
