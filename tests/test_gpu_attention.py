@@ -343,12 +343,16 @@ def test_chunk_tile16_and_long_context(gpu):
 
 @pytest.mark.parametrize("kv_bf16,new_bf16", [(True, False), (True, True), (False, False)])
 @pytest.mark.parametrize("mixed", [False, True])
-def test_store_then_attend(gpu, kv_bf16, new_bf16, mixed):
+@pytest.mark.parametrize("part", [256, 0])
+def test_store_then_attend(gpu, kv_bf16, new_bf16, mixed, part):
     """le_ragged_paged_attention_store: the step's new K/V rows are stored at
     the plan's slots (inside the decode launch on a decode-only step) and
     attended to. Equal to the oracle's store_kv then attention: the caches
-    bit-exact on every slot, the outputs within tolerance. Split rows
-    (partition 256) put the new row in the last partition."""
+    bit-exact on every slot, the outputs within tolerance. Split rows put the
+    new row in the last partition: with 256-token partitions the storing
+    workgroup's first tiles hold the new key (loaded again after the store);
+    with the planner's partitions (part 0: about 500 keys for the 1500- and
+    2049-token rows) they do not, and stand."""
     import oracle
     from llm_engine_amd import kernels
     rng = np.random.default_rng(51)
@@ -370,7 +374,7 @@ def test_store_then_attend(gpu, kv_bf16, new_bf16, mixed):
     old_k = make_case(ctx, q_len=q_len, num_blocks=1024, seed=52, kv_bf16=kv_bf16)
     kc, vc = to_dev_cache(old_k.k_cache, gpu), to_dev_cache(old_k.v_cache, gpu)
     plan = kernels.Plan(slices_of(case), case.q_heads, case.kv_heads, case.head_dim, case.block_size,
-                        kc.dtype, partition_tokens=256).upload()
+                        kc.dtype, partition_tokens=part).upload()
     assert np.array_equal(plan.host_array("slots"), slots)
     nd = torch.bfloat16 if new_bf16 else torch.float32
     out = kernels.ragged_paged_attention(q, kc, vc, plan, case.scale,
@@ -382,7 +386,7 @@ def test_store_then_attend(gpu, kv_bf16, new_bf16, mixed):
     assert np.array_equal(got_k.view(np.uint8), want_k.view(np.uint8))
     assert np.array_equal(got_v.view(np.uint8), want_v.view(np.uint8))
     err = max_abs(out.float().cpu().numpy(), oracle_out(case, qh))
-    print(f"store+attend kv_bf16={kv_bf16} new_bf16={new_bf16} mixed={mixed}: parts {plan.plan.n_parts} "
+    print(f"store+attend kv_bf16={kv_bf16} new_bf16={new_bf16} mixed={mixed} part={part}: parts {plan.plan.n_parts} "
           f"max|err| {err:.3e}")
     assert within(out.float().cpu().numpy(), oracle_out(case, qh), tol_for(case, qh))
 
