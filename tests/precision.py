@@ -2,7 +2,9 @@
 and bound their error against the fp32 oracle without a GPU.
 
 With a 16-bit cache (bf16 or fp16) the MFMA tiles take 16-bit operands: the
-query is rounded to the cache type before S = q.K^T, and the softmax weights
+query is rounded to the cache type before S = q.K^T (the decode tile rounds q;
+the chunk tile rounds q * scale * log2(e), the softmax scale folded in, with
+scale_log2 formed in fp32 as the host code forms it), and the softmax weights
 P = exp2(s - m) (each <= 1) are rounded to the cache type before O = P.V.
 Accumulation is fp32. The decode tile sums l from the unrounded weights; the
 chunk tile sums l on the MFMA from the rounded ones (a row of ones beside V).
@@ -41,6 +43,11 @@ def emulate(case, q: np.ndarray, dt: str, chunk_rows: np.ndarray | None = None, 
     G = case.q_heads // case.kv_heads
     hd = case.head_dim
     qr = (_round(q, dt) if round_q else np.asarray(q, np.float32)).astype(np.float64)
+    if round_q and chunk_rows is not None and chunk_rows.any():
+        # chunk rows: q * scale_log2 rounded, then taken back to q's units
+        c = np.float32(case.scale) * np.float32(1.4426950408889634)
+        qc = _round(np.asarray(q, np.float32) * c, dt).astype(np.float64) / np.float64(c)
+        qr[chunk_rows] = qc[chunk_rows]
     out = np.zeros((q.shape[0], case.q_heads * hd), dtype=np.float64)
     bs = case.block_size
     for t in range(q.shape[0]):

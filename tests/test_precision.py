@@ -1,6 +1,7 @@
 """The 16-bit attention kernels' error, stated without a GPU: the host
-emulation of their roundings (tests/precision.py: q and the softmax weights
-rounded to the cache type before the MFMA) on configs 2 and 3, against the
+emulation of their roundings (tests/precision.py: q, or in the chunk tile
+q * scale * log2(e), and the softmax weights rounded to the cache type before
+the MFMA) on configs 2 and 3, against the
 fp32 oracle. The GPU parity tests hold each 16-bit case to twice its own
 emulated error (gpu_util.emulated_bar); here the emulated errors of the
 benchmark configs are stated and kept under half the north star's 2e-2, so
@@ -15,7 +16,7 @@ from precision import emulate
 NORTH_STAR = 2e-2  # max-abs bound for 16-bit K/V
 # the emulated max-abs error, decode rows and prefill-chunk rows, within 20 %
 STATED = {"config2": {"bf16": 1.66e-3, "f16": 2.29e-4},
-          "config3": {"bf16": (1.12e-3, 5.64e-3), "f16": (1.27e-4, 8.09e-4)}}
+          "config3": {"bf16": (1.12e-3, 5.79e-3), "f16": (1.27e-4, 8.74e-4)}}
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
