@@ -25,9 +25,10 @@ weights and K/V (benchmark config 4 shape) and reports decode tok/s at
 Poisson serving workload and the shared-prefix + preemption stress instead
 or as well.
 
-A config2 run also measures the target point and config3 the same way
-(fewer steps) and reports them under "target" and "config3", each with its
-own roofline ("config3" adds the chunk rows' MFMA flops and utilisation).
+A config2 run also measures the target point (bf16 and fp32 K/V) and
+config3 the same way (fewer steps) and reports them under "target",
+"target_f32" and "config3", each with its own roofline ("config3" adds the
+chunk rows' MFMA flops and utilisation).
 "plan.pack_us" is the steady-state host cost of le_plan_step on the step
 (sizing + packing call); the e2e legs report "plan_us_per_step", the C++
 engine's own timing of le_plan_step + le_plan_upload per step.
@@ -160,6 +161,21 @@ def pack_cost_us(slices, kv_dt, reps=200):
     return (time.perf_counter() - t0) / reps * 1e6
 
 
+_ARENA = {}
+
+
+def kv_arena(nbytes: int, dev):
+    """One byte buffer per device for the legs' K/V pools, grown (reallocated)
+    only when a leg needs more than any before it (main sizes it for the
+    largest leg of the run before the first one)."""
+    import torch
+    a = _ARENA.get(str(dev))
+    if a is None or a.numel() < nbytes:
+        _ARENA.pop(str(dev), None)
+        a = _ARENA[str(dev)] = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    return a
+
+
 def attention_leg(workload, kv, L, steps, warmup, partition=0, chunk_partition=0, graph=False,
                   separate_scatter=False, flags=0):
     """The hot path over one workload for L layers per step (see the module
@@ -178,8 +194,20 @@ def attention_leg(workload, kv, L, steps, warmup, partition=0, chunk_partition=0
     n = int(q_len.sum())
     g = torch.Generator(device=dev)
     g.manual_seed(1234)
-    kc = [torch.randn(pool * BS, kv_dim, device=dev, generator=g).to(kv_dt) for _ in range(L)]
-    vc = [torch.randn(pool * BS, kv_dim, device=dev, generator=g).to(kv_dt) for _ in range(L)]
+    # The K/V pools live in one arena allocated once per process and reused by
+    # every leg, as the engine's model allocates its pools at start-up (one
+    # allocation for all layers). With a pair of allocations per layer and
+    # leg, a leg that allocated after an earlier leg freed its pools measured
+    # up to 3.5 % slower (64 x 4096: 29.5 against 28.5 us per launch); the
+    # arena also runs that point at 28.0 us.
+    pool_elems = pool * BS * kv_dim
+    esz = torch.empty((), dtype=kv_dt).element_size()
+    arena = kv_arena(2 * L * pool_elems * esz, dev)
+    pools = arena[:2 * L * pool_elems * esz].view(kv_dt).view(2 * L, pool * BS, kv_dim)
+    for i in range(2 * L):
+        pools[i].normal_(generator=g)
+    kc = [pools[2 * l] for l in range(L)]
+    vc = [pools[2 * l + 1] for l in range(L)]
     qs = [torch.randn(n, Q_HEADS * HEAD_DIM, device=dev, generator=g).to(act_dt) for _ in range(L)]
     knew = [torch.randn(n, kv_dim, device=dev, generator=g).to(act_dt) for _ in range(L)]
     vnew = [torch.randn(n, kv_dim, device=dev, generator=g).to(act_dt) for _ in range(L)]
@@ -386,7 +414,7 @@ def main():
     ap.add_argument("--e2e-layers", type=int, default=None, help="model layers (default: all)")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
     ap.add_argument("--no-extra-workloads", action="store_true",
-                    help="skip the target and config3 sub-measurements of a config2 run")
+                    help="skip the target, target_f32 and config3 sub-measurements of a config2 run")
     ap.add_argument("--partition", type=int, default=0, help="decode partition tokens (0 = planner's choice)")
     ap.add_argument("--flags", type=int, default=0, help="le_plan_config.flags (1 = LE_PLAN_WRITE_THROUGH, 2 = LE_PLAN_TWO_LAUNCHES)")
     ap.add_argument("--chunk-partition", type=int, default=0,
@@ -418,15 +446,23 @@ def main():
               "sequence with no exchange; multi-GPU runs are not part of it).", file=sys.stderr)
         sys.exit(2)
 
+    # The north star's target point and the mixed step are measured the same
+    # way (fewer steps), each with its own roofline, after the main workload.
+    extras = []
+    if args.workload == "config2" and not args.no_extra_workloads:
+        extras = [("target", "target", "bf16"), ("target_f32", "target", "f32"), ("config3", "config3", "bf16")]
+    # the K/V arena at the size of the largest leg, before the first
+    import torch
+    need = max(2 * args.layers * workload_shape(w)[2] * BS * KV_HEADS * HEAD_DIM * (2 if k == "bf16" else 4)
+               for w, k in [(args.workload, args.kv)] + [(e[1], e[2]) for e in extras])
+    kv_arena(need, torch.device("cuda:0"))
     res = attention_leg(args.workload, args.kv, args.layers, args.steps, args.warmup, args.partition,
                         args.chunk_partition, args.graph, args.separate_scatter, args.flags)
-    # The north star's target point and the mixed step, measured the same way
-    # (fewer steps), each with its own roofline.
-    if args.workload == "config2" and not args.no_extra_workloads:
-        for extra in ("target", "config3"):
-            sub = attention_leg(extra, "bf16", args.layers, max(10, args.steps // 2), args.warmup)
-            res[extra] = {k: sub[k] for k in ("value", "unit", "ms_per_step", "pct_of_peak", "config", "plan",
-                                               "roofline")}
+    if extras:
+        for key, extra, kv in extras:
+            sub = attention_leg(extra, kv, args.layers, max(10, args.steps // 2), args.warmup)
+            res[key] = {k: sub[k] for k in ("value", "unit", "ms_per_step", "pct_of_peak", "config", "plan",
+                                             "roofline")}
     ctx, q_len, _ = workload_shape(args.workload)
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(ctx, q_len, args.kv == "bf16", args.cpu_budget)

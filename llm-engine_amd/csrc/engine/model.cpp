@@ -247,17 +247,21 @@ Model::Model(const le_model_desc& d, int num_blocks, int block_size) : d_(d) {
   }
   cos_ = upload_f32(c.data(), c.size());
   sin_ = upload_f32(s.data(), s.size());
+  // Every layer's K and V pool in one allocation: the decode attention's
+  // block gathers ran faster over pools carved from one large allocation
+  // than over one allocation per pool (64 x 4096 rows over 268 MB pools:
+  // 28.0 against 28.5 us per launch; the end-to-end decode leg's 42 MB pools
+  // show no difference).
   const size_t cache_bytes = static_cast<size_t>(num_blocks) * bs_ * KVD_ * (kv_dt_ == LE_F32 ? 4 : 2);
+  const size_t arena_bytes = 2 * cache_bytes * static_cast<size_t>(d.layers);
+  void* arena = nullptr;
+  hip_ok(hipMalloc(&arena, arena_bytes), "hipMalloc kv");
+  owned_.push_back(arena);
+  hip_ok(hipMemsetAsync(arena, 0, arena_bytes, stream_), "memset kv");
   for (int l = 0; l < d.layers; l++) {
-    void *k = nullptr, *v = nullptr;
-    hip_ok(hipMalloc(&k, cache_bytes), "hipMalloc kv");
-    owned_.push_back(k);
-    hip_ok(hipMalloc(&v, cache_bytes), "hipMalloc kv");
-    owned_.push_back(v);
-    hip_ok(hipMemsetAsync(k, 0, cache_bytes, stream_), "memset kv");
-    hip_ok(hipMemsetAsync(v, 0, cache_bytes, stream_), "memset kv");
-    kc_.push_back(k);
-    vc_.push_back(v);
+    char* base = static_cast<char*>(arena) + 2 * cache_bytes * static_cast<size_t>(l);
+    kc_.push_back(base);
+    vc_.push_back(base + cache_bytes);
   }
   miss_dev_ = le::xcd_miss_counter();
   if (miss_dev_) *static_cast<int32_t*>(miss_host_.get(4)) = 0;
