@@ -137,6 +137,74 @@ def cpu_baseline(ctx, q_len, kv_bf16: bool, budget_s: float):
                       f"in {el1:.1f} s on 1 thread (value_1_thread)"}
 
 
+def cpu_e2e_decode_baseline(budget_s: float = 3.0):
+    """End-to-end decode on the host cores: the oracle's model forward (a
+    restatement of the reference CPU backend, cpu_model.cpp:98-214, naive
+    threaded GEMMs, bf16 K/V) on one 64-row decode step of the decode64 leg's
+    shape (TinyLlama-1.1B, contexts = prompts U[128, 1024] plus up to 256
+    generated tokens, block 16). Its caches are filled directly (no CPU
+    prefill); a bounded sample times the step with 1 and with 4 layers, and
+    the 22-layer step is the 1-layer step plus 21 times the per-layer
+    difference. The
+    weights' and caches' values do not change the time of naive GEMMs and the
+    attention loop, so both are filled from a small random block (N(0, 0.02)
+    weights, N(0, 1) bf16 K/V) rather than drawn in full."""
+    import oracle
+    from e2e_util import OracleModel
+    from llm_engine_amd import _lib
+    from llm_engine_amd.engine import ARCHS, Weights
+    rng = np.random.default_rng(9)
+    wtile = (rng.standard_normal(1 << 20, dtype=np.float32) * np.float32(0.02))
+
+    def filled(*shape):
+        return np.resize(wtile, shape).astype(np.float32)
+
+    def weights(nl):
+        a = dict(ARCHS["tinyllama-1.1b"], layers=nl)
+        H, I, V = a["hidden"], a["inter"], a["vocab"]
+        QD, KVD = a["q_heads"] * a["head_dim"], a["kv_heads"] * a["head_dim"]
+        w = Weights(a, filled(V, H), np.ones(H, np.float32), None if a["tie"] else filled(V, H))
+        for _ in range(nl):
+            L = dict(wq=filled(QD, H), wk=filled(KVD, H), wv=filled(KVD, H), wo=filled(H, QD),
+                     wgate=filled(I, H), wup=filled(I, H), wdown=filled(H, I),
+                     in_norm=np.ones(H, np.float32), post_norm=np.ones(H, np.float32))
+            if a["qkv_bias"]:
+                L.update(bq=np.zeros(QD, np.float32), bk=np.zeros(KVD, np.float32), bv=np.zeros(KVD, np.float32))
+            w.layers.append(L)
+        return w
+
+    S = 64
+    ctx = rng.integers(128, 1025, S) + rng.integers(0, 257, S)
+    nb = (ctx + BS - 1) // BS
+    pool = int(nb.sum()) + 64
+    perm = rng.permutation(pool).astype(np.int32)
+    tables = np.split(perm[:int(nb.sum())], np.cumsum(nb)[:-1])
+    tables = [np.ascontiguousarray(t) for t in tables]
+    toks = [rng.integers(0, 32000, int(c)).astype(np.int32) for c in ctx]
+    step = [_lib.StepSlice(s, int(ctx[s]) - 1, 1, 1, int(nb[s]), tables[s].ctypes.data, toks[s].ctypes.data)
+            for s in range(S)]
+    tile = oracle.f32_to_bf16(rng.standard_normal(1 << 20, dtype=np.float32))
+    per_step = {}
+    for nl in (1, 4):
+        om = OracleModel(weights(nl), pool, BS, kv_bf16=True)
+        for c in om.kc + om.vc:
+            c.reshape(-1)[:] = np.resize(tile, c.size)
+        om.logits(step)  # warm-up
+        reps, t0 = 0, time.perf_counter()
+        while reps < 2 or time.perf_counter() - t0 < budget_s / 2:
+            om.logits(step)
+            reps += 1
+        per_step[nl] = ((time.perf_counter() - t0) / reps, reps)
+        del om
+    t1, t4 = per_step[1][0], per_step[4][0]
+    t22 = t1 + 21 * (t4 - t1) / 3
+    threads = oracle.threads_default()
+    return {"decode_tok_per_s": round(S / t22, 2), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"64-row decode steps at contexts {int(ctx.min())}-{int(ctx.max())}, oracle.c model forward "
+                      f"on {threads} threads: 1 layer {t1:.3f} s/step ({per_step[1][1]} steps), 4 layers "
+                      f"{t4:.3f} s/step ({per_step[4][1]} steps); 22 layers estimated {t22:.2f} s/step"}
+
+
 def pack_cost_us(slices, kv_dt, reps=200):
     """Steady-state host cost of le_plan_step on a step's slices (the
     sized call and the packing call, as the engine makes them each step),
@@ -471,6 +539,8 @@ def main():
     for leg in (["decode64", "config4", "config5"] if args.e2e == "all" else [args.e2e]):
         if leg != "none":
             res["e2e_" + leg] = e2e_leg(leg, layers=args.e2e_layers)
+            if leg == "decode64" and not args.no_cpu_baseline:
+                res["e2e_decode64"]["cpu_baseline"] = cpu_e2e_decode_baseline()
     print(json.dumps(res), flush=True)
 
 
