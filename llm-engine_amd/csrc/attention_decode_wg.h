@@ -328,12 +328,37 @@ template <int HD> constexpr int kVStride16 = HD * 2 + 16;
 
 constexpr int kTabCap = 1024;  // block ids of a partition staged in LDS
 
-// One wave's K/V registers for a 64-key tile: this lane's key of each of the
-// four 16-key subtiles, KS 16-byte chunks (8 dims) each.
+// One wave's K/V registers for a 64-key tile. K: this lane's key of each of
+// the four 16-key subtiles, KS 16-byte chunks (8 dims) each, in the MFMA
+// operand layout. V: 4 * KS 16-byte loads bound for the wave's LDS tile, where
+// the layout is free (VLanes).
 template <int KS> struct TileRegs {
-  uint4 k[4][KS], v[4][KS];
-  bool ok[4];  // the lane's block id of subtile i was a valid cache block
+  uint4 k[4][KS], v[4 * KS];
+  uint32_t vok;  // bit j: the block id of V load j was a valid cache block
 };
+
+// The key row of the tile and the 16-byte piece of it that this lane moves in
+// V load j, for key rows of ROW_BYTES. With WHOLE, each load instruction
+// covers whole rows (ROW_BYTES / 16 lanes per row, consecutive rows per load):
+// with 128-byte rows that reads 8 whole rows per instruction instead of half
+// of each of 16 rows (the K operand layout), config 2 13.2 -> 12.9 us.
+// Without it, load j is the K operand layout's: row 16 * (j / KS) + col, piece
+// 4 * (j % KS) + group (kept for 256-byte 16-bit rows, where whole rows need
+// 16 address computations per tile and the tile no longer fits two waves per
+// SIMD).
+template <int ROW_BYTES, bool WHOLE, int KS> struct VLanes {
+  static constexpr int kLanesPerRow = ROW_BYTES / 16;
+  static constexpr int kRowsPerLoad = kWave / kLanesPerRow;
+  int a, b;  // WHOLE: first row, piece; else: col, group
+  __device__ __forceinline__ VLanes() {
+    const int lane = threadIdx.x & (kWave - 1);
+    a = WHOLE ? lane / kLanesPerRow : lane & 15;
+    b = WHOLE ? lane % kLanesPerRow : lane >> 4;
+  }
+  __device__ __forceinline__ int row(int j) const { return WHOLE ? j * kRowsPerLoad + a : (j / KS) * 16 + a; }
+  __device__ __forceinline__ int piece(int j) const { return WHOLE ? b : (j % KS) * 4 + b; }
+};
+template <int HD> using VLanes16 = VLanes<HD * 2, HD == 64, HD / 32>;
 
 // State the wave carries across tiles.
 template <int HD> struct WaveAcc {
@@ -381,17 +406,28 @@ __device__ __forceinline__ void load_tile(TileRegs<HD / 32>& r, const T* kc, con
                                           const int* tab, int tab_base, int col) {
   constexpr int KS = HD / 32;
   const int bs_mask = (1 << bs_shift) - 1;
+  const VLanes16<HD> vl;
+  // vc points at this lane's K operand dims (group * 8); V loads address
+  // their own pieces from the row start
+  const T* vrow = vc - (threadIdx.x & (kWave - 1)) / 16 * 8;
+  r.vok = 0;
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int key = min(key0 + i * 16 + col, key_end - 1);
     const int bid = tab[(key >> bs_shift) - tab_base];
-    r.ok[i] = bid >= 0;  // the staging step marks invalid ids as -1
-    const int64_t slot = (static_cast<int64_t>(r.ok[i] ? bid : 0) << bs_shift) + (key & bs_mask);
+    const bool ok = bid >= 0;  // the staging step marks invalid ids as -1
+    const int64_t slot = (static_cast<int64_t>(ok ? bid : 0) << bs_shift) + (key & bs_mask);
 #pragma unroll
-    for (int ks = 0; ks < KS; ks++) {
-      r.k[i][ks] = ld16_stream(kc + slot * kv_stride + ks * 32);
-      r.v[i][ks] = ld16_stream(vc + slot * kv_stride + ks * 32);
-    }
+    for (int ks = 0; ks < KS; ks++) r.k[i][ks] = ld16_stream(kc + slot * kv_stride + ks * 32);
+  }
+#pragma unroll
+  for (int j = 0; j < 4 * KS; j++) {
+    const int key = min(key0 + vl.row(j), key_end - 1);
+    const int bid = tab[(key >> bs_shift) - tab_base];
+    const bool ok = bid >= 0;
+    r.vok |= static_cast<uint32_t>(ok) << j;
+    const int64_t slot = (static_cast<int64_t>(ok ? bid : 0) << bs_shift) + (key & bs_mask);
+    r.v[j] = ld16_stream(vrow + slot * kv_stride + vl.piece(j) * 8);
   }
 }
 
@@ -429,18 +465,17 @@ __device__ __forceinline__ void compute_tile(WaveAcc<HD>& st, const TileRegs<HD 
   // V rows into this wave's LDS tile, row-major (key rows), with 16-byte
   // stores. A dead key's row is replaced by zeros (its p is 0, but the row
   // read may hold NaNs).
+  const VLanes16<HD> vl;
 #pragma unroll
-  for (int i = 0; i < 4; i++)
-#pragma unroll
-    for (int ks = 0; ks < KS; ks++) {
-      // a mask, not a select: a select becomes a branch, and the loads it
-      // skips count as outstanding at every later join (the loop head then
-      // waits for the next tile's loads too)
-      const uint32_t m = 0u - static_cast<uint32_t>(key0 + i * 16 + col < key_end && r.ok[i]);
-      const uint4 v = r.v[i][ks];
-      *reinterpret_cast<uint4*>(vt + (i * 16 + col) * V_STRIDE + (ks * 32 + grp * 8) * 2) =
-          make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
-    }
+  for (int j = 0; j < 4 * KS; j++) {
+    // a mask, not a select: a select becomes a branch, and the loads it
+    // skips count as outstanding at every later join (the loop head then
+    // waits for the next tile's loads too)
+    const int row = vl.row(j);
+    const uint32_t m = 0u - static_cast<uint32_t>(key0 + row < key_end && ((r.vok >> j) & 1u));
+    const uint4 v = r.v[j];
+    *reinterpret_cast<uint4*>(vt + row * V_STRIDE + vl.piece(j) * 16) = make_uint4(v.x & m, v.y & m, v.z & m, v.w & m);
+  }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -521,17 +556,26 @@ template <typename T, int HD> struct DecodeTile16 {
                                                      int64_t num_blocks, int col) {
     constexpr int KS = HD / 32;
     const int bs_mask = (1 << bs_shift) - 1;
+    const VLanes16<HD> vl;
+    const T* vrow = vc - (threadIdx.x & (kWave - 1)) / 16 * 8;
+    r.vok = 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int rel = rel0 + i * 16 + col;
       const int bid = ids[min(rel >> bs_shift, n_ids - 1)];
-      r.ok[i] = bid >= 0 && bid < num_blocks;
-      const int64_t slot = (static_cast<int64_t>(r.ok[i] ? bid : 0) << bs_shift) + (rel & bs_mask);
+      const bool ok = bid >= 0 && bid < num_blocks;
+      const int64_t slot = (static_cast<int64_t>(ok ? bid : 0) << bs_shift) + (rel & bs_mask);
 #pragma unroll
-      for (int ks = 0; ks < KS; ks++) {
-        r.k[i][ks] = ld16_stream(kc + slot * kv_stride + ks * 32);
-        r.v[i][ks] = ld16_stream(vc + slot * kv_stride + ks * 32);
-      }
+      for (int ks = 0; ks < KS; ks++) r.k[i][ks] = ld16_stream(kc + slot * kv_stride + ks * 32);
+    }
+#pragma unroll
+    for (int j = 0; j < 4 * KS; j++) {
+      const int rel = rel0 + vl.row(j);
+      const int bid = ids[min(rel >> bs_shift, n_ids - 1)];
+      const bool ok = bid >= 0 && bid < num_blocks;
+      r.vok |= static_cast<uint32_t>(ok) << j;
+      const int64_t slot = (static_cast<int64_t>(ok ? bid : 0) << bs_shift) + (rel & bs_mask);
+      r.v[j] = ld16_stream(vrow + slot * kv_stride + vl.piece(j) * 8);
     }
   }
 };
@@ -557,9 +601,11 @@ template <int HD> struct DecodeTile<float, HD> {
   static constexpr int VT_BYTES = kKeys * V_STRIDE;
   static constexpr bool kPipe = HD == 64;
   static constexpr bool kEarly = false;  // measured slower: more registers for no gain
+  using VL = VLanes<HD * 4, true, 0>;
+  // K in the MFMA operand layout; V as whole key rows for the LDS tile
   struct Regs {
-    float4 k[kSub][kPieces], v[kSub][kPieces];
-    bool ok[kSub];
+    float4 k[kSub][kPieces], v[kSub * kPieces];
+    uint32_t vok;  // bit j: the block id of V load j was a valid cache block
   };
   struct QOp { float q[kLaneDims]; };
   template <typename Src>
@@ -578,38 +624,52 @@ template <int HD> struct DecodeTile<float, HD> {
   __device__ __forceinline__ static void load(Regs& r, const float* kc, const float* vc, int key0, int key_end,
                                               int kv_stride, int bs_shift, const int* tab, int tab_base, int col) {
     const int bs_mask = (1 << bs_shift) - 1;
+    const VL vl;
+    const float* vrow = vc - (threadIdx.x & (kWave - 1)) / 16 * kLaneDims + vl.piece(0) * 4;
+    r.vok = 0;
 #pragma unroll
     for (int i = 0; i < kSub; i++) {
       const int key = min(key0 + i * 16 + col, key_end - 1);
       const int bid = tab[(key >> bs_shift) - tab_base];
-      r.ok[i] = bid >= 0;
-      const int64_t slot = (static_cast<int64_t>(r.ok[i] ? bid : 0) << bs_shift) + (key & bs_mask);
+      const bool ok = bid >= 0;
+      const int64_t slot = (static_cast<int64_t>(ok ? bid : 0) << bs_shift) + (key & bs_mask);
 #pragma unroll
-      for (int c = 0; c < kPieces; c++) {
-        const uint4 kk = ld16_stream(kc + slot * kv_stride + c * 4);
-        const uint4 vv = ld16_stream(vc + slot * kv_stride + c * 4);
-        r.k[i][c] = make_float4(__uint_as_float(kk.x), __uint_as_float(kk.y), __uint_as_float(kk.z), __uint_as_float(kk.w));
-        r.v[i][c] = make_float4(__uint_as_float(vv.x), __uint_as_float(vv.y), __uint_as_float(vv.z), __uint_as_float(vv.w));
-      }
+      for (int c = 0; c < kPieces; c++) r.k[i][c] = as_float4(ld16_stream(kc + slot * kv_stride + c * 4));
+    }
+#pragma unroll
+    for (int j = 0; j < kSub * kPieces; j++) {
+      const int key = min(key0 + vl.row(j), key_end - 1);
+      const int bid = tab[(key >> bs_shift) - tab_base];
+      const bool ok = bid >= 0;
+      r.vok |= static_cast<uint32_t>(ok) << j;
+      const int64_t slot = (static_cast<int64_t>(ok ? bid : 0) << bs_shift) + (key & bs_mask);
+      r.v[j] = as_float4(ld16_stream(vrow + slot * kv_stride));
     }
   }
   __device__ __forceinline__ static void load_direct(Regs& r, const float* kc, const float* vc, int rel0,
                                                      const int32_t* ids, int n_ids, int bs_shift, int kv_stride,
                                                      int64_t num_blocks, int col) {
     const int bs_mask = (1 << bs_shift) - 1;
+    const VL vl;
+    const float* vrow = vc - (threadIdx.x & (kWave - 1)) / 16 * kLaneDims + vl.piece(0) * 4;
+    r.vok = 0;
 #pragma unroll
     for (int i = 0; i < kSub; i++) {
       const int rel = rel0 + i * 16 + col;
       const int bid = ids[min(rel >> bs_shift, n_ids - 1)];
-      r.ok[i] = bid >= 0 && bid < num_blocks;
-      const int64_t slot = (static_cast<int64_t>(r.ok[i] ? bid : 0) << bs_shift) + (rel & bs_mask);
+      const bool ok = bid >= 0 && bid < num_blocks;
+      const int64_t slot = (static_cast<int64_t>(ok ? bid : 0) << bs_shift) + (rel & bs_mask);
 #pragma unroll
-      for (int c = 0; c < kPieces; c++) {
-        const uint4 kk = ld16_stream(kc + slot * kv_stride + c * 4);
-        const uint4 vv = ld16_stream(vc + slot * kv_stride + c * 4);
-        r.k[i][c] = make_float4(__uint_as_float(kk.x), __uint_as_float(kk.y), __uint_as_float(kk.z), __uint_as_float(kk.w));
-        r.v[i][c] = make_float4(__uint_as_float(vv.x), __uint_as_float(vv.y), __uint_as_float(vv.z), __uint_as_float(vv.w));
-      }
+      for (int c = 0; c < kPieces; c++) r.k[i][c] = as_float4(ld16_stream(kc + slot * kv_stride + c * 4));
+    }
+#pragma unroll
+    for (int j = 0; j < kSub * kPieces; j++) {
+      const int rel = rel0 + vl.row(j);
+      const int bid = ids[min(rel >> bs_shift, n_ids - 1)];
+      const bool ok = bid >= 0 && bid < num_blocks;
+      r.vok |= static_cast<uint32_t>(ok) << j;
+      const int64_t slot = (static_cast<int64_t>(ok ? bid : 0) << bs_shift) + (rel & bs_mask);
+      r.v[j] = as_float4(ld16_stream(vrow + slot * kv_stride));
     }
   }
   __device__ __forceinline__ static void compute(WaveAcc<HD>& st, const Regs& r, const QOp& q, int key0, int key_end,
@@ -642,16 +702,15 @@ template <int HD> struct DecodeTile<float, HD> {
     softmax_tile<kSub>(st, s, mt);
 
     // V rows into this wave's LDS tile (row-major); a dead key's row is zeros.
+    const VL vl;
 #pragma unroll
-    for (int i = 0; i < kSub; i++) {
-      const uint32_t m = 0u - static_cast<uint32_t>(key0 + i * 16 + col < key_end && r.ok[i]);  // as above
-#pragma unroll
-      for (int c = 0; c < kPieces; c++) {
-        const float4 v = r.v[i][c];
-        *reinterpret_cast<float4*>(vt + (i * 16 + col) * V_STRIDE + (grp * kLaneDims + c * 4) * 4) =
-            make_float4(__uint_as_float(__float_as_uint(v.x) & m), __uint_as_float(__float_as_uint(v.y) & m),
-                        __uint_as_float(__float_as_uint(v.z) & m), __uint_as_float(__float_as_uint(v.w) & m));
-      }
+    for (int j = 0; j < kSub * kPieces; j++) {
+      const int row = vl.row(j);
+      const uint32_t m = 0u - static_cast<uint32_t>(key0 + row < key_end && ((r.vok >> j) & 1u));  // as above
+      const float4 v = r.v[j];
+      *reinterpret_cast<float4*>(vt + row * V_STRIDE + vl.piece(j) * 16) =
+          make_float4(__uint_as_float(__float_as_uint(v.x) & m), __uint_as_float(__float_as_uint(v.y) & m),
+                      __uint_as_float(__float_as_uint(v.z) & m), __uint_as_float(__float_as_uint(v.w) & m));
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();

@@ -147,6 +147,9 @@ __device__ __forceinline__ typename mma16<T>::v4 lds_read_tr16(const char* p) {
 // K/V history load (read once per step). A non-temporal variant measured no
 // faster on the decode rows.
 __device__ __forceinline__ uint4 ld16_stream(const void* p) { return ld16(p); }
+__device__ __forceinline__ float4 as_float4(uint4 u) {
+  return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
+}
 
 // Cross-lane moves inside a 16-lane DPP row: no LDS traffic, one VALU op each.
 namespace dpp {
