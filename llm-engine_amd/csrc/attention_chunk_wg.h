@@ -248,7 +248,6 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
   const int tok0 = it.tok_begin;
   const int kv_stride = p.kv_heads * HD;
   const int key_begin = it.blk_begin << bs_shift;
-  const int n_keys_blk = (it.blk_end - it.blk_begin) << bs_shift;  // load range: whole blocks
   // The item's block ids sit at a fixed stride in the plan, padded with -1:
   // each thread reads the ids of its own keys there directly, so the K/V
   // loads wait for one round trip and no barrier.
@@ -257,9 +256,11 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
   const char* vbase = static_cast<const char*>(p.v_cache);
 
   // Stage staging: thread pieces k cover key (tid + k*kThreads) / CPR, 16-byte
-  // piece c of that key's K row and of its V row. Keys past the item (or in
-  // an invalid block) read a valid address and are stored as zeros: their
-  // scores are masked, and a zero V row keeps p * v finite.
+  // piece c of that key's K row and of its V row. Keys past the item's live
+  // keys (the unused rows of its last block, which may hold anything, NaN
+  // included) or in an invalid block read the item's last live key instead
+  // and are stored as zeros: their scores are masked, and a zero V row keeps
+  // p * v finite.
   uint4 kv[2][PER / 2];
   bool okp[PER / 2];
   auto issue = [&](int rel0) {
@@ -267,14 +268,14 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
     for (int k = 0; k < PER / 2; k++) {
       const int piece = tid + k * kThreads;
       const int key_l = piece / CPR, c = piece - key_l * CPR;
-      // a piece past the item reads the item's last key instead (a line the
-      // workgroup loads anyway), not one shared address that every
+      // a piece past the item reads the item's last live key instead (a line
+      // the workgroup loads anyway), not one shared address that every
       // workgroup's surplus pieces would pile onto
       const int rel = rel0 + key_l;
-      const int relc = min(rel, n_keys_blk - 1);
+      const int relc = min(rel, it.key_live - 1);
       const int bid = ids[min(relc >> bs_shift, p.ids_stride - 1)];
       const bool bid_ok = bid >= 0 && bid < p.num_cache_blocks;
-      okp[k] = rel < n_keys_blk && bid_ok;
+      okp[k] = rel < it.key_live && bid_ok;
       const int64_t slot = (static_cast<int64_t>(bid_ok ? bid : 0) << bs_shift) + (relc & bs_mask);
       const int64_t off = (slot * kv_stride + kvh * HD) * static_cast<int64_t>(sizeof(KV)) + c * 16;
       kv[0][k] = ld16_stream(kbase + off);
@@ -367,7 +368,7 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
     __syncthreads();
     const int s0 = key_begin + rel0;
     if (computes) {
-      const int key_end = min(key_begin + n_keys_blk, pos0 + nq);  // past the last row's position: dead
+      const int key_end = key_begin + it.key_live;  // past the last row's position: dead
       // Tiles of the stage with a live key.
       const int nt = min(kStageKeys<KV, HD> / kTileKeys, (key_end - s0 + kTileKeys - 1) / kTileKeys);
       // ---- S^T of tile kt: 64 keys x 32 rows, less the rows' current base ----
@@ -547,7 +548,7 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
       }
     }
     rel0 += kStageKeys<KV, HD>;
-    if (rel0 >= n_keys_blk) break;
+    if (rel0 >= it.key_live) break;
     __syncthreads();  // the stage is no longer read
     issue(rel0);
   }

@@ -39,6 +39,9 @@ struct DecodeItem {
 // part_stride) of each row.
 struct ChunkItem {
   int32_t tok_begin, n_q, blk_begin, blk_end, part0, part_stride, seq, part;
+  // keys of [blk_begin * block_size, ...) that hold a live position (at most
+  // the tile's last position + 1): rows past it are never read
+  int32_t key_live;
 };
 
 // Element types are passed as le_dtype codes: 0 fp32, 1 bf16, 2 fp16.

@@ -251,6 +251,7 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
             c.part_stride = J;
             c.seq = slice_seq[i];
             c.part = j;
+            c.key_live = std::min((c.blk_end - c.blk_begin) * bs, last + 1 - c.blk_begin * bs);
             chk.push_back(c);
           }
           if (J > 1) parts += nq * J;

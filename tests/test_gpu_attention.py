@@ -486,3 +486,43 @@ def test_graph_replays_match_eager(gpu):
         again = kernels.ragged_paged_attention(q, kc, vc, plan, case.scale, workspace=ws)
         torch.cuda.synchronize()
         assert torch.equal(again, eager)
+
+
+def _poison_unused(case):
+    """NaN in every cache row that no sequence's live positions map to (the
+    rest of each last block, and every block outside the tables): a kernel
+    that reads one of them into a live result turns that row's output NaN."""
+    bs = case.block_size
+    used = np.zeros(case.num_blocks * bs, dtype=bool)
+    ctx = case.seq_start + case.seq_qlen
+    for s in range(len(ctx)):
+        pos = np.arange(int(ctx[s]))
+        blocks = case.tables[case.table_offset[s] + pos // bs].astype(np.int64)
+        used[blocks * bs + pos % bs] = True
+    for c in (case.k_cache, case.v_cache):
+        if c.dtype == np.uint16:
+            c[~used] = 0x7FC0  # bf16 quiet NaN
+        else:
+            c[~used] = np.nan
+
+
+@pytest.mark.parametrize("kv", ["f32", "bf16", "f16"])
+def test_unused_cache_rows_never_read(gpu, kv):
+    """Dead keys of a tile (past a partition's or row's end) are read at a
+    live key's address and masked: with every unused cache row NaN, decode
+    rows (both entry points, split rows included) and a mixed step with
+    prefill-chunk rows still match the oracle everywhere."""
+    rng = np.random.default_rng(11)
+    ctx = list(loguniform_ctx(rng, 24, 1, 3000)) + [700, 1333]
+    q_len = [1] * 24 + [77, 300]
+    for ql in (None, q_len):
+        case = make_case(ctx, q_len=ql, num_blocks=4096, seed=11, kv_bf16=kv == "bf16", kv_f16=kv == "f16")
+        _poison_unused(case)
+        b, qh, _ = run_ragged(case, torch.float32, gpu)
+        want = oracle_out(case, qh)
+        assert np.isfinite(b).all()
+        assert within(b, want, tol_for(case, qh))
+        if ql is None:
+            a, _ = run_decode(case, torch.float32, gpu)
+            assert np.isfinite(a).all()
+            assert within(a, want, tol_for(case, qh))
