@@ -68,7 +68,7 @@ def _plan(slices, kv=torch.bfloat16, **kw):
 def _items(plan, kind):
     P = plan.plan
     n, w, off = {"decode": (P.n_decode_items, 8, P.off_decode_items),
-                 "chunk": (P.n_chunk_items, 8, P.off_chunk_items)}[kind]
+                 "chunk": (P.n_chunk_items, 9, P.off_chunk_items)}[kind]
     return plan.host.numpy()[off:off + 4 * n * w].view(np.int32).reshape(n, w)
 
 
@@ -107,11 +107,14 @@ def check_work_lists(plan, slices, bs=16):
     # numbered 0..J-1 in key order, with part0 = base + j
     tiles, tile_bins = {}, {}
     for k, it in enumerate(chk):
-        tb, nq, b0, b1, p0, stride, seq, part = (int(x) for x in it)
+        tb, nq, b0, b1, p0, stride, seq, part, live = (int(x) for x in it)
         if nq == 0:  # padding that keeps split tiles on one XCD
             assert b0 == b1 and p0 == -1
             continue
         assert 1 <= nq <= 32 and all(pos[tb + r] == pos[tb] + r for r in range(nq))
+        # live keys from the partition's first key: whole blocks, except that
+        # the partition holding the tile's last position stops just past it
+        assert live == min((b1 - b0) * bs, pos[tb + nq - 1] + 1 - b0 * bs) and live >= 1
         tiles.setdefault(tb, []).append((b0, b1, p0, stride, nq, part))
         if p0 >= 0:  # a split tile's partitions sit at indices equal modulo 8 (one XCD)
             tile_bins.setdefault(tb, set()).add(k % 8)
