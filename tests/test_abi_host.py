@@ -301,3 +301,68 @@ def test_fixed_layout_is_constant_across_decode_steps():
         check_work_lists(plan, sl)
     with pytest.raises(ValueError):  # prefill chunks have no fixed layout
         _plan([Slice(1, 0, 5, True, blocks[0][:1], np.zeros(5, np.int32))], partition_tokens=512, table_capacity=cap)
+
+
+@pytest.mark.parametrize("bs", [8, 16, 32])
+def test_plan_fuzz_accepts_exactly_the_valid_steps(bs):
+    """Random steps, valid and not: sequences whose keys repeat across
+    slices, tables shorter than a slice's positions, empty tables, negative
+    starts and lengths, chunk and decode slices mixed. le_plan_step accepts
+    exactly the steps whose every slice has a block for each of its positions
+    in its own table and in its sequence's first table (one table per
+    sequence), and rejects the rest with LE_EINVAL, never reading past a
+    table; every accepted step packs as the oracle packer does (slots by the
+    closed form of kv_cache.h:29-31 through the first slice's table) with
+    consistent work lists."""
+    from llm_engine_amd.kernels import Slice
+    rng = np.random.default_rng(1000 + bs)
+    toks = rng.integers(0, 32000, size=4096).astype(np.int32)
+    n_ok = n_bad = 0
+    for case in range(300):
+        n_keys = int(rng.integers(1, 6))
+        tables = {k: rng.permutation(2048)[:int(rng.integers(0, 12))].astype(np.int32) for k in range(n_keys)}
+        slices, first_nb, valid = [], {}, True
+        for _ in range(int(rng.integers(1, 8))):
+            key = int(rng.integers(0, n_keys))
+            nb = tables[key].size
+            # a table of its own that sometimes differs from the first slice's
+            own = tables[key] if rng.random() < 0.8 else rng.permutation(2048)[:int(rng.integers(0, 14))].astype(np.int32)
+            cap = max(own.size * bs, 1)
+            ln = 1 if rng.random() < 0.5 else int(rng.integers(-1, min(cap, 200) + 2))
+            start = int(rng.integers(-1, cap + 2)) if rng.random() < 0.1 else int(rng.integers(0, max(cap - max(ln, 1), 0) + 2))
+            if ln <= 0 or start < 0:
+                valid = False
+            else:
+                last = start + ln - 1
+                if last // bs >= own.size:
+                    valid = False
+                if key in first_nb and last // bs >= first_nb[key]:
+                    valid = False
+            first_nb.setdefault(key, own.size)
+            slices.append(Slice(key, start, ln, bool(rng.random() < 0.7), own, toks))
+        try:
+            plan = kernels_plan(slices, bs)
+        except ValueError:
+            assert not valid, (case, [(s.seq_key, s.start, s.len, s.blocks.size) for s in slices])
+            n_bad += 1
+            continue
+        assert valid, (case, [(s.seq_key, s.start, s.len, s.blocks.size) for s in slices])
+        n_ok += 1
+        want = oracle.pack_step([(s.seq_key, s.start, s.len, s.needs_logits, s.blocks, s.tokens)
+                                 for s in slices], bs)
+        for f in ("token_ids", "positions", "slots", "token_seq", "tables", "table_offset", "logit_rows"):
+            assert np.array_equal(plan.host_array(f), getattr(want, f)), (case, f)
+        # slots by the closed form, through each sequence's first table
+        firsts = {}
+        for s in slices:
+            firsts.setdefault(s.seq_key, s.blocks)
+        slots = np.concatenate([firsts[s.seq_key][(s.start + np.arange(s.len)) // bs] * bs
+                                + (s.start + np.arange(s.len)) % bs for s in slices])
+        assert np.array_equal(plan.host_array("slots"), slots)
+        check_work_lists(plan, slices, bs=bs)
+    assert n_ok > 50 and n_bad > 50
+
+
+def kernels_plan(slices, bs):
+    from llm_engine_amd import kernels
+    return kernels.Plan(slices, 14, 2, 64, bs, torch.bfloat16, device="cpu", pin=False)
