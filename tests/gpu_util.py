@@ -105,3 +105,21 @@ def emulated_bar(case: AttnCase, q_f32: np.ndarray, want: np.ndarray | None = No
 
 def _widen_cache(c: np.ndarray) -> np.ndarray:
     return oracle.bf16_to_f32(c) if c.dtype == np.uint16 else c.astype(np.float32)
+
+
+def poison_unused(case: AttnCase) -> None:
+    """NaN in every cache row that no sequence's live positions map to (the
+    rest of each last block, and every block outside the tables): a kernel
+    that reads one of them into a live result turns that row's output NaN."""
+    bs = case.block_size
+    used = np.zeros(case.num_blocks * bs, dtype=bool)
+    ctx = case.seq_start + case.seq_qlen
+    for s in range(len(ctx)):
+        pos = np.arange(int(ctx[s]))
+        blocks = case.tables[case.table_offset[s] + pos // bs].astype(np.int64)
+        used[blocks * bs + pos % bs] = True
+    for c in (case.k_cache, case.v_cache):
+        if c.dtype == np.uint16:
+            c[~used] = 0x7FC0  # bf16 quiet NaN
+        else:
+            c[~used] = np.nan

@@ -18,7 +18,7 @@ import pytest
 import torch
 
 from cases import loguniform_ctx, make_case, make_shared_prefix_case
-from gpu_util import device_q, emulated_bar, i32, max_abs, oracle_out, slices_of, to_dev_cache
+from gpu_util import device_q, emulated_bar, i32, max_abs, oracle_out, poison_unused, slices_of, to_dev_cache
 from llm_engine_amd._lib import LE_PLAN_TWO_LAUNCHES, LE_PLAN_WRITE_THROUGH
 
 pytestmark = pytest.mark.gpu
@@ -399,7 +399,8 @@ def test_random_ragged_steps(gpu, seed):
     dtypes, and the decode partition size all drawn from a seeded generator.
     Every launch shape the planner produces for such steps (one launch or
     decode only, split and unsplit rows and tiles) is reached across the
-    seeds."""
+    seeds. Every cache row outside the live positions is NaN, so a tile
+    variant that lets a dead row into a result fails here too."""
     rng = np.random.default_rng(1000 + seed)
     q_heads, kv_heads = [(14, 2), (32, 4), (8, 8), (16, 2), (4, 1), (28, 4)][rng.integers(6)]
     head_dim = int(rng.choice([64, 128]))
@@ -415,9 +416,11 @@ def test_random_ragged_steps(gpu, seed):
     need = int(((ctx + block_size - 1) // block_size).sum())
     case = make_case(ctx, q_len=q_len, q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim,
                      block_size=block_size, num_blocks=need + 64, seed=seed, kv_bf16=kv_bf16)
+    poison_unused(case)
     part = int(rng.choice([0, 256, 640, 2048]))
     got, qh, plan = run_ragged(case, act, gpu, partition_tokens=part)
     want = oracle_out(case, qh)
+    assert np.isfinite(got).all()
     err = max_abs(got, want)
     print(f"seed {seed}: {q_heads}/{kv_heads}x{head_dim} bs {block_size} kv_bf16 {kv_bf16} act {act} "
           f"rows {plan.plan.n_tokens} dec {plan.plan.n_decode_items} chunk {plan.plan.n_chunk_items} "
@@ -488,24 +491,6 @@ def test_graph_replays_match_eager(gpu):
         assert torch.equal(again, eager)
 
 
-def _poison_unused(case):
-    """NaN in every cache row that no sequence's live positions map to (the
-    rest of each last block, and every block outside the tables): a kernel
-    that reads one of them into a live result turns that row's output NaN."""
-    bs = case.block_size
-    used = np.zeros(case.num_blocks * bs, dtype=bool)
-    ctx = case.seq_start + case.seq_qlen
-    for s in range(len(ctx)):
-        pos = np.arange(int(ctx[s]))
-        blocks = case.tables[case.table_offset[s] + pos // bs].astype(np.int64)
-        used[blocks * bs + pos % bs] = True
-    for c in (case.k_cache, case.v_cache):
-        if c.dtype == np.uint16:
-            c[~used] = 0x7FC0  # bf16 quiet NaN
-        else:
-            c[~used] = np.nan
-
-
 @pytest.mark.parametrize("kv", ["f32", "bf16", "f16"])
 def test_unused_cache_rows_never_read(gpu, kv):
     """Dead keys of a tile (past a partition's or row's end) are read at a
@@ -517,7 +502,7 @@ def test_unused_cache_rows_never_read(gpu, kv):
     q_len = [1] * 24 + [77, 300]
     for ql in (None, q_len):
         case = make_case(ctx, q_len=ql, num_blocks=4096, seed=11, kv_bf16=kv == "bf16", kv_f16=kv == "f16")
-        _poison_unused(case)
+        poison_unused(case)
         b, qh, _ = run_ragged(case, torch.float32, gpu)
         want = oracle_out(case, qh)
         assert np.isfinite(b).all()

@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from cases import loguniform_ctx, make_case
-from gpu_util import device_q, emulated_bar, i32, max_abs, oracle_out, slices_of, to_dev_cache
+from gpu_util import device_q, emulated_bar, i32, max_abs, oracle_out, poison_unused, slices_of, to_dev_cache
 
 pytestmark = pytest.mark.gpu
 
@@ -101,8 +101,10 @@ def test_f16_random_steps(gpu, seed):
     q_len = np.where(rng.random(S) < 0.3, np.minimum(ctx, rng.integers(2, 200, S)), 1)
     case = make_case(ctx, q_len=q_len, q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim, block_size=bs,
                      num_blocks=int(((ctx + bs - 1) // bs).sum()) + 64, seed=600 + seed, kv_f16=True)
+    poison_unused(case)  # no dead cache row may reach a result
     _, b, qh, plan = run_both(case, torch.float16, gpu, partition_tokens=int(rng.choice([0, 256, 640])))
     want = oracle_out(case, qh)
+    assert np.isfinite(b).all()
     err = max_abs(b, want)
     print(f"seed {seed}: {q_heads}/{kv_heads}x{head_dim} bs {bs} rows {plan.plan.n_tokens} "
           f"parts {plan.plan.n_parts}: max|err| {err:.3e}")
