@@ -381,12 +381,12 @@ void orc_linear(const float* A, int m, int k, const float* B, int n, const float
 }
 
 /* ---------------- cpu_model.cpp:98-214 ---------------- */
-void orc_forward(const orc_model* m, const float* rope_cos, const float* rope_sin,
-                 void* const* k_caches, void* const* v_caches, int kv_bf16,
-                 const int32_t* token_ids, const int32_t* positions, const int32_t* slots,
-                 const int32_t* token_seq, const int32_t* tables, const int32_t* table_offset,
-                 int n_tokens, const int32_t* logit_rows, int n_logits, int block_size,
-                 float* logits, int threads) {
+void orc_forward_trace(const orc_model* m, const float* rope_cos, const float* rope_sin,
+                       void* const* k_caches, void* const* v_caches, int kv_bf16,
+                       const int32_t* token_ids, const int32_t* positions, const int32_t* slots,
+                       const int32_t* token_seq, const int32_t* tables,
+                       const int32_t* table_offset, int n_tokens, const int32_t* logit_rows,
+                       int n_logits, int block_size, float* logits, int threads, float* resid) {
   const int N = n_tokens, H = m->hidden, hd = m->head_dim, nh = m->q_heads, nkv = m->kv_heads,
             I = m->inter, kv_dim = nkv * hd;
   const float scale = 1.0f / sqrtf((float)hd);
@@ -405,6 +405,9 @@ void orc_forward(const orc_model* m, const float* rope_cos, const float* rope_si
 
   for (int i = 0; i < N; i++)
     memcpy(x + (size_t)i * H, m->embed + (size_t)token_ids[i] * H, sizeof(float) * H);
+  /* The residual stream after the embedding and after every layer, as the
+   * reference's per-layer capture records it (test_cpu_model.cpp:112-125). */
+  if (resid) memcpy(resid, x, sizeof(float) * (size_t)N * H);
 
   const int QD = nh * hd;
   for (int l = 0; l < m->layers; l++) {
@@ -436,6 +439,7 @@ void orc_forward(const orc_model* m, const float* rope_cos, const float* rope_si
     orc_silu_mul(gate, up, (size_t)N * I);
     orc_linear(gate, N, I, m->wdown[l], H, NULL, o, threads);
     for (size_t i = 0; i < (size_t)N * H; i++) x[i] += o[i];
+    if (resid) memcpy(resid + (size_t)(l + 1) * N * H, x, sizeof(float) * (size_t)N * H);
   }
 
   if (n_logits > 0) {
@@ -445,4 +449,15 @@ void orc_forward(const orc_model* m, const float* rope_cos, const float* rope_si
     orc_linear(h, n_logits, H, head, m->vocab, NULL, logits, threads);
   }
   free(x); free(h); free(q); free(k); free(v); free(attn); free(o); free(gate); free(up);
+}
+
+void orc_forward(const orc_model* m, const float* rope_cos, const float* rope_sin,
+                 void* const* k_caches, void* const* v_caches, int kv_bf16,
+                 const int32_t* token_ids, const int32_t* positions, const int32_t* slots,
+                 const int32_t* token_seq, const int32_t* tables, const int32_t* table_offset,
+                 int n_tokens, const int32_t* logit_rows, int n_logits, int block_size,
+                 float* logits, int threads) {
+  orc_forward_trace(m, rope_cos, rope_sin, k_caches, v_caches, kv_bf16, token_ids, positions,
+                    slots, token_seq, tables, table_offset, n_tokens, logit_rows, n_logits,
+                    block_size, logits, threads, NULL);
 }

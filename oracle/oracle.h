@@ -131,6 +131,16 @@ void orc_forward(const orc_model* m, const float* rope_cos, const float* rope_si
                  int n_tokens, const int32_t* logit_rows, int n_logits, int block_size,
                  float* logits, int threads);
 
+/* orc_forward that also records the residual stream: resid, when not NULL,
+ * receives [layers+1][n_tokens][hidden] floats (after the embedding, then
+ * after each layer), the capture of test_cpu_model.cpp:112-125. */
+void orc_forward_trace(const orc_model* m, const float* rope_cos, const float* rope_sin,
+                       void* const* k_caches, void* const* v_caches, int kv_bf16,
+                       const int32_t* token_ids, const int32_t* positions, const int32_t* slots,
+                       const int32_t* token_seq, const int32_t* tables,
+                       const int32_t* table_offset, int n_tokens, const int32_t* logit_rows,
+                       int n_logits, int block_size, float* logits, int threads, float* resid);
+
 #ifdef __cplusplus
 }
 #endif

@@ -66,6 +66,7 @@ def lib() -> ctypes.CDLL:
         L.orc_argmax.argtypes = [_P, _i]
         L.orc_forward.argtypes = [_P, _P, _P, _P, _P, _i, _P, _P, _P, _P, _P, _P, _i, _P, _i, _i,
                                   _P, _i]
+        L.orc_forward_trace.argtypes = L.orc_forward.argtypes + [_P]
         _lib = L
     return _lib
 

@@ -49,6 +49,11 @@ class OracleModel:
         self.vp = (P * n)(*[c.ctypes.data for c in self.vc])
 
     def logits(self, slices):
+        return self.trace(slices, resid=False)[0]
+
+    def trace(self, slices, resid=True):
+        """Logits of the step's logit rows and, with resid, the residual
+        stream [layers+1][tokens][hidden] (orc_forward_trace)."""
         pk = oracle.pack_step([(s.seq_key, s.start, s.len, s.needs_logits,
                                 np.ctypeslib.as_array(ctypes.cast(s.blocks, ctypes.POINTER(ctypes.c_int32)), (s.num_blocks,)),
                                 np.ctypeslib.as_array(ctypes.cast(s.tokens, ctypes.POINTER(ctypes.c_int32)), (s.start + s.len,)))
@@ -56,11 +61,14 @@ class OracleModel:
         R = len(pk.logit_rows)
         out = np.zeros((max(R, 1), self.a["vocab"]), np.float32)
         pt = oracle.ptr
-        oracle.lib().orc_forward(ctypes.byref(self.m), pt(self.cos), pt(self.sin), self.kp, self.vp,
-                                 int(self.kv_bf16), pt(pk.token_ids), pt(pk.positions), pt(pk.slots),
-                                 pt(pk.token_seq), pt(pk.tables), pt(pk.table_offset),
-                                 len(pk.token_ids), pt(pk.logit_rows), R, self.bs, pt(out), self.threads)
-        return out[:R]
+        N = len(pk.token_ids)
+        res = np.zeros((self.a["layers"] + 1, N, self.a["hidden"]), np.float32) if resid else None
+        oracle.lib().orc_forward_trace(ctypes.byref(self.m), pt(self.cos), pt(self.sin), self.kp, self.vp,
+                                       int(self.kv_bf16), pt(pk.token_ids), pt(pk.positions), pt(pk.slots),
+                                       pt(pk.token_seq), pt(pk.tables), pt(pk.table_offset), N,
+                                       pt(pk.logit_rows), R, self.bs, pt(out), self.threads,
+                                       None if res is None else pt(res))
+        return out[:R], res
 
     def forward(self, slices, n_logits):
         lg = self.logits(slices)

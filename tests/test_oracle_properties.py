@@ -173,3 +173,44 @@ def test_pack_step_repeated_sequence_shares_one_table():
     assert list(got.tables) == list(t) + list(u)
     assert list(got.table_offset) == [0, 5]
     assert list(got.logit_rows) == [4, 5]
+
+
+def _bf16_rne(x):
+    """fp32 -> bf16 bits from the format's definition: round to nearest,
+    ties to even, on the top 16 bits; NaN stays NaN (quiet bit set)."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = np.isnan(x)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+@pytest.mark.parametrize("cache", ["f32", "bf16"])
+def test_store_kv_closed_form(cache):
+    """store_kv.cu:20-36: row t of k and v lands at row slots[t] of the
+    caches, tokens in order (a repeated slot keeps the last token's row),
+    and no other row changes. bf16 rows are the round-to-nearest-even of
+    the fp32 rows, computed here from the bit pattern."""
+    rng = np.random.default_rng(5)
+    n, kv_dim, slots_total = 40, 24, 128
+    k = rng.standard_normal((n, kv_dim)).astype(np.float32)
+    v = rng.standard_normal((n, kv_dim)).astype(np.float32)
+    k[0, :4] = [np.inf, -np.inf, 0.0, -0.0]
+    k[1, 0] = np.float32(1.0 + 2.0 ** -8)  # a tie between two bf16 values: rounds to even
+    k[1, 1] = np.float32(1.0 + 3 * 2.0 ** -8)  # a tie that rounds up
+    slots = rng.choice(slots_total, n, replace=False).astype(np.int32)
+    slots[-1] = slots[3]  # a repeated slot: the later token wins
+    dt = np.float32 if cache == "f32" else np.uint16
+    kc = np.full((slots_total, kv_dim), 7, dt)
+    vc = np.full((slots_total, kv_dim), 9, dt)
+    oracle.store_kv(k, v, slots, kc, vc)
+    conv = (lambda x: x) if cache == "f32" else _bf16_rne
+    want_k = np.full_like(kc, 7)
+    want_v = np.full_like(vc, 9)
+    for t in range(n):
+        want_k[slots[t]] = conv(k[t])
+        want_v[slots[t]] = conv(v[t])
+    assert np.array_equal(kc.view(np.uint8), want_k.view(np.uint8))
+    assert np.array_equal(vc.view(np.uint8), want_v.view(np.uint8))
+    if cache == "bf16":
+        assert kc[slots[1], 0] == 0x3F80 and kc[slots[1], 1] == 0x3F82
