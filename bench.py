@@ -484,7 +484,7 @@ def main():
     ap.add_argument("--no-extra-workloads", action="store_true",
                     help="skip the target, target_f32 and config3 sub-measurements of a config2 run")
     ap.add_argument("--partition", type=int, default=0, help="decode partition tokens (0 = planner's choice)")
-    ap.add_argument("--flags", type=int, default=0, help="le_plan_config.flags (1 = LE_PLAN_WRITE_THROUGH, 2 = LE_PLAN_TWO_LAUNCHES)")
+    ap.add_argument("--flags", type=int, default=0, help="le_plan_config.flags (2 = LE_PLAN_TWO_LAUNCHES)")
     ap.add_argument("--chunk-partition", type=int, default=0,
                     help="chunk-row key partition tokens (0 = planner's choice)")
     ap.add_argument("--calibrate-copy", action="store_true",

@@ -113,19 +113,14 @@ void le_model_destroy(le_model* m);
  * replays so far. */
 int le_model_set_decode_graph(le_model* m, int enable);
 int64_t le_model_graph_replays(const le_model* m);
+/* Decode steps that ran eagerly although graph replay was on: the step's
+ * fixed-layout plan was rejected (a table longer than max_pos allows) or
+ * the capture failed (after which every step runs eagerly). */
+int64_t le_model_eager_fallbacks(const le_model* m);
 
-/* Every step copies the device's XCD misplacement counter back with its
- * tokens (see le_xcd_misplacements in llm_engine_amd.h). A nonzero count means
- * a split row's merge found its partitions on different XCDs and wrote NaN
- * instead of its output (and so did the K/V of later layers of that step):
- * the model then clears the counter, which switches the device to
- * write-through partials, drops its captured graphs and runs the same step
- * again before returning its tokens. le_model_placement_reruns counts such
- * re-runs. le_model_set_plan_flags passes le_plan_config.flags to the model's
- * plans (LE_PLAN_WRITE_THROUGH, LE_PLAN_TWO_LAUNCHES, or
- * LE_PLAN_SIMULATE_MISPLACEMENT to exercise the re-run in tests). */
+/* le_model_set_plan_flags passes le_plan_config.flags to the model's plans
+ * (LE_PLAN_TWO_LAUNCHES: the tests check that launch shape end to end). */
 int le_model_set_plan_flags(le_model* m, int32_t flags);
-int64_t le_model_placement_reruns(const le_model* m);
 
 
 /* One step: slices in scheduler order. tokens_out receives the greedy token

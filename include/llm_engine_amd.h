@@ -162,15 +162,10 @@ typedef struct le_plan_config {
                                   depend only on the row count */
 } le_plan_config;
 
-/* le_plan_config.flags. The first two select slower, equivalent launches;
- * the tests use them to check that every launch shape gives the same result. */
-#define LE_PLAN_WRITE_THROUGH 1 /* split rows exchange partials through write-through
-                                   stores, without relying on the XCD placement */
+/* le_plan_config.flags. It selects a slower, equivalent launch shape; the
+ * tests use it to check that every launch shape gives the same result. */
 #define LE_PLAN_TWO_LAUNCHES 2  /* a mixed step runs its decode and chunk rows as two
                                    launches instead of one */
-#define LE_PLAN_SIMULATE_MISPLACEMENT 4 /* fault injection for tests of the placement
-                                   guard (le_xcd_misplacements): workgroups whose linear
-                                   bits 3 and 4 differ report another XCD */
 
 typedef struct le_step_plan {
   le_plan_config cfg;
@@ -248,30 +243,6 @@ int le_ragged_paged_attention_noalloc(const void* q, le_dtype act_dtype, const v
                                       const le_step_plan* plan, float scale, void* out, hipStream_t stream);
 
 /* ------------------------------------------------------------------------
- * XCD placement guard. No counterpart in the reference (its GPU has one L2).
- * A plan launch places all partitions of a split row on one XCD: the
- * device deals a launch's workgroups to its 8 XCDs round robin, so
- * workgroups whose ids are equal modulo 8 share an XCD (wherever the deal
- * starts), and the partitions exchange their partials through that XCD's L2
- * with plain stores. The dealing is probed once per device (first plan
- * launch with split rows, outside stream capture); if it is not round robin,
- * partials are stored write-through and placement plays no part. Every
- * partition also reports its XCD (HW_REG_XCC_ID, relative to its id) when it
- * arrives, and the last to arrive merges only if all partitions shared its
- * XCD; otherwise it writes NaN over its outputs instead of a wrong value and
- * counts the event. So results are correct or NaN, never silently wrong.
- *
- * le_xcd_misplacements reads and clears the current device's count of split
- * rows found spread over XCDs (synchronises `stream`); a nonzero count
- * switches the device to write-through partials for the rest of the
- * process. le_xcd_placement_recheck forgets the probe result of the current
- * device, so the next plan launch probes again: call it after changing the
- * device's compute partitioning or the CU masks of the streams in use.
- * ------------------------------------------------------------------------ */
-int le_xcd_misplacements(hipStream_t stream, int64_t* count);
-void le_xcd_placement_recheck(void);
-
-/* ------------------------------------------------------------------------
  * (2)+(3) The scatter and the attention of a step in one call.
  * Equals le_kv_cache_write(k_new, v_new, new_dtype, <plan slots>, k_cache,
  * v_cache, kv_dtype, n_tokens, kv_heads*head_dim, num_cache_blocks*block_size)
@@ -310,6 +281,39 @@ int le_ragged_paged_attention_qkv(const void* qkv, le_dtype act_dtype, int64_t q
                                   int64_t num_cache_blocks, const le_step_plan* plan, float scale,
                                   void* out, void* q_scratch, void* workspace, size_t workspace_bytes,
                                   hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * The layer ops between the GEMMs and attention, for any element type.
+ * The reference launches them one by one (cuda_kernels.h:17-40, called at
+ * cuda_model.cu:347-390); the device model here fuses them (residual add
+ * with the next norm, bias and RoPE with the cache write), and these entry
+ * points let the reference's own call sequence run unchanged (the
+ * le_cuda_kernels.h bridge). Arithmetic is fp32 with one rounding to the
+ * element type per stored value, as the reference's kernels do. Return 0,
+ * a negative le_status for a rejected argument (nothing launched), or the
+ * launch's hipError_t.
+ * ------------------------------------------------------------------------ */
+/* out[t][j] = table[ids[t]][j] (launch_embedding, cuda_kernels.h:17-18). */
+int le_embedding(const void* table, le_dtype dtype, const int32_t* ids, void* out, int n_tokens,
+                 int hidden, hipStream_t stream);
+/* out[r][j] = x[r][j] / sqrt(mean_j x[r][j]^2 + eps) * weight[j], fp32 weight
+ * (launch_rmsnorm, cuda_kernels.h:20-23). */
+int le_rmsnorm(const void* x, le_dtype dtype, const float* weight, void* out, int rows, int cols,
+               float eps, hipStream_t stream);
+/* gate[i] = silu(gate[i]) * up[i] in place (launch_silu_mul, cuda_kernels.h:25-26). */
+int le_silu_mul(void* gate, const void* up, le_dtype dtype, size_t n, hipStream_t stream);
+/* Rotary embedding in place, rotate_half pairing, over x[n_tokens][row_stride]'s
+ * first `heads` heads (launch_rope, cuda_kernels.h:28-33). cos/sin tables are
+ * [max_pos][head_dim/2] fp32; a token whose position is outside [0, max_pos)
+ * is left unchanged (max_pos <= 0: positions are not bounded, as in the
+ * reference). */
+int le_rope(void* x, le_dtype dtype, const int32_t* positions, const float* cos_table,
+            const float* sin_table, int max_pos, int n_tokens, int heads, int head_dim,
+            int row_stride, hipStream_t stream);
+/* x[i] += y[i] (launch_add_inplace, cuda_kernels.h:35-36). */
+int le_add_inplace(void* x, const void* y, le_dtype dtype, size_t n, hipStream_t stream);
+/* x[r][c] += bias[c], fp32 bias (launch_add_bias, cuda_kernels.h:38-39). */
+int le_add_bias(void* x, le_dtype dtype, const float* bias, int rows, int cols, hipStream_t stream);
 
 #ifdef __cplusplus
 }

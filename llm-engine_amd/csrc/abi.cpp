@@ -225,10 +225,6 @@ int ragged_attention(const void* q, le_dtype act_dtype, const void* k_new, const
   d.n_rows = plan->n_decode_items; d.nsplit = 1;
   d.q_heads = cfg.q_heads; d.kv_heads = cfg.kv_heads; d.head_dim = cfg.head_dim;
   d.block_size = cfg.block_size; d.scale_log2 = scale_log2; d.num_cache_blocks = num_cache_blocks;
-  d.l2_local = plan->n_parts > 0 && !(cfg.flags & LE_PLAN_WRITE_THROUGH) && le::xcd_placement_holds(stream);
-  if (d.l2_local) d.parts.misplaced = le::xcd_miss_counter();
-  if (!d.parts.misplaced) d.l2_local = 0;
-  if (d.l2_local && (cfg.flags & LE_PLAN_SIMULATE_MISPLACEMENT)) d.l2_local = le::kL2LocalSimulateMisses;
   const int64_t num_slots = num_cache_blocks * cfg.block_size;
   hipError_t e = hipSuccess;
   if (k_new) {
@@ -265,8 +261,6 @@ int ragged_attention(const void* q, le_dtype act_dtype, const void* k_new, const
   c.q_heads = cfg.q_heads; c.kv_heads = cfg.kv_heads; c.head_dim = cfg.head_dim;
   c.block_size = cfg.block_size; c.scale_log2 = scale_log2;
   c.num_cache_blocks = num_cache_blocks;
-  c.l2_local = d.l2_local;
-  c.parts.misplaced = d.parts.misplaced;
   // A mixed step is one launch (chunk and decode workgroups in one grid);
   // LE_PLAN_TWO_LAUNCHES runs the two kernels one after the other instead.
   const bool two_launches = (cfg.flags & LE_PLAN_TWO_LAUNCHES) != 0;
@@ -281,13 +275,6 @@ int ragged_attention(const void* q, le_dtype act_dtype, const void* k_new, const
 }  // namespace
 
 extern "C" {
-
-int le_xcd_misplacements(hipStream_t stream, int64_t* count) {
-  if (!count) return LE_EINVAL;
-  return hip_status(le::xcd_misplacements(stream, count));
-}
-
-void le_xcd_placement_recheck(void) { le::xcd_placement_recheck(); }
 
 int le_ragged_paged_attention(const void* q, le_dtype act_dtype, const void* k_cache,
                               const void* v_cache, le_dtype kv_dtype, int64_t num_cache_blocks,

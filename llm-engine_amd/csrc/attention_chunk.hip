@@ -10,7 +10,6 @@ namespace {
 template <typename ACT, typename KV, int HD>
 __global__ __launch_bounds__(chk::kThreads) void chunk_kernel(ChunkParams p) {
   __shared__ chk::ChunkSmem<KV, HD> sm;
-  p.lin = blockIdx.x + blockIdx.y * p.n_items;
   chk::chunk_wg<ACT, KV, HD>(p, sm, blockIdx.x, blockIdx.y);
 }
 

@@ -599,38 +599,26 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
           if constexpr (kHalfPartials<KV>) {
             const uint32_t off = static_cast<uint32_t>(((rec - rec_tile) * HD + d * 16 + grp * 4) * 2);
             const uint2 v = make_uint2(pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3]));
-            if (p.l2_local) st_l2_8(acc_rsrc, off, v);
-            else st_coherent8(acc_rsrc, off, v);
+            st_coherent8(acc_rsrc, off, v);
           } else {
             const uint32_t off = static_cast<uint32_t>(((rec - rec_tile) * HD + d * 16 + grp * 4) * 4);
             const f32x4v v = __builtin_bit_cast(f32x4v, o);
-            if (p.l2_local) st_l2_16(acc_rsrc, off, v);
-            else st_coherent16(acc_rsrc, off, v);
+            st_coherent16(acc_rsrc, off, v);
           }
         }
         if (grp == 0) {
-          if (p.l2_local) {
-            reinterpret_cast<float2*>(ml)[rec] = make_float2(m_run[rs], l_tot[rs]);
-          } else {
-            st_dev(ml + rec * 2, m_run[rs]);
-            st_dev(ml + rec * 2 + 1, l_tot[rs]);
-          }
+          st_dev(ml + rec * 2, m_run[rs]);
+          st_dev(ml + rec * 2 + 1, l_tot[rs]);
         }
       }
     }
   }
-  const int rot = p.l2_local ? xcd_rotation(p.l2_local, p.lin) : 0;
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are performed
   __syncthreads();                // ... and every other thread's
   arrival_t* counter = p.parts.counters + static_cast<int64_t>(tok0) * p.kv_heads + kvh;
   if (tid == 0) {
-    const arrival_t mine = arrival_token(rot);
-    const arrival_t seen = __hip_atomic_fetch_add(counter, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const bool is_last = arrival_count(seen) == it.part_stride - 1;
-    // partials left in another XCD's L2 are out of reach: poison the tile
-    const bool apart = is_last && p.l2_local && !arrivals_colocated(seen + mine, rot);
-    if (apart) __hip_atomic_fetch_add(p.parts.misplaced, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last = !is_last ? 0 : (apart ? 2 : 1);
+    const arrival_t seen = __hip_atomic_fetch_add(counter, arrival_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = seen == static_cast<arrival_t>(it.part_stride - 1);
   }
   __syncthreads();
   if (!last) return;
@@ -641,13 +629,7 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
   const int base = it.part0 - it.part;
   // Rounds of loads as wide as the tile's partition count (up to 6 for hd
   // 64), so no load is issued twice.
-  if (last == 2) {
-    for (int i = tid; i < nq * G * HD; i += kThreads) {
-      const int r = i / (G * HD), j = i - r * (G * HD);
-      elem<ACT>::store1(static_cast<ACT*>(p.out) + (static_cast<int64_t>(tok0 + r) * p.q_heads + kvh * G) * HD + j,
-                        __builtin_nanf(""));
-    }
-  } else if constexpr (HD == 64) {
+  if constexpr (HD == 64) {
     if (J <= 4) merge_tile<ACT, HD, 4, kHalfPartials<KV>>(p, it, acc_rsrc, ml, rec_tile, base, J, G, kvh, nq, tok0);
     else merge_tile<ACT, HD, 6, kHalfPartials<KV>>(p, it, acc_rsrc, ml, rec_tile, base, J, G, kvh, nq, tok0);
   } else {

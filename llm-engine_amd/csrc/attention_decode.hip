@@ -4,8 +4,6 @@
 // the fused ragged kernel (attention_ragged.hip) shares.
 #include "attention_decode_wg.h"
 
-#include <atomic>
-
 namespace le {
 namespace {
 
@@ -15,7 +13,6 @@ constexpr int kMfmaThreads = kMfmaWaves * 64;
 template <typename ACT, typename KV, int HD>
 __global__ __launch_bounds__(kMfmaThreads) void mfma_kernel(DecodeParams p) {
   __shared__ dec::DecodeSmem<KV, HD, kMfmaWaves> sm;
-  p.lin = blockIdx.x + blockIdx.y * p.n_rows;  // used with items only (2-D grid)
   dec::decode_wg<ACT, KV, HD, kMfmaWaves>(p, sm, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
@@ -29,98 +26,6 @@ hipError_t launch(const DecodeParams& p, hipStream_t s) {
 
 }  // namespace
 
-
-namespace {
-__global__ void xcd_probe_kernel(int* out) {
-  if (threadIdx.x == 0) {
-    unsigned v;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
-    out[blockIdx.x + blockIdx.y * gridDim.x] = static_cast<int>(v & 0xf);
-  }
-}
-
-constexpr int kProbeW = 1000, kProbeH = 2;
-__device__ int g_xcd_probe[kProbeW * kProbeH];  // static: the check allocates nothing
-
-// 1-D and 2-D grids of the sizes decode launches use, wider than the chip.
-int probe_placement(hipStream_t stream) {
-  int* d = nullptr;
-  if (hipGetSymbolAddress(reinterpret_cast<void**>(&d), HIP_SYMBOL(g_xcd_probe)) != hipSuccess) return 0;
-  int h[kProbeW * kProbeH];  // the caller's own copy: concurrent probes of two devices do not share it
-  bool ok = true;
-  for (int shape = 0; shape < 2 && ok; shape++) {
-    const dim3 grid = shape == 0 ? dim3(kProbeW * kProbeH) : dim3(kProbeW, kProbeH);
-    xcd_probe_kernel<<<grid, 64, 0, stream>>>(d);
-    ok = hipGetLastError() == hipSuccess &&
-         hipMemcpyAsync(h, d, sizeof(h), hipMemcpyDeviceToHost, stream) == hipSuccess &&
-         hipStreamSynchronize(stream) == hipSuccess;
-    // round robin from any starting XCD: ids equal modulo 8 share an XCD
-    for (int i = 0; ok && i < kProbeW * kProbeH; i++) ok = h[i] == (h[0] + i) % 8;
-  }
-  return ok ? 1 : 0;
-}
-}  // namespace
-
-namespace {
-constexpr int kMaxDevices = 64;
-std::atomic<int> g_placement[kMaxDevices];  // 0 unknown, 1 holds, 2 does not
-
-__device__ int32_t g_xcd_misses;  // static: one per device, zero at load
-
-int current_device() {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return -1;
-  return dev;
-}
-}  // namespace
-
-bool xcd_placement_holds(hipStream_t stream) {
-  const int dev = current_device();
-  if (dev < 0) return false;
-  int st = g_placement[dev].load();
-  if (st == 0) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
-      return false;  // no probe inside a capture; the coherent stores are correct anywhere
-    st = probe_placement(stream) && xcd_miss_counter() ? 1 : 2;
-    g_placement[dev].store(st);
-  }
-  return st == 1;
-}
-
-int32_t* xcd_miss_counter() {
-  static std::atomic<int32_t*> ptr[kMaxDevices];
-  const int dev = current_device();
-  if (dev < 0) return nullptr;
-  int32_t* d = ptr[dev].load();
-  if (!d) {
-    if (hipGetSymbolAddress(reinterpret_cast<void**>(&d), HIP_SYMBOL(g_xcd_misses)) != hipSuccess) return nullptr;
-    ptr[dev].store(d);
-  }
-  return d;
-}
-
-void xcd_placement_recheck() {
-  const int dev = current_device();
-  if (dev >= 0) g_placement[dev].store(0);
-}
-
-hipError_t xcd_misplacements(hipStream_t stream, int64_t* count) {
-  *count = 0;
-  const int dev = current_device();
-  int32_t* d = xcd_miss_counter();
-  if (dev < 0 || !d) return hipErrorInvalidDevice;
-  int32_t h = 0;
-  hipError_t e = hipMemcpyAsync(&h, d, sizeof(h), hipMemcpyDeviceToHost, stream);
-  if (e == hipSuccess) e = hipStreamSynchronize(stream);
-  if (e == hipSuccess && h != 0) {
-    g_placement[dev].store(2);
-    e = hipMemsetAsync(d, 0, sizeof(h), stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(stream);
-  }
-  *count = h;
-  return e;
-}
 
 int decode_nsplit(int n_tokens, int kv_heads) {
   const int rows = n_tokens * kv_heads;

@@ -181,16 +181,12 @@ __device__ __forceinline__ void store_new_row(const DecodeParams& p, const Work&
   elem<C>::store8(static_cast<C*>(const_cast<void*>(which ? p.v_cache : p.k_cache)) + dst, v);
 }
 
-// Partials cross workgroups through loads that miss the CU's L1 (the sc1
-// policy of agent-scope relaxed atomics), so a merging workgroup never reads
-// a stale L1 line. Where they are stored depends on the launch. Without a
-// plan, a row's splits run on different XCDs, whose L2s are not coherent
-// with each other, so partials are stored write-through (sc1) to the
-// coherence point. With a plan, every partition of a row runs on one XCD
-// (the plan places them at workgroup ids equal modulo 8, and the dispatcher
-// sends workgroup i to XCD i % 8), so plain stores into that XCD's L2 are
-// enough: 28.9 -> 28.6 us on 64 rows x 4096 keys. Agent-scope fences are
-// avoided either way: they write back the whole L2 of the XCD.
+// Partials cross workgroups, possibly on different XCDs, whose L2s are not
+// coherent with each other: they are stored write-through (the sc1 policy of
+// agent-scope relaxed atomics) to the coherence point, and read back with
+// loads that miss the CU's L1 and the XCD's L2, so a merging workgroup never
+// reads a stale line. Agent-scope fences are avoided: they write back the
+// whole L2 of the XCD.
 __device__ __forceinline__ void st_dev(float* p, float v) {
   __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
@@ -260,16 +256,10 @@ __device__ __forceinline__ void write_piece(const DecodeParams& p, const Work& w
   const int64_t rec0 = static_cast<int64_t>(w.part) * p.q_heads + kvh * G;
   float* ml = reinterpret_cast<float*>(p.parts.ml);
   const __amdgpu_buffer_rsrc_t r = coherent_rsrc(p.parts.acc + rec0 * HD);
-  const bool first = c * 4 - g * HD == 0;  // the head's first piece also writes (m, l)
-  if (p.l2_local) {  // partitions of the row share this XCD's L2
-    st_l2_16(r, static_cast<uint32_t>(c * 16), o);
-    if (first) reinterpret_cast<float2*>(ml)[rec0 + g] = make_float2(M, Ls);
-  } else {
-    st_coherent16(r, static_cast<uint32_t>(c * 16), o);
-    if (first) {
-      st_dev(ml + (rec0 + g) * 2, M);
-      st_dev(ml + (rec0 + g) * 2 + 1, Ls);
-    }
+  st_coherent16(r, static_cast<uint32_t>(c * 16), o);
+  if (c * 4 - g * HD == 0) {  // the head's first piece also writes (m, l)
+    st_dev(ml + (rec0 + g) * 2, M);
+    st_dev(ml + (rec0 + g) * 2 + 1, Ls);
   }
 }
 
@@ -282,18 +272,12 @@ __device__ __forceinline__ void arrive_and_merge(const DecodeParams& p, const Wo
   const int n4 = G * HD / 4;
   const int64_t head0 = static_cast<int64_t>(w.token) * p.q_heads + kvh * G;
   float* ml = reinterpret_cast<float*>(p.parts.ml);
-  const int rot = p.l2_local ? xcd_rotation(p.l2_local, p.lin) : 0;
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are performed
   __syncthreads();                // ... and every other thread's
   arrival_t* counter = p.parts.counters + static_cast<int64_t>(w.token) * p.kv_heads + kvh;
   if (tid == 0) {
-    const arrival_t mine = arrival_token(rot);
-    const arrival_t seen = __hip_atomic_fetch_add(counter, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const bool last = arrival_count(seen) == w.n_parts - 1;
-    // partials left in another XCD's L2 are out of reach: poison the output
-    const bool apart = last && p.l2_local && !arrivals_colocated(seen + mine, rot);
-    if (apart) __hip_atomic_fetch_add(p.parts.misplaced, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *flag = !last ? 0 : (apart ? 2 : 1);
+    const arrival_t seen = __hip_atomic_fetch_add(counter, arrival_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag = seen == static_cast<arrival_t>(w.n_parts - 1);
   }
   __syncthreads();
   if (!*flag) return;
@@ -304,10 +288,7 @@ __device__ __forceinline__ void arrive_and_merge(const DecodeParams& p, const Wo
   const __amdgpu_buffer_rsrc_t r = coherent_rsrc(p.parts.acc + rbase * HD);
   // Batches as wide as the row's partition count (up to kMergeBatch), so no
   // load is issued twice.
-  if (*flag == 2) {
-    ACT* out = static_cast<ACT*>(p.out) + head0 * HD;
-    for (int i = tid; i < G * HD; i += NTHR) elem<ACT>::store1(out + i, __builtin_nanf(""));
-  } else if (np <= kMergeBatch / 2) {
+  if (np <= kMergeBatch / 2) {
     merge_parts<ACT, HD, NTHR, kMergeBatch / 2>(p, r, ml, rbase, np, n4, head0);
   } else {
     merge_parts<ACT, HD, NTHR, kMergeBatch>(p, r, ml, rbase, np, n4, head0);

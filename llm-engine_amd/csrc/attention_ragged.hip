@@ -34,7 +34,6 @@ __global__ __launch_bounds__(kRaggedThreads) void ragged_kernel(DecodeParams dp,
   __shared__ RaggedSmem<KV, HD> sm;
   const int n_chunk_wg = cp.n_items * cp.kv_heads;
   const int b = blockIdx.x;
-  dp.lin = cp.lin = b;
   if (b < n_chunk_wg) {
     // item-major within each kv head, as the chunk kernel's 2-D grid (the
     // plan places a split tile's partitions at item indices equal modulo 8)

@@ -71,17 +71,24 @@ struct Generation {
   uint64_t value = 0;
 };
 
+// Thrown by a step buffer that would have to grow while the step's stream is
+// being captured (allocating and clearing memory are not capturable): the
+// capture is abandoned and the step runs eagerly.
+struct GrowthDuringCapture {};
+
 // Device buffer that grows on demand and is then reused across steps.
 struct DevBuf {
   void* p = nullptr;
   size_t cap = 0;
   Generation* gen = nullptr;
+  const bool* capturing = nullptr;
   DevBuf() = default;
   DevBuf(const DevBuf&) = delete;
   DevBuf& operator=(const DevBuf&) = delete;
   ~DevBuf() { if (p) (void)hipFree(p); }
   void* get(size_t bytes, bool zero = false, hipStream_t s = nullptr) {
     if (bytes > cap) {
+      if (capturing && *capturing) throw GrowthDuringCapture{};
       if (p) hip_ok(hipFree(p), "hipFree");
       p = nullptr;
       hip_ok(hipMalloc(&p, bytes), "hipMalloc");
@@ -131,8 +138,8 @@ class Model {
   void forward(const le_step_slice* slices, int n_slices, int32_t* tokens_out, float* logits_out);
   void set_decode_graph(bool on) { graph_on_ = on; }
   void set_plan_flags(int flags) { plan_flags_ = flags; graphs_clear(); }
-  int64_t placement_reruns() const { return placement_reruns_; }
   int64_t graph_replays() const { return graph_replays_; }
+  int64_t eager_fallbacks() const { return eager_fallbacks_; }
   int num_blocks() const { return num_blocks_; }
   double plan_seconds() const { return plan_seconds_; }
   int block_size() const { return bs_; }
@@ -145,14 +152,14 @@ class Model {
   // The device work of a step on stream_, from the plan upload to the token
   // read-back into the pinned tokens buffer (nothing synchronises).
   void enqueue_step(le_step_plan& plan, const void* host_plan, float* logits_out);
+  // Grows every step buffer enqueue_step uses to this plan's sizes (and
+  // clears a new workspace), so that a capture of the same plan allocates
+  // nothing.
+  void size_buffers(const le_step_plan& plan);
   bool forward_graph(const le_step_slice* slices, int n_slices, int32_t* tokens_out);
-  // After a step's sync: true if some split row's partitions were found on
-  // different XCDs during the step (the misplacement counter, copied back
-  // with the tokens, is nonzero). Such a merge wrote NaN instead of its
-  // output, so the caller runs the step again: the counter is read and
-  // cleared, which switches the device to write-through partials, and the
-  // captured graphs (which hold the L2 exchange) are dropped.
-  bool step_poisoned();
+  // The captured-graph path is not available: this step and every later one
+  // run eagerly.
+  void eager_fallback(le_step_plan& plan, const void* host, int n_slices, int32_t* tokens_out);
   void graphs_clear();
 
   le_model_desc d_;
@@ -171,10 +178,9 @@ class Model {
   std::vector<Layer> layers_;
   std::vector<void*> kc_, vc_;
   DevBuf x_, h_, qkv_, q_, attn_, o_, gate_up_, act_buf_, logits_, tokens_, plan_dev_, ws_;
-  HostBuf plan_host_, tokens_host_, miss_host_;
-  int32_t* miss_dev_ = nullptr;  // the device's misplacement counter (static device array)
+  HostBuf plan_host_, tokens_host_;
   int plan_flags_ = 0;
-  int64_t placement_reruns_ = 0;
+  bool capturing_ = false;  // stream_ is being captured: step buffers must not grow
   // Decode graphs: per row count, the whole decode step captured once (after
   // one eager run of the same layout) and replayed while the buffers stay.
   struct DecodeGraph {
@@ -185,7 +191,7 @@ class Model {
   };
   Generation gen_;
   bool graph_on_ = false, graph_failed_ = false;
-  int64_t graph_replays_ = 0;
+  int64_t graph_replays_ = 0, eager_fallbacks_ = 0;
   std::map<int, DecodeGraph> graphs_;
 };
 
@@ -208,9 +214,11 @@ Model::Model(const le_model_desc& d, int num_blocks, int block_size) : d_(d) {
   num_blocks_ = num_blocks;
   act_ = bf16_ ? 2 : 4;
   if (nh_ % nkv_ != 0 || hd_ % 2 != 0) throw std::invalid_argument("head layout");
-  for (DevBuf* b : {&x_, &h_, &qkv_, &q_, &attn_, &o_, &gate_up_, &act_buf_, &logits_, &tokens_, &plan_dev_, &ws_})
+  for (DevBuf* b : {&x_, &h_, &qkv_, &q_, &attn_, &o_, &gate_up_, &act_buf_, &logits_, &tokens_, &plan_dev_, &ws_}) {
     b->gen = &gen_;
-  for (HostBuf* b : {&plan_host_, &tokens_host_, &miss_host_}) b->gen = &gen_;
+    b->capturing = &capturing_;
+  }
+  for (HostBuf* b : {&plan_host_, &tokens_host_}) b->gen = &gen_;
   hip_ok(hipStreamCreate(&stream_), "hipStreamCreate");
   blas_ok(rocblas_create_handle(&blas_), "rocblas_create_handle");
   blas_ok(rocblas_set_stream(blas_, stream_), "rocblas_set_stream");
@@ -263,8 +271,6 @@ Model::Model(const le_model_desc& d, int num_blocks, int block_size) : d_(d) {
     kc_.push_back(base);
     vc_.push_back(base + cache_bytes);
   }
-  miss_dev_ = le::xcd_miss_counter();
-  if (miss_dev_) *static_cast<int32_t*>(miss_host_.get(4)) = 0;
   hip_ok(hipStreamSynchronize(stream_), "sync");
 }
 
@@ -272,16 +278,6 @@ void Model::graphs_clear() {
   for (auto& [n, g] : graphs_)
     if (g.exec) (void)hipGraphExecDestroy(g.exec);
   graphs_.clear();
-}
-
-bool Model::step_poisoned() {
-  if (!miss_dev_ || *static_cast<const int32_t*>(miss_host_.p) == 0) return false;
-  int64_t n = 0;
-  hip_ok(le::xcd_misplacements(stream_, &n), "xcd_misplacements");
-  *static_cast<int32_t*>(miss_host_.p) = 0;
-  graphs_clear();
-  placement_reruns_++;
-  return true;
 }
 
 Model::~Model() {
@@ -349,10 +345,6 @@ void Model::forward(const le_step_slice* slices, int n_slices, int32_t* tokens_o
   if (plan.n_tokens == 0) return;
   enqueue_step(plan, host, logits_out);
   hip_ok(hipStreamSynchronize(stream_), "step sync");
-  if (step_poisoned()) {  // once: the device now stores partials write-through
-    enqueue_step(plan, host, logits_out);
-    hip_ok(hipStreamSynchronize(stream_), "step sync");
-  }
   if (tokens_out && plan.n_logits > 0)
     std::memcpy(tokens_out, tokens_host_.p, static_cast<size_t>(plan.n_logits) * 4);
 }
@@ -375,7 +367,10 @@ bool Model::forward_graph(const le_step_slice* slices, int n_slices, int32_t* to
   le_plan_config cfg{nh_, nkv_, hd_, bs_, kv_dt_, kGraphPartition, 0, 0, plan_flags_, cap_blocks};
   le_step_plan plan{};
   int st = le_plan_step(slices, n_slices, &cfg, nullptr, 0, &plan);
-  if (st != LE_ENOSPACE) return false;  // e.g. a table longer than max_pos allows: run eagerly
+  if (st != LE_ENOSPACE) {  // e.g. a table longer than max_pos allows: run eagerly
+    eager_fallbacks_++;
+    return false;
+  }
   DecodeGraph& g = graphs_[n_slices];
   void* host = plan_host_.get(static_cast<size_t>(plan.bytes));
   le_ok(le_plan_step(slices, n_slices, &cfg, host, plan.bytes, &plan), "le_plan_step");
@@ -385,42 +380,39 @@ bool Model::forward_graph(const le_step_slice* slices, int n_slices, int32_t* to
     g = DecodeGraph{};
     enqueue_step(plan, host, nullptr);
     hip_ok(hipStreamSynchronize(stream_), "step sync");
-    if (step_poisoned()) {
-      enqueue_step(plan, host, nullptr);
-      hip_ok(hipStreamSynchronize(stream_), "step sync");
-    }
-    DecodeGraph& g2 = graphs_[n_slices];  // step_poisoned may have cleared the map
-    g2.warm = true;
-    g2.plan_bytes = plan.bytes;
+    g.warm = true;
+    g.plan_bytes = plan.bytes;
   } else {
     if (!g.exec || g.gen != gen_.value) {
       if (g.exec) (void)hipGraphExecDestroy(g.exec);
       g.exec = nullptr;
+      // Every buffer at its size before the capture, outside it.
+      size_buffers(plan);
+      hip_ok(hipStreamSynchronize(stream_), "sync");
       const uint64_t gen0 = gen_.value;
       hipGraph_t graph = nullptr;
       hip_ok(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+      capturing_ = true;
+      bool grew = false;
       try {
         enqueue_step(plan, host, nullptr);
+      } catch (const GrowthDuringCapture&) {
+        grew = true;
       } catch (...) {
+        capturing_ = false;
         (void)hipStreamEndCapture(stream_, &graph);
         if (graph) (void)hipGraphDestroy(graph);
         throw;
       }
+      capturing_ = false;
       const hipError_t ec = hipStreamEndCapture(stream_, &graph);
-      const hipError_t ei = ec == hipSuccess ? hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0) : ec;
+      const hipError_t ei =
+          ec == hipSuccess && !grew ? hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0) : hipErrorUnknown;
       if (graph) (void)hipGraphDestroy(graph);
       if (ei != hipSuccess || gen_.value != gen0) {  // not capturable here: run every step eagerly
         if (g.exec) (void)hipGraphExecDestroy(g.exec);
         g.exec = nullptr;
-        graph_failed_ = true;
-        (void)hipGetLastError();
-        enqueue_step(plan, host, nullptr);
-        hip_ok(hipStreamSynchronize(stream_), "step sync");
-        if (step_poisoned()) {
-          enqueue_step(plan, host, nullptr);
-          hip_ok(hipStreamSynchronize(stream_), "step sync");
-        }
-        if (tokens_out) std::memcpy(tokens_out, tokens_host_.p, static_cast<size_t>(n_slices) * 4);
+        eager_fallback(plan, host, n_slices, tokens_out);
         return true;
       }
       g.gen = gen_.value;
@@ -428,13 +420,42 @@ bool Model::forward_graph(const le_step_slice* slices, int n_slices, int32_t* to
     hip_ok(hipGraphLaunch(g.exec, stream_), "hipGraphLaunch");
     hip_ok(hipStreamSynchronize(stream_), "step sync");
     graph_replays_++;
-    if (step_poisoned()) {  // the graphs are gone: run this step eagerly
-      enqueue_step(plan, host, nullptr);
-      hip_ok(hipStreamSynchronize(stream_), "step sync");
-    }
   }
   if (tokens_out) std::memcpy(tokens_out, tokens_host_.p, static_cast<size_t>(n_slices) * 4);
   return true;
+}
+
+void Model::eager_fallback(le_step_plan& plan, const void* host, int n_slices, int32_t* tokens_out) {
+  graph_failed_ = true;
+  eager_fallbacks_++;
+  (void)hipGetLastError();
+  enqueue_step(plan, host, nullptr);
+  hip_ok(hipStreamSynchronize(stream_), "step sync");
+  if (tokens_out) std::memcpy(tokens_out, tokens_host_.p, static_cast<size_t>(n_slices) * 4);
+}
+
+void Model::size_buffers(const le_step_plan& plan) {
+  const size_t n = static_cast<size_t>(plan.n_tokens);
+  const int QKV = QD_ + 2 * KVD_;
+  plan_dev_.get(static_cast<size_t>(plan.bytes));
+  x_.get(n * H_ * act_);
+  h_.get(n * H_ * act_);
+  qkv_.get(n * QKV * act_);
+  q_.get(n * QD_ * act_);
+  attn_.get(n * QD_ * act_);
+  o_.get(n * H_ * act_);
+  gate_up_.get(n * 2 * I_ * act_);
+  act_buf_.get(n * I_ * act_);
+  const size_t ws_bytes = d_.attention == LE_ATTN_REFERENCE
+                              ? le_attention_decode_workspace_size(plan.n_tokens, nh_, nkv_, hd_)
+                              : le_ragged_workspace_size(&plan);
+  if (ws_bytes) ws_.get(ws_bytes, /*zero=*/true, stream_);
+  const size_t R = static_cast<size_t>(plan.n_logits);
+  if (R > 0) {
+    logits_.get(R * V_ * 4);
+    tokens_.get(R * 4);
+    tokens_host_.get(R * 4);
+  }
 }
 
 void Model::enqueue_step(le_step_plan& plan, const void* host_plan, float* logits_out) {
@@ -514,9 +535,6 @@ void Model::enqueue_step(le_step_plan& plan, const void* host_plan, float* logit
       hip_ok(hipMemcpyAsync(logits_out, logits, static_cast<size_t>(R) * V_ * 4, hipMemcpyDeviceToHost,
                             stream_), "logits");
   }
-  // every step, sampled or not: a poisoned merge also poisons the K/V that
-  // later layers wrote
-  if (miss_dev_) hip_ok(hipMemcpyAsync(miss_host_.p, miss_dev_, 4, hipMemcpyDeviceToHost, stream_), "misplacements");
 }
 
 
@@ -570,12 +588,12 @@ int64_t le_model_graph_replays(const le_model* m) { return m ? m->impl->graph_re
 
 int le_model_set_plan_flags(le_model* m, int32_t flags) {
   if (!m) return LE_EINVAL;
-  if ((flags & ~(LE_PLAN_WRITE_THROUGH | LE_PLAN_TWO_LAUNCHES | LE_PLAN_SIMULATE_MISPLACEMENT)) != 0) return LE_EINVAL;
+  if ((flags & ~LE_PLAN_TWO_LAUNCHES) != 0) return LE_EINVAL;
   m->impl->set_plan_flags(flags);
   return LE_OK;
 }
 
-int64_t le_model_placement_reruns(const le_model* m) { return m ? m->impl->placement_reruns() : 0; }
+int64_t le_model_eager_fallbacks(const le_model* m) { return m ? m->impl->eager_fallbacks() : 0; }
 
 
 int le_argmax_rows(const float* logits, int rows, int vocab, int32_t* out, hipStream_t stream) {

@@ -251,49 +251,11 @@ __device__ __forceinline__ f32x4v ld_coherent16(__amdgpu_buffer_rsrc_t r, uint32
 __device__ __forceinline__ void st_coherent16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, f32x4v v) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4raw, v), r, byte_off, 0, kCachePolicySc1);
 }
-// Split rows of a plan launch are placed so that all partitions of a row
-// share one XCD: the dispatcher deals a launch's workgroups to the XCDs
-// round robin, so workgroups whose linear ids `lin` are equal modulo 8 land
-// on one XCD, and their partials can go through its L2 with plain stores.
-// Where the deal starts is not fixed (it moves with earlier dispatches on
-// the same queue), so the kernels check co-location, not XCD numbers: each
-// partition arrives with its rotation (XCC_ID - lin) mod 8, and the last to
-// arrive merges only if every arrival had its own rotation; otherwise some
-// partial sits in another XCD's L2, and it writes NaN instead of a wrong
-// result (and counts the event). l2_local: 0 off (write-through partials, no
-// check), 1 on, 2 on with fault injection (workgroups whose lin bits 3 and 4 differ
-// report another rotation).
-__device__ __forceinline__ int xcd_rotation(int l2_local, int lin) {
-  unsigned v;
-  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
-  int rot = (static_cast<int>(v & 7) - lin) & 7;
-  if (l2_local == 2 && (((lin >> 3) ^ (lin >> 4)) & 1)) rot ^= 1;
-  return rot;
-}
-// 64-bit arrival counters: the number of arrivals in bits 0..10, the sum of
-// their rotations in bits 11..23 and the sum of squares from bit 24 (at most
-// 1024 partitions per row). All rotations equal r iff both sums equal n*r
-// and n*r*r (zero variance).
+// Arrival counters of split rows: one per (row, kv head), zero between
+// launches (the last arriver resets it).
 typedef unsigned long long arrival_t;
-__device__ __forceinline__ arrival_t arrival_token(int rot) {
-  return 1ull + (static_cast<arrival_t>(rot) << 11) + (static_cast<arrival_t>(rot * rot) << 24);
-}
-__device__ __forceinline__ int arrival_count(arrival_t c) { return static_cast<int>(c & 0x7ff); }
-__device__ __forceinline__ bool arrivals_colocated(arrival_t c, int rot) {
-  const arrival_t n = c & 0x7ff, s1 = (c >> 11) & 0x1fff, s2 = c >> 24;
-  return s1 == n * rot && s2 == n * rot * rot;
-}
 
-// A plain 16-byte store (write-back into the XCD's L2), for data that only
-// workgroups on the same XCD read back.
-__device__ __forceinline__ void st_l2_16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, f32x4v v) {
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4raw, v), r, byte_off, 0, 0);
-}
 typedef uint32_t u32x2raw __attribute__((vector_size(8)));
-// A plain 8-byte store into the XCD's L2.
-__device__ __forceinline__ void st_l2_8(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, uint2 v) {
-  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2raw, v), r, byte_off, 0, 0);
-}
 __device__ __forceinline__ void st_coherent8(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, uint2 v) {
   __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2raw, v), r, byte_off, 0, kCachePolicySc1);
 }

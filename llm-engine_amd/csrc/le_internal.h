@@ -14,9 +14,6 @@ struct PartialLayout {
   float* acc;         // [n_parts][q_heads][head_dim]
   float2* ml;         // [n_parts][q_heads]  (m, l)
   unsigned long long* counters;  // [n_rows][kv_heads] arrivals; zero between launches
-  // Device-wide count of split-row merges that found their partitions on
-  // different XCDs (only touched when that happens; see xcd_misplacements).
-  int32_t* misplaced;
 };
 
 // Decode work item: query row `token` (position `pos`, block table starting
@@ -96,36 +93,7 @@ struct DecodeParams {
   int q_heads, kv_heads, head_dim, block_size;
   float scale_log2;         // softmax scale * log2(e)
   int64_t num_cache_blocks;
-  // With items: every partition of a split row runs on one XCD (the plan's
-  // placement, confirmed on this device by xcd_placement_holds), so partials
-  // go through that XCD's L2 with plain stores. 0 off, 1 on,
-  // kL2LocalSimulateMisses: on, with fault injection (xcd_rotation).
-  int l2_local;
-  int lin;  // set by the kernel: the workgroup's linear id in its grid
 };
-
-// True when this device sends workgroup i of a launch to XCD i % 8 (checked
-// once per device with a probe launch, then cached). False while the stream
-// is being captured and the device is not checked yet, or on any error.
-bool xcd_placement_holds(hipStream_t stream);
-
-// The current device's misplacement counter (a static device array; null on
-// error), which launches with l2_local pass to their kernels.
-int32_t* xcd_miss_counter();
-
-// Reads and clears the current device's misplacement counter (split rows
-// whose partitions were found on different XCDs; synchronises `stream`). A
-// nonzero count turns the L2 exchange off for the device: from then on split
-// rows store write-through, as when the probe fails.
-hipError_t xcd_misplacements(hipStream_t stream, int64_t* count);
-
-// Forgets the current device's probe result: the next plan launch with split
-// rows probes the placement again.
-void xcd_placement_recheck();
-
-// l2_local value that makes every workgroup whose bits 3 and 4 of the linear id differ
-// report another XCD rotation (fault injection for the guard's tests).
-constexpr int kL2LocalSimulateMisses = 2;
 
 hipError_t attention_decode(const DecodeParams& p, int act_dtype, int kv_dtype, hipStream_t stream);
 
@@ -145,11 +113,6 @@ struct ChunkParams {
   int q_heads, kv_heads, head_dim, block_size;
   float scale_log2;
   int64_t num_cache_blocks;
-  // every partition of a split tile runs on one XCD (the plan's placement,
-  // confirmed by xcd_placement_holds): partials go through its L2 (values
-  // as DecodeParams::l2_local)
-  int l2_local;
-  int lin;  // set by the kernel: the workgroup's linear id in its grid
 };
 
 hipError_t attention_chunk(const ChunkParams& p, int act_dtype, int kv_dtype, hipStream_t stream);

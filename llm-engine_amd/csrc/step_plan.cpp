@@ -56,14 +56,12 @@ int round_to_blocks(int tokens, int bs) {
 }
 
 // The dispatcher sends workgroup i of a launch (linear id) to XCD i % 8, and
-// each XCD has its own L2. The partitions of a split row (decode) or tile
-// (chunk) exchange partials and an arrival counter at the end of the launch;
-// with all of them on one XCD that exchange stays in one L2. So the groups
-// (one row's or tile's partitions) are dealt longest-first into kXcds bins,
-// each to the bin with the least work so far, and item k of bin b goes to
-// index k * kXcds + b. Bins are padded to one length with empty items, so the
-// item count is a multiple of kXcds and the kv head's offset in the grid (a
-// multiple of the item count) keeps every group on its bin's XCD.
+// each XCD has its own L2. The partitions of a split chunk tile are kept on
+// one XCD: the groups (one tile's partitions) are dealt longest-first into
+// kXcds bins, each to the bin with the least work so far, and item k of bin b
+// goes to index k * kXcds + b. Bins are padded to one length with empty
+// items, so the item count is a multiple of kXcds and the kv head's offset in
+// the grid (a multiple of the item count) keeps every group on its bin's XCD.
 template <typename Item, typename Same, typename Blocks>
 std::vector<Item> place_on_xcds(const std::vector<Item>& items, Same same_group, Blocks blocks, const Item& pad) {
   struct Group { size_t first, n; int64_t longest, work; };
@@ -103,16 +101,6 @@ std::vector<Item> place_on_xcds(const std::vector<Item>& items, Same same_group,
   return out;
 }
 
-std::vector<le::DecodeItem> place_decode_items(const std::vector<le::DecodeItem>& dec) {
-  le::DecodeItem pad{};
-  pad.token = -1;
-  pad.part = -1;
-  pad.n_parts = 0;  // resolved as "no work"
-  return place_on_xcds(
-      dec, [](const le::DecodeItem& a, const le::DecodeItem& b) { return a.token == b.token && a.part_begin == b.part_begin; },
-      [](const le::DecodeItem& d) { return static_cast<int64_t>(d.blk_end - d.blk_begin); }, pad);
-}
-
 std::vector<le::ChunkItem> place_chunk_items(const std::vector<le::ChunkItem>& chk) {
   le::ChunkItem pad{};
   pad.n_q = 0;  // no rows: the workgroup returns at once
@@ -133,7 +121,7 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
   if (cfg.block_size <= 0 || cfg.q_heads <= 0 || cfg.kv_heads <= 0 || cfg.head_dim <= 0)
     return LE_EINVAL;
   if (cfg.kv_dtype != LE_F32 && cfg.kv_dtype != LE_BF16 && cfg.kv_dtype != LE_F16) return LE_EINVAL;
-  if ((cfg.flags & ~(LE_PLAN_WRITE_THROUGH | LE_PLAN_TWO_LAUNCHES | LE_PLAN_SIMULATE_MISPLACEMENT)) != 0 || cfg.table_capacity < 0)
+  if ((cfg.flags & ~LE_PLAN_TWO_LAUNCHES) != 0 || cfg.table_capacity < 0)
     return LE_EINVAL;
   // Fixed layout (table_capacity > 0): decode rows only, a given partition.
   const bool fixed = cfg.table_capacity > 0;
@@ -287,16 +275,10 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
   // Longest work first: workgroups start over a couple of microseconds in
   // launch order, so the items on the critical path (most keys) go first.
   // Merges do not depend on the order (partials are addressed by index).
-  bool split = parts > 0;  // chunk or decode partials (fixed layout: decode rows checked below)
-  for (const auto& d : dec) split |= d.part >= 0;
   if (fixed) parts = static_cast<int32_t>(n_tok) * parts_cap;
-  if (split) {
-    dec = place_decode_items(dec);
-  } else {
-    std::stable_sort(dec.begin(), dec.end(), [](const le::DecodeItem& a, const le::DecodeItem& b) {
-      return a.blk_end - a.blk_begin > b.blk_end - b.blk_begin;
-    });
-  }
+  std::stable_sort(dec.begin(), dec.end(), [](const le::DecodeItem& a, const le::DecodeItem& b) {
+    return a.blk_end - a.blk_begin > b.blk_end - b.blk_begin;
+  });
   bool chunk_split = false;
   for (const auto& c : chk) chunk_split |= c.part0 >= 0;
   if (chunk_split) {
@@ -308,11 +290,11 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
   }
 
   if (fixed) {
-    // one item count for every step of this row count: rows * parts_cap
-    // items dealt into eight bins, each bin at most one row's partitions
-    // longer than the mean, padded to that with empty items
-    const size_t cap_items = kXcds * ((static_cast<size_t>(n_tok) * parts_cap + kXcds - 1) / kXcds + parts_cap);
-    if (dec.size() > cap_items) return LE_EUNSUPPORTED;
+    // one item count for every step of this row count: each row has at most
+    // parts_cap partitions, so rows * parts_cap items, padded with empty
+    // ones (n_parts 0: resolved as no work)
+    const size_t cap_items = static_cast<size_t>(n_tok) * parts_cap;
+    if (dec.size() > cap_items) return LE_EUNSUPPORTED;  // unreachable: J <= parts_cap per row
     le::DecodeItem pad{};
     pad.token = -1;
     pad.part = -1;

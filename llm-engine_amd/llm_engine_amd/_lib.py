@@ -22,9 +22,7 @@ LE_ETOOLARGE = -5
 LE_F32 = 0
 LE_BF16 = 1
 LE_F16 = 2
-LE_PLAN_WRITE_THROUGH = 1
 LE_PLAN_TWO_LAUNCHES = 2
-LE_PLAN_SIMULATE_MISPLACEMENT = 4
 
 c_i32p = ctypes.POINTER(ctypes.c_int32)
 
@@ -130,6 +128,17 @@ class RunStats(ctypes.Structure):
 SIGNATURES = {
     "le_version": (ctypes.c_char_p, []),
     "le_status_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "le_embedding": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                     ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    "le_rmsnorm": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                   ctypes.c_int, ctypes.c_float, ctypes.c_void_p]),
+    "le_silu_mul": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t, ctypes.c_void_p]),
+    "le_rope": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    "le_add_inplace": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t,
+                                       ctypes.c_void_p]),
+    "le_add_bias": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_void_p]),
     "le_kv_cache_write": (ctypes.c_int, [
         ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
         ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64,
@@ -173,7 +182,7 @@ SIGNATURES = {
     "le_model_set_decode_graph": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int]),
     "le_model_graph_replays": (ctypes.c_int64, [ctypes.c_void_p]),
     "le_model_set_plan_flags": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32]),
-    "le_model_placement_reruns": (ctypes.c_int64, [ctypes.c_void_p]),
+    "le_model_eager_fallbacks": (ctypes.c_int64, [ctypes.c_void_p]),
     "le_model_forward": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(StepSlice), ctypes.c_int,
                                         ctypes.c_void_p, ctypes.c_void_p]),
     "le_run_greedy": (ctypes.c_int, [
@@ -187,8 +196,6 @@ SIGNATURES = {
         ctypes.c_int64, ctypes.POINTER(StepPlan), ctypes.c_float, ctypes.c_void_p,
         ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "le_noalloc_scratch_bytes": (ctypes.c_size_t, []),
-    "le_xcd_misplacements": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int64)]),
-    "le_xcd_placement_recheck": (None, []),
     "le_ragged_paged_attention_noalloc": (ctypes.c_int, [
         ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
         ctypes.c_int64, ctypes.POINTER(StepPlan), ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p]),

@@ -121,9 +121,9 @@ class Model:
         check("le_model_set_plan_flags", _lib.load().le_model_set_plan_flags(self._h, int(flags)))
 
     @property
-    def placement_reruns(self) -> int:
-        """Steps run again because a split row's partitions were spread over XCDs."""
-        return int(_lib.load().le_model_placement_reruns(self._h))
+    def eager_fallbacks(self) -> int:
+        """Decode steps run eagerly although graph replay is on (le_model_eager_fallbacks)."""
+        return int(_lib.load().le_model_eager_fallbacks(self._h))
 
     def close(self):
         if getattr(self, "_h", None):

@@ -218,20 +218,6 @@ class Plan:
         return int(_lib.load().le_ragged_workspace_size(ctypes.byref(self.plan)))
 
 
-def xcd_misplacements(stream=None) -> int:
-    """Reads and clears the current device's count of split-row workgroups
-    that ran off the XCD their plan placed them on (le_xcd_misplacements). A
-    nonzero count switches the device to write-through partials."""
-    n = ctypes.c_int64(0)
-    check("le_xcd_misplacements", _lib.load().le_xcd_misplacements(_stream(stream), ctypes.byref(n)))
-    return int(n.value)
-
-
-def xcd_placement_recheck() -> None:
-    """The next plan launch with split rows probes the XCD placement again."""
-    _lib.load().le_xcd_placement_recheck()
-
-
 def ragged_paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                            plan: Plan, scale: float, out: torch.Tensor | None = None,
                            workspace: torch.Tensor | None = None, stream=None,

@@ -20,6 +20,21 @@
 //     test_cuda_invariance.cpp:295-344);
 //   * a rejected shape (head_dim 96) throws std::runtime_error, as the
 //     reference's launchers do (attention_decode_gqa.cu:211-224).
+//
+// Then one whole layer of a decode step in the reference's launch order
+// (cuda_model.cu:347-390): launch_embedding, launch_rmsnorm, the q/k/v
+// projections, launch_add_bias x3, launch_rope on q and k, launch_store_kv,
+// both attention launchers, the o projection, launch_add_inplace,
+// launch_rmsnorm, gate/up projections, launch_silu_mul, the down projection,
+// launch_add_inplace. The GEMMs are not launchers of cuda_kernels.h (the
+// reference calls cuBLAS), so the test does them on the host with the
+// oracle's linear and uploads their fp16 outputs. Every launcher's output is
+// checked against the oracle op on the same fp16 inputs:
+//   * bit-exact: embedding, bias adds, RoPE, the cache rows, residual adds;
+//   * within the fp16 rounding of the output plus 1e-6 relative: RMSNorm
+//     (the oracle sums squares in double, the kernel in fp32) and SiLU
+//     (expf's last bits);
+//   * attention: as above.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -66,6 +81,206 @@ std::vector<float> widen(const std::vector<uint16_t>& h) {
 }
 
 }  // namespace
+
+// |got - want| <= 2^-11 |want| (the fp16 rounding of the output) + 1e-6 |want| + 2^-25 per element.
+bool within_f16_rounding(const std::vector<uint16_t>& got, const std::vector<float>& want, double* worst) {
+  const std::vector<float> g = widen(got);
+  bool ok = g.size() == want.size();
+  for (size_t i = 0; ok && i < g.size(); i++) {
+    const double w = std::fabs(static_cast<double>(want[i]));
+    const double d = std::fabs(static_cast<double>(g[i]) - want[i]);
+    const double bar = w * (std::ldexp(1.0, -11) + 1e-6) + std::ldexp(1.0, -25);
+    *worst = std::fmax(*worst, d / bar);
+    ok = d <= bar;
+  }
+  return ok;
+}
+
+std::vector<uint16_t> round_f16(const std::vector<float>& f) {
+  std::vector<uint16_t> h(f.size());
+  orc_f32_to_f16_n(f.data(), h.data(), f.size());
+  return h;
+}
+
+// One decode layer through the nine launchers (see the header comment).
+// Returns true if every stage matched.
+bool layer_sequence(int n, const std::vector<int>& tables, const std::vector<int>& table_offset,
+                    const std::vector<int>& token_seq, const std::vector<int>& token_pos,
+                    const std::vector<int>& slots, __half* d_kc, __half* d_vc, size_t cache_elems, int* d_slots,
+                    int* d_tables, int* d_toff, int* d_tseq, int* d_tpos, std::mt19937_64& rng) {
+  const int q_heads = 14, kv_heads = 2, hd = 64, bs = 16, H = 896, I = 4864, vocab = 1000, max_pos = 4096;
+  const int q_dim = q_heads * hd, kv_dim = kv_heads * hd;
+  const float eps = 1e-6f, scale = 1.0f / std::sqrt(static_cast<float>(hd));
+  std::normal_distribution<float> normal(0.f, 1.f);
+  auto randn = [&](size_t k, float sd) {
+    std::vector<float> f(k);
+    for (auto& x : f) x = normal(rng) * sd;
+    return f;
+  };
+  auto widen_round = [&](const std::vector<float>& f) { return widen(round_f16(f)); };
+  // weights as fp16 values (the reference's CudaModel holds __half weights), norms and biases fp32
+  const std::vector<float> embed = widen_round(randn(static_cast<size_t>(vocab) * H, 1.0f));
+  const std::vector<float> wq = widen_round(randn(static_cast<size_t>(q_dim) * H, 0.03f));
+  const std::vector<float> wk = widen_round(randn(static_cast<size_t>(kv_dim) * H, 0.03f));
+  const std::vector<float> wv = widen_round(randn(static_cast<size_t>(kv_dim) * H, 0.03f));
+  const std::vector<float> wo = widen_round(randn(static_cast<size_t>(H) * q_dim, 0.03f));
+  const std::vector<float> wg = widen_round(randn(static_cast<size_t>(I) * H, 0.03f));
+  const std::vector<float> wu = widen_round(randn(static_cast<size_t>(I) * H, 0.03f));
+  const std::vector<float> wd = widen_round(randn(static_cast<size_t>(H) * I, 0.015f));
+  std::vector<float> in_norm = randn(H, 0.1f), post_norm = randn(H, 0.1f);
+  for (int j = 0; j < H; j++) { in_norm[j] += 1.f; post_norm[j] += 1.f; }
+  const std::vector<float> bq = randn(q_dim, 0.1f), bk = randn(kv_dim, 0.1f), bv = randn(kv_dim, 0.1f);
+  std::vector<float> cos_t(static_cast<size_t>(max_pos) * hd / 2), sin_t(cos_t.size());
+  orc_rope_tables(hd, max_pos, 1e6f, cos_t.data(), sin_t.data());
+  std::vector<int32_t> ids(n);
+  for (auto& t : ids) t = static_cast<int32_t>(rng() % vocab);
+  auto linear = [&](const std::vector<float>& a, const std::vector<float>& w, int m, int k, int nout) {
+    std::vector<float> c(static_cast<size_t>(m) * nout);
+    orc_linear(a.data(), m, k, w.data(), nout, nullptr, c.data(), 8);
+    return round_f16(c);
+  };
+  bool ok = true;
+  double worst_norm = 0, worst_silu = 0;
+  hipStream_t st = nullptr;
+  auto dev_f16 = [&](const std::vector<uint16_t>& h) { return reinterpret_cast<__half*>(to_device(h)); };
+  auto host_f16 = [&](const __half* d, size_t k) { return to_host(reinterpret_cast<const uint16_t*>(d), k); };
+  auto report = [&](const char* what, bool good) {
+    if (!good) std::printf("layer stage %s FAILED\n", what);
+    ok = ok && good;
+  };
+
+  // embedding (bit-exact)
+  const std::vector<uint16_t> embed_h = round_f16(embed);
+  __half* d_embed = dev_f16(embed_h);
+  int32_t* d_ids = to_device(ids);
+  __half* d_x = nullptr;
+  HIP_OK(hipMalloc(&d_x, static_cast<size_t>(n) * H * 2));
+  engine::launch_embedding(d_embed, d_ids, d_x, n, H, st);
+  std::vector<uint16_t> x = host_f16(d_x, static_cast<size_t>(n) * H);
+  {
+    bool eq = true;
+    for (int t = 0; t < n; t++)
+      eq = eq && std::memcmp(&x[static_cast<size_t>(t) * H], &embed_h[static_cast<size_t>(ids[t]) * H], H * 2) == 0;
+    report("embedding", eq);
+  }
+  // rmsnorm (fp16 rounding)
+  float* d_in_norm = to_device(in_norm);
+  __half* d_h = nullptr;
+  HIP_OK(hipMalloc(&d_h, static_cast<size_t>(n) * H * 2));
+  engine::launch_rmsnorm(d_x, d_in_norm, d_h, n, H, eps, st);
+  std::vector<uint16_t> h = host_f16(d_h, static_cast<size_t>(n) * H);
+  {
+    std::vector<float> want(static_cast<size_t>(n) * H);
+    orc_rmsnorm(widen(x).data(), in_norm.data(), want.data(), n, H, eps);
+    report("rmsnorm", within_f16_rounding(h, want, &worst_norm));
+  }
+  // projections on the host, then bias (bit-exact) and RoPE (bit-exact)
+  const std::vector<float> hf = widen(h);
+  std::vector<uint16_t> q = linear(hf, wq, n, H, q_dim), k = linear(hf, wk, n, H, kv_dim),
+                        v = linear(hf, wv, n, H, kv_dim);
+  __half *d_q = dev_f16(q), *d_k = dev_f16(k), *d_v = dev_f16(v);
+  float *d_bq = to_device(bq), *d_bk = to_device(bk), *d_bv = to_device(bv);
+  engine::launch_add_bias(d_q, d_bq, n, q_dim, st);
+  engine::launch_add_bias(d_k, d_bk, n, kv_dim, st);
+  engine::launch_add_bias(d_v, d_bv, n, kv_dim, st);
+  engine::launch_add_bias(d_v, nullptr, n, kv_dim, st);  // no bias (Llama): a no-op
+  auto add_bias_host = [&](std::vector<uint16_t>& a, const std::vector<float>& b, int cols) {
+    std::vector<float> f = widen(a);
+    for (size_t i = 0; i < f.size(); i++) f[i] = f[i] + b[i % cols];
+    a = round_f16(f);
+  };
+  add_bias_host(q, bq, q_dim);
+  add_bias_host(k, bk, kv_dim);
+  add_bias_host(v, bv, kv_dim);
+  report("add_bias", host_f16(d_q, q.size()) == q && host_f16(d_k, k.size()) == k && host_f16(d_v, v.size()) == v);
+  float *d_cos = to_device(cos_t), *d_sin = to_device(sin_t);
+  engine::launch_rope(d_q, d_tpos, d_cos, d_sin, n, q_heads, hd, q_dim, st);
+  engine::launch_rope(d_k, d_tpos, d_cos, d_sin, n, kv_heads, hd, kv_dim, st);
+  auto rope_host = [&](std::vector<uint16_t>& a, int heads, int stride) {
+    std::vector<float> f = widen(a);
+    for (int t = 0; t < n; t++)
+      orc_rope_inplace(&f[static_cast<size_t>(t) * stride], heads, hd, token_pos[t], cos_t.data(), sin_t.data());
+    a = round_f16(f);
+  };
+  rope_host(q, q_heads, q_dim);
+  rope_host(k, kv_heads, kv_dim);
+  report("rope", host_f16(d_q, q.size()) == q && host_f16(d_k, k.size()) == k);
+  // store (bit-exact rows) and both attention launchers
+  engine::launch_store_kv(d_k, d_v, d_slots, d_kc, d_vc, n, kv_dim, st);
+  const std::vector<uint16_t> kc = host_f16(d_kc, cache_elems), vc = host_f16(d_vc, cache_elems);
+  {
+    bool eq = true;
+    for (int t = 0; t < n; t++) {
+      eq = eq && std::memcmp(&kc[static_cast<size_t>(slots[t]) * kv_dim], &k[static_cast<size_t>(t) * kv_dim], kv_dim * 2) == 0;
+      eq = eq && std::memcmp(&vc[static_cast<size_t>(slots[t]) * kv_dim], &v[static_cast<size_t>(t) * kv_dim], kv_dim * 2) == 0;
+    }
+    report("store_kv", eq);
+  }
+  __half *d_a1 = nullptr, *d_a2 = nullptr;
+  HIP_OK(hipMalloc(&d_a1, static_cast<size_t>(n) * q_dim * 2));
+  HIP_OK(hipMalloc(&d_a2, static_cast<size_t>(n) * q_dim * 2));
+  engine::launch_attention_decode_gqa(d_q, d_kc, d_vc, d_tables, d_toff, d_tseq, d_tpos, d_a1, n, q_heads, kv_heads,
+                                      hd, bs, scale, st);
+  engine::launch_attention_decode(d_q, d_kc, d_vc, d_tables, d_toff, d_tseq, d_tpos, d_a2, n, q_heads, kv_heads, hd,
+                                  bs, scale, st);
+  const std::vector<uint16_t> attn = host_f16(d_a1, static_cast<size_t>(n) * q_dim);
+  {
+    std::vector<float> want(static_cast<size_t>(n) * q_dim);
+    const std::vector<float> kf = widen(kc), vf = widen(vc), qf = widen(q);
+    orc_paged_attention(qf.data(), q_dim, kf.data(), vf.data(), tables.data(), table_offset.data(), token_seq.data(),
+                        token_pos.data(), n, q_heads, kv_heads, hd, bs, scale, want.data(), q_dim, 8);
+    const std::vector<float> g = widen(attn);
+    double err = 0;
+    for (size_t i = 0; i < want.size(); i++) err = std::fmax(err, std::fabs(static_cast<double>(g[i]) - want[i]));
+    report("attention", err < 6e-4 + 4.0 * std::ldexp(1.0, -11) && host_f16(d_a2, attn.size()) == attn);
+  }
+  // o projection (host), residual add (bit-exact), post norm
+  __half* d_o = dev_f16(linear(widen(attn), wo, n, q_dim, H));
+  const std::vector<uint16_t> o = host_f16(d_o, static_cast<size_t>(n) * H);
+  engine::launch_add_inplace(d_x, d_o, static_cast<size_t>(n) * H, st);
+  auto add_host = [&](std::vector<uint16_t>& a, const std::vector<uint16_t>& b) {
+    std::vector<float> fa = widen(a), fb = widen(b);
+    for (size_t i = 0; i < fa.size(); i++) fa[i] = fa[i] + fb[i];
+    a = round_f16(fa);
+  };
+  add_host(x, o);
+  report("add_inplace", host_f16(d_x, x.size()) == x);
+  float* d_post = to_device(post_norm);
+  engine::launch_rmsnorm(d_x, d_post, d_h, n, H, eps, st);
+  h = host_f16(d_h, static_cast<size_t>(n) * H);
+  {
+    std::vector<float> want(static_cast<size_t>(n) * H);
+    orc_rmsnorm(widen(x).data(), post_norm.data(), want.data(), n, H, eps);
+    report("rmsnorm (post)", within_f16_rounding(h, want, &worst_norm));
+  }
+  // gate/up (host), SiLU product (fp16 rounding), down (host), residual add (bit-exact)
+  const std::vector<float> h2 = widen(h);
+  const std::vector<uint16_t> gate = linear(h2, wg, n, H, I), up = linear(h2, wu, n, H, I);
+  __half *d_gate = dev_f16(gate), *d_up = dev_f16(up);
+  engine::launch_silu_mul(d_gate, d_up, static_cast<size_t>(n) * I, st);
+  const std::vector<uint16_t> act = host_f16(d_gate, gate.size());
+  {
+    std::vector<float> g = widen(gate);
+    orc_silu_mul(g.data(), widen(up).data(), g.size());
+    report("silu_mul", within_f16_rounding(act, g, &worst_silu));
+  }
+  __half* d_down = dev_f16(linear(widen(act), wd, n, I, H));
+  const std::vector<uint16_t> down = host_f16(d_down, static_cast<size_t>(n) * H);
+  engine::launch_add_inplace(d_x, d_down, static_cast<size_t>(n) * H, st);
+  add_host(x, down);
+  report("add_inplace (mlp)", host_f16(d_x, x.size()) == x);
+  HIP_OK(hipDeviceSynchronize());
+  std::printf("layer %s: 9 launchers in cuda_model.cu order, worst rmsnorm %.2f and silu %.2f of the fp16 bar\n",
+              ok ? "ok" : "FAILED", worst_norm, worst_silu);
+  for (void* p : {static_cast<void*>(d_embed), static_cast<void*>(d_ids), static_cast<void*>(d_x),
+                  static_cast<void*>(d_in_norm), static_cast<void*>(d_h), static_cast<void*>(d_q),
+                  static_cast<void*>(d_k), static_cast<void*>(d_v), static_cast<void*>(d_bq), static_cast<void*>(d_bk),
+                  static_cast<void*>(d_bv), static_cast<void*>(d_cos), static_cast<void*>(d_sin),
+                  static_cast<void*>(d_a1), static_cast<void*>(d_a2), static_cast<void*>(d_o), static_cast<void*>(d_post),
+                  static_cast<void*>(d_gate), static_cast<void*>(d_up), static_cast<void*>(d_down)})
+    HIP_OK(hipFree(p));
+  return ok;
+}
 
 int main(int argc, char** argv) {
   const int n_seqs = argc > 1 ? std::atoi(argv[1]) : 64;
@@ -164,9 +379,12 @@ int main(int argc, char** argv) {
   for (size_t i = 0; i < want.size(); i++) err = std::fmax(err, std::fabs(static_cast<double>(g1[i]) - want[i]));
   const double tol = 6e-4 + 4.0 * std::ldexp(1.0, -11);
   const bool same = o1 == o2;
-  const bool ok = caches_equal && err < tol && same && threw;
-  std::printf("bridge %s: n_seqs %d caches_equal %d max|err| %.3e (tol %.3e) decode==gqa %d throws %d\n",
-              ok ? "ok" : "FAILED", n_seqs, caches_equal ? 1 : 0, err, tol, same ? 1 : 0, threw ? 1 : 0);
+  const bool layer_ok = layer_sequence(n_seqs, tables, table_offset, token_seq, token_pos, slots, d_kc, d_vc,
+                                       kc.size(), d_slots, d_tables, d_toff, d_tseq, d_tpos, rng);
+  const bool ok = caches_equal && err < tol && same && threw && layer_ok;
+  std::printf("bridge %s: n_seqs %d caches_equal %d max|err| %.3e (tol %.3e) decode==gqa %d throws %d layer %d\n",
+              ok ? "ok" : "FAILED", n_seqs, caches_equal ? 1 : 0, err, tol, same ? 1 : 0, threw ? 1 : 0,
+              layer_ok ? 1 : 0);
   for (void* p : {static_cast<void*>(d_kc), static_cast<void*>(d_vc), static_cast<void*>(d_knew),
                   static_cast<void*>(d_vnew), static_cast<void*>(d_q), static_cast<void*>(d_slots),
                   static_cast<void*>(d_tables), static_cast<void*>(d_toff), static_cast<void*>(d_tseq),

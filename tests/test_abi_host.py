@@ -79,19 +79,18 @@ def check_work_lists(plan, slices, bs=16):
     toff = plan.host_array("table_offset")
     tseq = plan.host_array("token_seq")
     # decode items: per row, [blk_begin, blk_end) ranges tile [0, pos/bs] exactly once
-    rows, bins = {}, {}
+    rows = {}
+    lengths = []
     for k, it in enumerate(dec):
         token, p, to, b0, b1, part, pb, npart = (int(x) for x in it)
-        if npart == 0:  # padding that keeps split rows on one XCD
-            assert token == -1 and b0 == b1 and P.n_parts > 0
+        if npart == 0:  # padding of the fixed (graph-replay) layout
+            assert token == -1 and b0 == b1 and P.cfg.table_capacity > 0
             continue
         assert p == pos[token] and to == toff[tseq[token]]
         rows.setdefault(token, []).append((b0, b1, part, pb, npart))
-        if npart > 1:  # a split row's partitions sit at indices equal modulo 8 (one XCD)
-            bins.setdefault(token, set()).add(k % 8)
-    assert all(len(b) == 1 for b in bins.values())
-    if P.n_parts > 0:
-        assert len(dec) % 8 == 0
+        lengths.append(b1 - b0)
+    # longest items first (the critical path starts first)
+    assert lengths == sorted(lengths, reverse=True)
     for token, items in rows.items():
         items.sort()
         assert items[0][0] == 0 and items[-1][1] == pos[token] // bs + 1
@@ -227,9 +226,10 @@ def test_plan_rejects_slices_outgrowing_their_sequence_table():
 
 
 def test_bridge_exports_reference_signatures():
-    """libllm_engine_amd_bridge.so exports the reference's launcher names with
-    its argument lists (cuda_kernels.h:43-64, __half buffers, hipStream_t),
-    plus the two registration calls declared in include/le_cuda_kernels.h."""
+    """libllm_engine_amd_bridge.so exports all nine of the reference's
+    launcher names with its argument lists (cuda_kernels.h:17-64, __half
+    buffers, fp32 weights/bias/tables, hipStream_t), plus the registration
+    calls declared in include/le_cuda_kernels.h."""
     import subprocess
     lib = ROOT / "llm-engine_amd" / "lib" / "libllm_engine_amd_bridge.so"
     ctypes.CDLL(str(lib))
@@ -243,6 +243,13 @@ def test_bridge_exports_reference_signatures():
         "__half*, int, int, int, int, int, float, ihipStream_t*)",
         "engine::le_bridge_set_workspace(void*, unsigned long)",
         "engine::le_bridge_set_cache_slots(long)",
+        "engine::le_bridge_set_rope_positions(int)",
+        f"engine::launch_embedding({h}, int const*, __half*, int, int, ihipStream_t*)",
+        f"engine::launch_rmsnorm({h}, float const*, __half*, int, int, float, ihipStream_t*)",
+        f"engine::launch_silu_mul(__half*, {h}, unsigned long, ihipStream_t*)",
+        "engine::launch_rope(__half*, int const*, float const*, float const*, int, int, int, int, ihipStream_t*)",
+        f"engine::launch_add_inplace(__half*, {h}, unsigned long, ihipStream_t*)",
+        "engine::launch_add_bias(__half*, float const*, int, int, ihipStream_t*)",
     ]
     for w in want:
         assert w in syms, w
@@ -301,6 +308,36 @@ def test_fixed_layout_is_constant_across_decode_steps():
         check_work_lists(plan, sl)
     with pytest.raises(ValueError):  # prefill chunks have no fixed layout
         _plan([Slice(1, 0, 5, True, blocks[0][:1], np.zeros(5, np.int32))], partition_tokens=512, table_capacity=cap)
+
+
+def test_fixed_layout_accepts_skewed_decode_batches():
+    """Decode steps with a few full-length rows among many short ones (the
+    engine's graph-replay layout: partitions of 1024 tokens, block 16) plan
+    in the fixed layout for every table capacity and partition size: the
+    item list is rows * partitions-per-row long, so no mix of lengths can
+    overflow it. Seeded random batches as well."""
+    from llm_engine_amd.kernels import Slice
+    rng = np.random.default_rng(11)
+
+    def step(lens, cap):
+        return [Slice(100 + i, int(c) - 1, 1, True, rng.permutation(20000)[:(int(c) + 15) // 16].astype(np.int32),
+                      np.arange(int(c), dtype=np.int32)) for i, c in enumerate(lens)]
+
+    cases = [([128 * 16] * 7 + [6] * 16, 128, 1024)]  # the reported batch: 7 full rows, 16 at pos 5
+    for _ in range(60):
+        cap = int(rng.choice([32, 64, 128, 256]))
+        part = int(rng.choice([256, 512, 640, 1024, 2048]))
+        n = int(rng.integers(1, 80))
+        n_long = int(rng.integers(0, n + 1))
+        lens = [cap * 16 if i < n_long else int(rng.integers(1, 40)) for i in range(n)]
+        rng.shuffle(lens)
+        cases.append((lens, cap, part))
+    for lens, cap, part in cases:
+        sl = step(lens, cap)
+        plan = _plan(sl, partition_tokens=part, table_capacity=cap)
+        check_work_lists(plan, sl)
+        parts_cap = -(-cap // -(-part // 16))
+        assert plan.plan.n_decode_items == len(lens) * min(parts_cap, 1024 // 7)
 
 
 @pytest.mark.parametrize("bs", [8, 16, 32])
