@@ -406,6 +406,7 @@ def e2e_run(arch, prompts, out_lens, pool_blocks, max_seqs=64, budget=512, arriv
     t0 = time.perf_counter()
     w = synthetic_weights(arch, seed, layers=layers)
     L = w.arch["layers"]
+    w_arch = dict(w.arch)
     m = Model(w, pool_blocks, 16, dtype="bf16", kv_dtype="bf16", decode_graph=decode_graph)
     del w
     setup_s = time.perf_counter() - t0
@@ -417,6 +418,22 @@ def e2e_run(arch, prompts, out_lens, pool_blocks, max_seqs=64, budget=512, arriv
     gen_total = sum(len(t) for t in toks)
     if gen_total != sum(out_lens):
         raise SystemExit("bench.py: not every request finished")
+    # Decode-step roofline: every step streams all weights (bf16; the LM head
+    # too) and each row's K/V history once (bf16, per layer).
+    a = w_arch
+    kv_dim = a["kv_heads"] * a["head_dim"]
+    per_layer = a["hidden"] * (a["q_heads"] * a["head_dim"] + 2 * kv_dim) + a["q_heads"] * a["head_dim"] * a["hidden"] \
+        + 3 * a["hidden"] * a["inter"]
+    weight_bytes = 2 * (L * per_layer + a["vocab"] * a["hidden"])
+    roof = None
+    if st.decode_steps:
+        kv_bytes = st.decode_context_tokens / st.decode_steps * L * kv_dim * 2 * 2
+        step_s = st.decode_seconds / st.decode_steps
+        achieved = (weight_bytes + kv_bytes) / step_s / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "bytes_per_step": int(weight_bytes + kv_bytes),
+                "weight_bytes": int(weight_bytes), "kv_bytes_per_step": int(kv_bytes),
+                "what": "bf16 weights + K/V history per decode step / wall time per decode step"}
     return {"model": f"{arch}, {L} layers, random-init bf16 weights, bf16 KV",
             "requests": len(prompts), "pool_blocks": pool_blocks, "max_running": max_seqs,
             "prefix_caching": prefix_caching, "prompt_tokens_computed": int(st.prompt_tokens),
@@ -427,7 +444,7 @@ def e2e_run(arch, prompts, out_lens, pool_blocks, max_seqs=64, budget=512, arriv
             "ttft_mean_s": round(st.ttft_mean_s, 4), "latency_mean_s": round(st.latency_mean_s, 3),
             "preemptions": int(st.preemptions), "setup_s": round(setup_s, 1),
             "plan_us_per_step": round(1e6 * st.plan_seconds / st.steps, 1) if st.steps else None,
-            "decode_graph": decode_graph, "graph_replays": replays}
+            "decode_graph": decode_graph, "graph_replays": replays, "decode_roofline": roof}
 
 
 def e2e_leg(which, layers=None):
@@ -452,7 +469,8 @@ def e2e_leg(which, layers=None):
             eager = e2e_run("tinyllama-1.1b", prompts, [256] * n, 5120, layers=layers)
             graph = e2e_run("tinyllama-1.1b", prompts, [256] * n, 5120, layers=layers, decode_graph=True)
             return eager | {"with_decode_graph": {k: graph[k] for k in (
-                "decode_tok_per_s", "decode_ms_per_step", "tok_per_s", "graph_replays", "plan_us_per_step")}}
+                "decode_tok_per_s", "decode_ms_per_step", "tok_per_s", "graph_replays", "plan_us_per_step",
+                "decode_roofline")}}
         outs = rng.integers(64, 257, size=n).tolist()
         arr = np.cumsum(rng.exponential(1.0 / 8.0, size=n)).tolist()
         return e2e_run("tinyllama-1.1b", prompts, outs, 5120, arrivals_s=arr, layers=layers) | \
@@ -477,7 +495,7 @@ def main():
     ap.add_argument("--graph", action="store_true", help="replay the step as one captured HIP graph")
     ap.add_argument("--separate-scatter", action="store_true",
                     help="scatter with le_kv_cache_write, then attend (instead of the fused entry point)")
-    ap.add_argument("--e2e", choices=["decode64", "config4", "config5", "all", "none"], default="decode64",
+    ap.add_argument("--e2e", choices=["decode64", "config4", "config5", "default", "all", "none"], default="default",
                     help="end-to-end leg after the attention measurement (see e2e_leg)")
     ap.add_argument("--e2e-layers", type=int, default=None, help="model layers (default: all)")
     ap.add_argument("--cpu-budget", type=float, default=10.0)
@@ -536,7 +554,8 @@ def main():
         res["cpu_baseline"] = cpu_baseline(ctx, q_len, args.kv == "bf16", args.cpu_budget)
     else:
         res["cpu_baseline"] = None
-    for leg in (["decode64", "config4", "config5"] if args.e2e == "all" else [args.e2e]):
+    legs = {"all": ["decode64", "config4", "config5"], "default": ["decode64", "config4"]}.get(args.e2e, [args.e2e])
+    for leg in legs:
         if leg != "none":
             res["e2e_" + leg] = e2e_leg(leg, layers=args.e2e_layers)
             if leg == "decode64" and not args.no_cpu_baseline:

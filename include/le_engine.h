@@ -148,13 +148,21 @@ typedef struct le_run_stats {
   double ttft_mean_s;              /* arrival (or start) to first token, mean over sequences */
   double latency_mean_s;           /* arrival (or start) to last token, mean over sequences */
   double plan_seconds;             /* host time in le_plan_step + le_plan_upload, all steps */
+  int64_t decode_context_tokens;   /* keys attended (pos + 1) summed over the rows of those steps */
 } le_run_stats;
+
+/* Pool preparation code (the fragment_blocks argument of le_sched_trace,
+ * le_sched_create and le_run_greedy). n >= 0: the reference's fragmentation
+ * recipe (test_cuda_invariance.cpp:98-105) - allocate n one-block sequences,
+ * free every other one. LE_POOL_SHUFFLED | seed (seed < 2^30): the free list
+ * in a seeded random order, so every table is drawn from a random permutation
+ * of the pool (not in the reference; BASELINE config 1's fragmented tables). */
+#define LE_POOL_SHUFFLED (1 << 30)
 
 /* Greedy generation of n_seqs prompts through the scheduler and the model.
  * arrival_s (NULL = all at t=0) delays each request until that many seconds
  * after the start (Poisson arrivals for serving runs). fragment_blocks
- * pre-fragments the pool (allocate that many one-block sequences, free every
- * other one). gen_out receives, per sequence, max_tokens[i] ids (unused
+ * prepares the pool (LE_POOL_SHUFFLED above). gen_out receives, per sequence, max_tokens[i] ids (unused
  * entries -1). */
 int le_run_greedy(le_model* m, const le_sched_config* cfg, int prefix_caching, int fragment_blocks,
                   int n_seqs, const int32_t* prompt_lens, const int32_t* prompts_flat,

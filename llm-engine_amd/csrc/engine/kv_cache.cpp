@@ -48,6 +48,35 @@ KVCacheManager::KVCacheManager(int num_blocks, int block_size, bool enable_prefi
   for (BlockId b = num_blocks; b-- > 0;) free_.push_back(b);
 }
 
+void KVCacheManager::shuffle_free_blocks(uint64_t seed) {
+  uint64_t state = seed;
+  for (size_t i = free_.size(); i > 1; i--) {
+    state = mix64(state);
+    const size_t j = static_cast<size_t>(state % i);
+    std::swap(free_[i - 1], free_[j]);
+  }
+}
+
+std::vector<BlockTable> prepare_pool(KVCacheManager& kv, int fragment) {
+  std::vector<BlockTable> held;
+  if (fragment & kPoolShuffled) {
+    kv.shuffle_free_blocks(static_cast<uint64_t>(fragment & (kPoolShuffled - 1)));
+    return held;
+  }
+  for (int i = 0; i < fragment; i++) {
+    BlockTable bt;
+    std::vector<int32_t> one(static_cast<size_t>(std::max(1, kv.block_size() / 2)), 7000 + i);
+    if (!kv.allocate_prompt(bt, one)) break;
+    held.push_back(bt);
+  }
+  std::vector<BlockTable> kept;
+  for (size_t i = 0; i < held.size(); i++) {
+    if (i % 2 == 0) kv.free(held[i]);
+    else kept.push_back(held[i]);
+  }
+  return kept;
+}
+
 // ---- reuse queue ----
 
 void KVCacheManager::enqueue(BlockId b) {

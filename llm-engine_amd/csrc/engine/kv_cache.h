@@ -73,6 +73,11 @@ class KVCacheManager {
   // block's hash (splitmix64 mixing); never 0, which means "unhashed".
   static uint64_t hash_block(uint64_t prev_hash, const int32_t* tokens, int n);
 
+  // Test and benchmark aid, not in the reference: reorders the free stack by
+  // a seeded Fisher-Yates shuffle (splitmix64 draws), so that allocations
+  // hand out a random permutation of the free blocks.
+  void shuffle_free_blocks(uint64_t seed);
+
  private:
   // State of one physical block. A block with no owner but a published hash
   // waits in the reuse queue (an intrusive doubly linked list through
@@ -104,5 +109,17 @@ class KVCacheManager {
   std::unordered_map<uint64_t, BlockId> published_;
   KVCacheStats stats_;
 };
+
+// Bit of a pool-preparation code that selects the shuffled pool; the low 30
+// bits are then the seed.
+constexpr int kPoolShuffled = 1 << 30;
+
+// Prepares a fresh pool for a run. fragment >= 0 without kPoolShuffled: the
+// reference's fragmentation recipe (test_cuda_invariance.cpp:98-105) -
+// allocate `fragment` single-block sequences, then free every other one (the
+// rest stay allocated; their tables are returned so the caller may keep or
+// release them). With kPoolShuffled: the whole free stack in a seeded random
+// order, nothing held. Returns the tables still holding blocks.
+std::vector<BlockTable> prepare_pool(KVCacheManager& kv, int fragment);
 
 }  // namespace le::engine

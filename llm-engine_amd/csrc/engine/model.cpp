@@ -625,15 +625,8 @@ int le_run_greedy(le_model* m, const le_sched_config* cfg, int prefix_caching, i
   try {
     Model& model = *m->impl;
     KVCacheManager kv(model.num_blocks(), model.block_size(), prefix_caching != 0);
-    // Pre-fragment the pool (test_cuda_invariance.cpp:98-105).
-    std::vector<BlockTable> held;
-    for (int i = 0; i < fragment_blocks; i++) {
-      BlockTable bt;
-      std::vector<int32_t> one(std::max(1, model.block_size() / 2), 7000 + i);
-      if (!kv.allocate_prompt(bt, one)) break;
-      held.push_back(bt);
-    }
-    for (size_t i = 0; i < held.size(); i += 2) kv.free(held[i]);
+    // Pre-fragment or shuffle the pool (test_cuda_invariance.cpp:98-105).
+    std::vector<BlockTable> held = prepare_pool(kv, fragment_blocks);
 
     SchedulerConfig sc;
     sc.continuous = cfg->continuous != 0;
@@ -698,6 +691,7 @@ int le_run_greedy(le_model* m, const le_sched_config* cfg, int prefix_caching, i
         rs.decode_seconds += te - ts;
         rs.decode_steps++;
         rs.decode_step_tokens += step.num_logits;
+        for (const auto& s : step.slices) rs.decode_context_tokens += s.start + s.len;
       }
       rs.steps++;
       rs.prompt_tokens += step.num_prefill_tokens;
@@ -725,7 +719,7 @@ int le_run_greedy(le_model* m, const le_sched_config* cfg, int prefix_caching, i
     }
     rs.preemptions = static_cast<int64_t>(sch.stats().preemptions);
     rs.plan_seconds = model.plan_seconds() - plan_s0;
-    for (size_t i = 1; i < held.size(); i += 2) kv.free(held[i]);
+    for (BlockTable& bt : held) kv.free(bt);
     size_t out_off = 0;  // gen_out: max_tokens[i] entries per sequence, back to back
     for (int i = 0; i < n_seqs; i++) {
       const Sequence& s = *seqs[i];

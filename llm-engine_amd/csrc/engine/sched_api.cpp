@@ -7,6 +7,8 @@
 #include "le_engine.h"
 #include "scheduler.h"
 
+static_assert(le::engine::kPoolShuffled == LE_POOL_SHUFFLED, "pool preparation codes");
+
 extern "C" int64_t le_sched_trace(int num_blocks, int block_size, int prefix_caching,
                                   const le_sched_config* cfg, int fragment_blocks, int n_seqs,
                                   const int32_t* prompt_lens, const int32_t* prompts_flat,
@@ -16,14 +18,7 @@ extern "C" int64_t le_sched_trace(int num_blocks, int block_size, int prefix_cac
   if (!cfg || n_seqs < 0) return 0;
   try {
     KVCacheManager kv(num_blocks, block_size, prefix_caching != 0);
-    std::vector<BlockTable> held;
-    for (int i = 0; i < fragment_blocks; i++) {
-      BlockTable bt;
-      std::vector<int32_t> one(block_size / 2 > 0 ? block_size / 2 : 1, 7000 + i);
-      if (!kv.allocate_prompt(bt, one)) break;
-      held.push_back(bt);
-    }
-    for (size_t i = 0; i < held.size(); i += 2) kv.free(held[i]);
+    std::vector<BlockTable> held = prepare_pool(kv, fragment_blocks);
     SchedulerConfig sc;
     sc.continuous = cfg->continuous != 0;
     sc.max_num_seqs = cfg->max_num_seqs;
@@ -71,7 +66,7 @@ extern "C" int64_t le_sched_trace(int num_blocks, int block_size, int prefix_cac
       rec.push_back(s->num_tokens());
       for (int32_t t : s->tokens) rec.push_back(t);
     }
-    for (size_t i = 1; i < held.size(); i += 2) kv.free(held[i]);
+    for (BlockTable& bt : held) kv.free(bt);
     if (static_cast<int64_t>(rec.size()) > out_cap) return -static_cast<int64_t>(rec.size());
     std::memcpy(out, rec.data(), rec.size() * sizeof(int32_t));
     return static_cast<int64_t>(rec.size());
@@ -90,7 +85,7 @@ struct SchedHandle {
   SchedHandle(int nb, int bs, bool prefix, const le::engine::SchedulerConfig& c)
       : kv(nb, bs, prefix), sch(c, kv) {}
   ~SchedHandle() {
-    for (size_t i = 1; i < held.size(); i += 2) kv.free(held[i]);
+    for (le::engine::BlockTable& bt : held) kv.free(bt);
   }
 };
 
@@ -120,13 +115,7 @@ le_sched* le_sched_create(int num_blocks, int block_size, int prefix_caching,
   if (!cfg || num_blocks <= 0 || block_size <= 0) return nullptr;
   try {
     auto* s = new le_sched(num_blocks, block_size, prefix_caching != 0, to_config(cfg));
-    for (int i = 0; i < fragment_blocks; i++) {
-      le::engine::BlockTable bt;
-      std::vector<int32_t> one(block_size / 2 > 0 ? block_size / 2 : 1, 7000 + i);
-      if (!s->h.kv.allocate_prompt(bt, one)) break;
-      s->h.held.push_back(bt);
-    }
-    for (size_t i = 0; i < s->h.held.size(); i += 2) s->h.kv.free(s->h.held[i]);
+    s->h.held = le::engine::prepare_pool(s->h.kv, fragment_blocks);
     return s;
   } catch (...) {
     return nullptr;

@@ -128,9 +128,12 @@ Scheduler::Residents Scheduler::residents() const {
   return r;
 }
 
-// Frees the blocks of one resident. A finished static-batch member goes
-// first (its K/V is never read again, and preempting it would resurrect a
-// completed request); otherwise the youngest resident is preempted.
+// Picks the resident whose blocks return to the pool. Only static batching
+// leaves a finished member resident (it holds its place to mimic padded
+// generation); such a member is released outright, since nothing reads its
+// cache again and a preemption would put it back in the queue with its token
+// cap already spent. With none, the newest live resident is preempted and
+// recomputed later.
 bool Scheduler::reclaim_memory(Residents& r) {
   const auto drained = std::find_if(running_.rbegin(), running_.rend(),
                                     [](const SequencePtr& s) { return s->is_finished(); });
@@ -242,14 +245,15 @@ StepInput Scheduler::schedule() {
     for (const SequencePtr& w : waiting_) w->wait_steps++;
     admit(d);
     if (!cfg_.continuous && !waiting_.empty()) {
-      // The batch closes when it is full or memory, not this step's budget,
-      // stopped the next admission.
+      // A static batch stops accepting members once it holds max_num_seqs or
+      // the pool refused a request while budget was left over.
       const bool full = static_cast<int>(running_.size()) >= cfg_.max_num_seqs;
       if (full || (d.budget > 0 && !running_.empty())) static_batch_open_ = false;
     }
     if (!waiting_.empty() && running_.empty() && r.decoding.empty()) {
-      // Nothing runs and the head still cannot start: its prompt exceeds the
-      // whole pool. Reject it rather than wait forever.
+      // An empty engine that still cannot place the queue head never will
+      // (the prompt needs more blocks than the pool has): abort that request
+      // so the queue keeps moving.
       const SequencePtr s = waiting_.front();
       waiting_.pop_front();
       retire(s, FinishReason::Abort);

@@ -121,7 +121,7 @@ class RunStats(ctypes.Structure):
                 ("seconds", ctypes.c_double), ("decode_seconds", ctypes.c_double),
                 ("decode_steps", ctypes.c_int64), ("decode_step_tokens", ctypes.c_int64),
                 ("ttft_mean_s", ctypes.c_double), ("latency_mean_s", ctypes.c_double),
-                ("plan_seconds", ctypes.c_double)]
+                ("plan_seconds", ctypes.c_double), ("decode_context_tokens", ctypes.c_int64)]
 
 
 # name -> (restype, argtypes). Exactly the symbols include/*.h declare.

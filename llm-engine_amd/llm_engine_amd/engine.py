@@ -208,6 +208,11 @@ class Scheduler:
         return out[:min(n, cap)].tolist()
 
 
+# Pool preparation code for fragment_blocks (LE_POOL_SHUFFLED in le_engine.h):
+# POOL_SHUFFLED | seed puts the whole free list in a seeded random order.
+POOL_SHUFFLED = 1 << 30
+
+
 def greedy_loop(forward, prompts, max_tokens, num_blocks, block_size=16, cfg=None,
                 prefix_caching=False, fragment_blocks=0, max_steps=100000, on_step=None):
     """The reference's greedy_run (test_cuda_invariance.cpp:90-143) with any

@@ -94,3 +94,26 @@ def test_oracle_greedy_invariances():
     assert run(7, prompts, frag=10) == whole
     for i, p in enumerate(prompts):
         assert run(4096, [p])[0] == whole[i]
+
+
+def test_shuffled_pool_hands_out_a_seeded_permutation():
+    """POOL_SHUFFLED | seed: the tables of the admitted sequences hold distinct
+    blocks of the pool, in an order fixed by the seed (the same on every run,
+    different for another seed) and far from the default low-ids-first order."""
+    from llm_engine_amd.engine import POOL_SHUFFLED, Scheduler, sched_config
+
+    def tables(seed):
+        sch = Scheduler(64, 16, sched_config(max_num_batched_tokens=4096), False, POOL_SHUFFLED | seed)
+        for i in range(4):
+            sch.add(i, np.arange(16 * 16 - 1, dtype=np.int32) + 1, 1)  # 16 blocks each
+        sl = sch.step()
+        out = [np.ctypeslib.as_array(ctypes.cast(s.blocks, ctypes.POINTER(ctypes.c_int32)), (s.num_blocks,)).copy()
+               for s in sl]
+        sch.close()
+        return np.concatenate(out)
+
+    a, b, c = tables(7), tables(7), tables(8)
+    assert len(a) >= 32 and len(set(a.tolist())) == len(a) and a.min() >= 0 and a.max() < 64
+    assert np.array_equal(a, b)
+    assert not np.array_equal(a, c)
+    assert np.count_nonzero(np.diff(a) == 1) < 16  # not runs of consecutive ids

@@ -66,6 +66,48 @@ def test_config1_matches_oracle_token_for_token(gpu, attention, graph):
         assert replays > 10
 
 
+def test_config1_logit_margins(gpu):
+    """Config 1 step by step through the device model's forward with logits
+    (the same scheduler and shuffled pool as the fixture): at every step and
+    logits row, the device logits at the oracle's top-1 and top-2 indices are
+    compared with the oracle's values. Prints the smallest oracle top-2 margin
+    against the largest device-oracle logit difference, and the rows where
+    twice that difference reaches the margin (where a reordered fp32 sum could
+    legitimately have flipped the token). The tokens must equal the
+    fixture's, and the difference stays within 1e-4 (logits are about 3: a
+    few fp32 roundings per layer over 24 layers)."""
+    from llm_engine_amd.engine import Model, greedy_loop, sched_config, synthetic_weights
+    fx = json.loads((GOLD / "config1_tokens.json").read_text())
+    w = synthetic_weights(fx["arch"], fx["weight_seed"])
+    m = Model(w, fx["num_blocks"], 16, dtype="f32")
+    step = [0]
+    worst = [0.0, float("inf")]  # largest |device - oracle|, smallest margin
+    near = []
+
+    def fwd(slices, n_logits):
+        toks, lg = m.forward(slices, n_logits, want_logits=True)
+        rows = fx["top2"][step[0]]
+        assert len(rows) == n_logits
+        for k, (key, i1, v1, i2, v2) in enumerate(rows):
+            d = max(abs(float(lg[k][i1]) - v1), abs(float(lg[k][i2]) - v2))
+            worst[0] = max(worst[0], d)
+            worst[1] = min(worst[1], v1 - v2)
+            if 2 * d >= v1 - v2:
+                near.append((step[0], key, d, v1 - v2))
+            assert d < 1e-4, (step[0], key, d)
+        step[0] += 1
+        return toks
+
+    toks = greedy_loop(fwd, fx["prompts"], [fx["gen"]] * len(fx["prompts"]), fx["num_blocks"], 16,
+                       sched_config(max_num_batched_tokens=fx["max_num_batched_tokens"]),
+                       fragment_blocks=fx["fragment_blocks"])
+    m.close()
+    print(f"config1: {step[0]} steps; smallest oracle top-2 margin {worst[1]:.3g}, "
+          f"largest device-oracle logit difference at the top-2 indices {worst[0]:.3g}; "
+          f"rows with 2 x difference >= margin: {near}")
+    assert toks == fx["tokens"]
+
+
 @pytest.mark.parametrize("case", ["fragmented_multi", "chunked16", "preempt", "prefix"])
 def test_small_model_matches_oracle(gpu, case):
     from llm_engine_amd.engine import sched_config
