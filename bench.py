@@ -397,6 +397,37 @@ def attention_leg(workload, kv, L, steps, warmup, partition=0, chunk_partition=0
     return res
 
 
+def phase_summary(n_workgroups):
+    """Per-phase stamps of the last decode launch, from a measurement build
+    (python llm-engine_amd/build.py -D LE_TIMING --out <dir>/libllm_engine_amd.so,
+    loaded with LE_LIB_PATH): microseconds from the first workgroup's start,
+    median and max over workgroups, per phase (attention_decode_wg.h, slots
+    0-4), with the number of distinct CUs the workgroups ran on."""
+    import ctypes
+    from llm_engine_amd import _lib
+    lib = _lib.load()
+    if not hasattr(lib, "le_timing_read"):
+        raise SystemExit("bench.py --phases needs a LE_TIMING build (LE_LIB_PATH)")
+    buf = np.zeros(65536 * 8, dtype=np.uint64)
+    rc = lib.le_timing_read(ctypes.c_void_p(buf.ctypes.data), ctypes.c_int64(buf.nbytes))
+    if rc != 0:
+        raise SystemExit(f"le_timing_read: {rc}")
+    t = buf[:n_workgroups * 8].reshape(n_workgroups, 8).astype(np.int64)
+    t = t[t[:, 0] > 0]
+    us = (t[:, :5] - t[:, 0].min()) / 100.0  # realtime counter: 100 MHz
+    split = (t[:, 6] & 0xffffffff) > 0
+    out = {"workgroups": int(len(t)), "distinct_cus": int(len(set(t[:, 5].tolist())))}
+    for i, name in enumerate(("start", "staged", "tiles_done", "written", "end")):
+        out[name] = {"median": round(float(np.median(us[:, i])), 2), "max": round(float(us[:, i].max()), 2)}
+    if split.any():
+        out["end_split_rows"] = {"median": round(float(np.median(us[split, 4])), 2),
+                                 "max": round(float(us[split, 4].max()), 2)}
+    if (~split).any():
+        out["end_unsplit_rows"] = {"median": round(float(np.median(us[~split, 4])), 2),
+                                   "max": round(float(us[~split, 4].max()), 2)}
+    return out
+
+
 def e2e_run(arch, prompts, out_lens, pool_blocks, max_seqs=64, budget=512, arrivals_s=None,
             prefix_caching=False, seed=4, layers=None, decode_graph=False):
     """One end-to-end run of the engine: scheduler, packing, device model,
@@ -505,6 +536,9 @@ def main():
     ap.add_argument("--flags", type=int, default=0, help="le_plan_config.flags (2 = LE_PLAN_TWO_LAUNCHES)")
     ap.add_argument("--chunk-partition", type=int, default=0,
                     help="chunk-row key partition tokens (0 = planner's choice)")
+    ap.add_argument("--phases", action="store_true",
+                    help="add per-phase workgroup stamps of the last decode launch (needs a LE_TIMING "
+                         "build of the library, selected with LE_LIB_PATH)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
@@ -544,6 +578,8 @@ def main():
     kv_arena(need, torch.device("cuda:0"))
     res = attention_leg(args.workload, args.kv, args.layers, args.steps, args.warmup, args.partition,
                         args.chunk_partition, args.graph, args.separate_scatter, args.flags)
+    if args.phases:
+        res["phases"] = phase_summary(res["plan"]["decode_items"] * KV_HEADS)
     if extras:
         for key, extra, kv in extras:
             sub = attention_leg(extra, kv, args.layers, max(10, args.steps // 2), args.warmup)

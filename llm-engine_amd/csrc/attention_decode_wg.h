@@ -50,6 +50,37 @@ constexpr int kMergeBatch = 8;       // partial accumulators loaded per batch in
 
 
 
+// Phase stamps (measurement builds, -DLE_TIMING; no code otherwise): thread
+// 0 of each decode workgroup records realtime stamps (100 MHz) of its phases
+// and the CU/XCD it ran on, per linear workgroup id; the last launch's values
+// stay. Slots: 0 start, 1 item and block ids staged, 2 tiles done, 3 output
+// or partial written, 4 end (after the split row's arrival and merge),
+// 5 HW_ID | XCC_ID << 32, 6 partition blocks << 32 | partitions of its row.
+#ifdef LE_TIMING
+constexpr int kTimSlots = 8;
+constexpr int kTimWorkgroups = 65536;
+__device__ uint64_t g_timing[kTimWorkgroups * kTimSlots];
+__device__ __forceinline__ void tim_put(int slot, uint64_t v) {
+  if (threadIdx.x == 0) {
+    const int64_t wg = blockIdx.x + static_cast<int64_t>(blockIdx.y) * gridDim.x;
+    if (wg < kTimWorkgroups) g_timing[wg * kTimSlots + slot] = v;
+  }
+}
+__device__ __forceinline__ uint64_t tim_place() {
+  uint32_t hw, xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  return (static_cast<uint64_t>(xcc) << 32) | hw;
+}
+#define LE_TIM(slot, v) tim_put(slot, v)
+#define LE_TIM_NOW() __builtin_amdgcn_s_memrealtime()
+#define LE_TIM_PLACE() tim_place()
+#else
+#define LE_TIM(slot, v) ((void)0)
+#define LE_TIM_NOW() uint64_t{0}
+#define LE_TIM_PLACE() uint64_t{0}
+#endif
+
 struct Work {
   int token, pos, table_off, b_begin, b_end, part, part_begin, n_parts;
   bool valid;
@@ -732,6 +763,7 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
   constexpr bool kPipe = T::kPipe;
   char* lds = sm.lds;
   int* tab = sm.tab;
+  [[maybe_unused]] const uint64_t t_start = LE_TIM_NOW();
 
   // With a plan, the item's block ids sit at a fixed stride: fetch them now,
   // in the same memory round trip as the item itself, and issue each wave's
@@ -757,6 +789,9 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
   }
   const Work w = resolve(p, bx, bz);
   if (!w.valid) return;
+  LE_TIM(0, t_start);
+  LE_TIM(5, LE_TIM_PLACE());
+  LE_TIM(6, (static_cast<uint64_t>(w.b_end - w.b_begin) << 32) | static_cast<uint32_t>(w.part < 0 ? 0 : w.n_parts));
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
@@ -821,6 +856,7 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
     // this workgroup reads those lines in the launch: the others do not wait.
     if (stores_new_row(p, w)) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    LE_TIM(1, LE_TIM_NOW());
     const int key_end = min(sb1 << bs_shift, w.pos + 1);
     int key0 = (sb0 << bs_shift) + wave * T::kKeys;
     if (key0 >= key_end) continue;
@@ -855,6 +891,7 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
   }
 
   // ---- merge the four waves ----
+  LE_TIM(2, LE_TIM_NOW());
   float l_tot = st.l + __shfl_xor(st.l, 16, kWave);
   l_tot += __shfl_xor(l_tot, 32, kWave);
   __syncthreads();  // V^T tiles are dead; reuse the LDS for the merge
@@ -888,7 +925,12 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
     }
     write_piece<ACT, HD>(p, w, G, kvh, c, o, M, Ls);
   }
+  LE_TIM(3, LE_TIM_NOW());
   arrive_and_merge<ACT, HD, kMfmaThreads>(p, w, G, kvh, &sm.flag);
+#ifdef LE_TIMING
+  __builtin_amdgcn_s_waitcnt(0);  // the merge's output stores are performed
+  LE_TIM(4, LE_TIM_NOW());
+#endif
 }
 }  // namespace
 }  // namespace dec
