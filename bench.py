@@ -414,6 +414,8 @@ def phase_summary(n_workgroups):
         raise SystemExit(f"le_timing_read: {rc}")
     t = buf[:n_workgroups * 8].reshape(n_workgroups, 8).astype(np.int64)
     t = t[t[:, 0] > 0]
+    if not len(t):  # the fused mixed-step kernel keeps its own stamps (another translation unit)
+        raise SystemExit("bench.py --phases: no stamps (decode-only workloads run the stamped kernel)")
     us = (t[:, :5] - t[:, 0].min()) / 100.0  # realtime counter: 100 MHz
     split = (t[:, 6] & 0xffffffff) > 0
     out = {"workgroups": int(len(t)), "distinct_cus": int(len(set(t[:, 5].tolist())))}
@@ -533,16 +535,44 @@ def main():
     ap.add_argument("--no-extra-workloads", action="store_true",
                     help="skip the target, target_f32 and config3 sub-measurements of a config2 run")
     ap.add_argument("--partition", type=int, default=0, help="decode partition tokens (0 = planner's choice)")
-    ap.add_argument("--flags", type=int, default=0, help="le_plan_config.flags (2 = LE_PLAN_TWO_LAUNCHES)")
+    ap.add_argument("--flags", type=int, default=4,
+                    help="le_plan_config.flags (2 = LE_PLAN_TWO_LAUNCHES, 4 = LE_PLAN_XCD_LOCAL, the default: "
+                         "the bench launches on torch's default stream, no CU mask)")
     ap.add_argument("--chunk-partition", type=int, default=0,
                     help="chunk-row key partition tokens (0 = planner's choice)")
     ap.add_argument("--phases", action="store_true",
                     help="add per-phase workgroup stamps of the last decode launch (needs a LE_TIMING "
                          "build of the library, selected with LE_LIB_PATH)")
+    ap.add_argument("--calibrate-stream", action="store_true",
+                    help="only measure the read rate of a library reduction (torch sum) over 134 MB "
+                         "buffers that no recent launch touched: the practical HBM read ceiling")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
     args = ap.parse_args()
+    if args.calibrate_stream:
+        import torch
+        # 8 buffers of the target point's K/V size (134 MB), read round robin so
+        # that the 256 MB MALL never holds the next one
+        nbuf, nbytes = 8, 134217728
+        bufs = [torch.empty(nbytes // 2, dtype=torch.bfloat16, device="cuda").normal_() for _ in range(nbuf)]
+        outs = torch.empty(nbuf, dtype=torch.float32, device="cuda")
+        for i in range(2 * nbuf):
+            torch.sum(bufs[i % nbuf], 0, dtype=torch.float32, out=outs[i % nbuf])
+        reps = 10 * nbuf
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record()
+        for i in range(reps):
+            torch.sum(bufs[i % nbuf], 0, dtype=torch.float32, out=outs[i % nbuf])
+        t1.record()
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) * 1e3 / reps
+        print(json.dumps({"calibration": "read-only reduction (torch.sum, bf16 -> fp32) over 8 rotating "
+                                         "134217728-byte buffers, HIP events over 80 launches",
+                          "bytes_per_launch": nbytes, "us_per_launch": round(us, 3),
+                          "gbs": round(nbytes / us / 1e3, 1), "frac_of_8tbs": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}))
+        return
     if args.calibrate_copy:
         import torch
         x = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
@@ -582,7 +612,7 @@ def main():
         res["phases"] = phase_summary(res["plan"]["decode_items"] * KV_HEADS)
     if extras:
         for key, extra, kv in extras:
-            sub = attention_leg(extra, kv, args.layers, max(10, args.steps // 2), args.warmup)
+            sub = attention_leg(extra, kv, args.layers, max(10, args.steps // 2), args.warmup, flags=args.flags)
             res[key] = {k: sub[k] for k in ("value", "unit", "ms_per_step", "pct_of_peak", "config", "plan",
                                              "roofline")}
     ctx, q_len, _ = workload_shape(args.workload)

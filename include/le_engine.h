@@ -118,8 +118,10 @@ int64_t le_model_graph_replays(const le_model* m);
  * the capture failed (after which every step runs eagerly). */
 int64_t le_model_eager_fallbacks(const le_model* m);
 
-/* le_model_set_plan_flags passes le_plan_config.flags to the model's plans
- * (LE_PLAN_TWO_LAUNCHES: the tests check that launch shape end to end). */
+/* le_model_set_plan_flags sets le_plan_config.flags of the model's plans
+ * (default LE_PLAN_XCD_LOCAL: the model launches on its own stream, without a
+ * CU mask; LE_PLAN_TWO_LAUNCHES: the tests check that launch shape end to
+ * end; 0: write-through partials). */
 int le_model_set_plan_flags(le_model* m, int32_t flags);
 
 

@@ -162,10 +162,25 @@ typedef struct le_plan_config {
                                   depend only on the row count */
 } le_plan_config;
 
-/* le_plan_config.flags. It selects a slower, equivalent launch shape; the
- * tests use it to check that every launch shape gives the same result. */
+/* le_plan_config.flags. LE_PLAN_TWO_LAUNCHES selects a slower, equivalent
+ * launch shape (the tests use it to check that launch shapes agree);
+ * LE_PLAN_XCD_LOCAL a faster exchange of partials under a precondition. */
 #define LE_PLAN_TWO_LAUNCHES 2  /* a mixed step runs its decode and chunk rows as two
                                    launches instead of one */
+#define LE_PLAN_XCD_LOCAL 4     /* opt in to the XCD-local exchange of split rows' partials
+                                   (no counterpart in the reference, whose GPU has one L2):
+                                   the plan places all partitions of a split decode row or
+                                   chunk tile at workgroup ids equal modulo 8, and the launch
+                                   stores their partials into one XCD's L2 with plain stores
+                                   instead of write-through ones (config 3: 22.9 -> 20.6 us per
+                                   launch). Precondition: the device deals a launch's workgroups
+                                   to its XCDs round robin, which holds in every compute
+                                   partition mode but not on streams with a CU mask; do not use
+                                   the flag on such streams. The dealing is probed once per device
+                                   (a small launch, outside stream capture); where it does not
+                                   hold, or before it is probed inside a capture, the launch
+                                   stores write-through as without the flag. Ignored by
+                                   fixed-layout plans. */
 
 typedef struct le_step_plan {
   le_plan_config cfg;
@@ -185,7 +200,8 @@ typedef struct le_step_plan {
   int64_t off_decode_ids;     /* block ids of each decode item, then of each chunk item,
                                  decode_ids_stride apart */
   int32_t decode_ids_stride;  /* entries per work item in that array (padded with -1) */
-  int32_t reserved1_;
+  int32_t xcd_local;          /* 1: every split row's or tile's partitions sit at item indices
+                                 equal modulo 8 (LE_PLAN_XCD_LOCAL honoured) */
   int64_t bytes;         /* total size of the packed buffer */
   const void* dev;       /* device copy, set by le_plan_upload */
 } le_step_plan;

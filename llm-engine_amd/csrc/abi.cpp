@@ -225,6 +225,7 @@ int ragged_attention(const void* q, le_dtype act_dtype, const void* k_new, const
   d.n_rows = plan->n_decode_items; d.nsplit = 1;
   d.q_heads = cfg.q_heads; d.kv_heads = cfg.kv_heads; d.head_dim = cfg.head_dim;
   d.block_size = cfg.block_size; d.scale_log2 = scale_log2; d.num_cache_blocks = num_cache_blocks;
+  d.l2_local = plan->xcd_local && plan->n_parts > 0 && le::xcd_placement_holds(stream);
   const int64_t num_slots = num_cache_blocks * cfg.block_size;
   hipError_t e = hipSuccess;
   if (k_new) {
@@ -261,6 +262,7 @@ int ragged_attention(const void* q, le_dtype act_dtype, const void* k_new, const
   c.q_heads = cfg.q_heads; c.kv_heads = cfg.kv_heads; c.head_dim = cfg.head_dim;
   c.block_size = cfg.block_size; c.scale_log2 = scale_log2;
   c.num_cache_blocks = num_cache_blocks;
+  c.l2_local = d.l2_local;
   // A mixed step is one launch (chunk and decode workgroups in one grid);
   // LE_PLAN_TWO_LAUNCHES runs the two kernels one after the other instead.
   const bool two_launches = (cfg.flags & LE_PLAN_TWO_LAUNCHES) != 0;

@@ -599,16 +599,22 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
           if constexpr (kHalfPartials<KV>) {
             const uint32_t off = static_cast<uint32_t>(((rec - rec_tile) * HD + d * 16 + grp * 4) * 2);
             const uint2 v = make_uint2(pack_f16x2(o[0], o[1]), pack_f16x2(o[2], o[3]));
-            st_coherent8(acc_rsrc, off, v);
+            if (p.l2_local) st_l2_8(acc_rsrc, off, v);
+            else st_coherent8(acc_rsrc, off, v);
           } else {
             const uint32_t off = static_cast<uint32_t>(((rec - rec_tile) * HD + d * 16 + grp * 4) * 4);
             const f32x4v v = __builtin_bit_cast(f32x4v, o);
-            st_coherent16(acc_rsrc, off, v);
+            if (p.l2_local) st_l2_16(acc_rsrc, off, v);
+            else st_coherent16(acc_rsrc, off, v);
           }
         }
         if (grp == 0) {
-          st_dev(ml + rec * 2, m_run[rs]);
-          st_dev(ml + rec * 2 + 1, l_tot[rs]);
+          if (p.l2_local) {  // the tile's partitions share this XCD's L2
+            reinterpret_cast<float2*>(ml)[rec] = make_float2(m_run[rs], l_tot[rs]);
+          } else {
+            st_dev(ml + rec * 2, m_run[rs]);
+            st_dev(ml + rec * 2 + 1, l_tot[rs]);
+          }
         }
       }
     }

@@ -4,6 +4,8 @@
 // the fused ragged kernel (attention_ragged.hip) shares.
 #include "attention_decode_wg.h"
 
+#include <atomic>
+
 namespace le {
 namespace {
 
@@ -26,6 +28,53 @@ hipError_t launch(const DecodeParams& p, hipStream_t s) {
 
 }  // namespace
 
+
+namespace {
+__global__ void xcd_probe_kernel(int* out) {
+  if (threadIdx.x == 0) {
+    unsigned v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    out[blockIdx.x + blockIdx.y * gridDim.x] = static_cast<int>(v & 0xf);
+  }
+}
+
+constexpr int kProbeW = 1000, kProbeH = 2;
+__device__ int g_xcd_probe[kProbeW * kProbeH];  // static: the check allocates nothing
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_placement[kMaxDevices];  // per device: 0 unknown, 1 holds, 2 does not
+
+// 1-D and 2-D grids of the sizes the attention launches use, wider than the
+// chip: ids equal modulo 8 must share an XCD, wherever the deal starts.
+bool probe_placement(hipStream_t stream) {
+  int* d = nullptr;
+  if (hipGetSymbolAddress(reinterpret_cast<void**>(&d), HIP_SYMBOL(g_xcd_probe)) != hipSuccess) return false;
+  static thread_local int h[kProbeW * kProbeH];
+  bool ok = true;
+  for (int shape = 0; shape < 2 && ok; shape++) {
+    const dim3 grid = shape == 0 ? dim3(kProbeW * kProbeH) : dim3(kProbeW, kProbeH);
+    xcd_probe_kernel<<<grid, 64, 0, stream>>>(d);
+    ok = hipGetLastError() == hipSuccess &&
+         hipMemcpyAsync(h, d, sizeof(h), hipMemcpyDeviceToHost, stream) == hipSuccess &&
+         hipStreamSynchronize(stream) == hipSuccess;
+    for (int i = 0; ok && i < kProbeW * kProbeH; i++) ok = h[i] == (h[0] + i) % 8;
+  }
+  return ok;
+}
+}  // namespace
+
+bool xcd_placement_holds(hipStream_t stream) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+  int st = g_placement[dev].load();
+  if (st == 0) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+      return false;  // no probe inside a capture; the write-through stores are correct anywhere
+    st = probe_placement(stream) ? 1 : 2;
+    g_placement[dev].store(st);
+  }
+  return st == 1;
+}
 
 int decode_nsplit(int n_tokens, int kv_heads) {
   const int rows = n_tokens * kv_heads;

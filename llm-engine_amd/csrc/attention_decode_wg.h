@@ -215,9 +215,11 @@ __device__ __forceinline__ void store_new_row(const DecodeParams& p, const Work&
 // Partials cross workgroups, possibly on different XCDs, whose L2s are not
 // coherent with each other: they are stored write-through (the sc1 policy of
 // agent-scope relaxed atomics) to the coherence point, and read back with
-// loads that miss the CU's L1 and the XCD's L2, so a merging workgroup never
-// reads a stale line. Agent-scope fences are avoided: they write back the
-// whole L2 of the XCD.
+// loads that miss the CU's L1 and take no stale line from the XCD's L2, so a
+// merging workgroup never reads a stale value. With l2_local every partition
+// of the row shares one XCD, and plain stores into its L2 are enough (the
+// same loads read them there). Agent-scope fences are avoided: they write
+// back the whole L2 of the XCD.
 __device__ __forceinline__ void st_dev(float* p, float v) {
   __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
@@ -287,10 +289,16 @@ __device__ __forceinline__ void write_piece(const DecodeParams& p, const Work& w
   const int64_t rec0 = static_cast<int64_t>(w.part) * p.q_heads + kvh * G;
   float* ml = reinterpret_cast<float*>(p.parts.ml);
   const __amdgpu_buffer_rsrc_t r = coherent_rsrc(p.parts.acc + rec0 * HD);
-  st_coherent16(r, static_cast<uint32_t>(c * 16), o);
-  if (c * 4 - g * HD == 0) {  // the head's first piece also writes (m, l)
-    st_dev(ml + (rec0 + g) * 2, M);
-    st_dev(ml + (rec0 + g) * 2 + 1, Ls);
+  const bool first = c * 4 - g * HD == 0;  // the head's first piece also writes (m, l)
+  if (p.l2_local) {
+    st_l2_16(r, static_cast<uint32_t>(c * 16), o);
+    if (first) reinterpret_cast<float2*>(ml)[rec0 + g] = make_float2(M, Ls);
+  } else {
+    st_coherent16(r, static_cast<uint32_t>(c * 16), o);
+    if (first) {
+      st_dev(ml + (rec0 + g) * 2, M);
+      st_dev(ml + (rec0 + g) * 2 + 1, Ls);
+    }
   }
 }
 

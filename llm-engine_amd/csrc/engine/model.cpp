@@ -179,7 +179,9 @@ class Model {
   std::vector<void*> kc_, vc_;
   DevBuf x_, h_, qkv_, q_, attn_, o_, gate_up_, act_buf_, logits_, tokens_, plan_dev_, ws_;
   HostBuf plan_host_, tokens_host_;
-  int plan_flags_ = 0;
+  // The model launches on its own stream (no CU mask), where the XCD-local
+  // exchange's precondition holds.
+  int plan_flags_ = LE_PLAN_XCD_LOCAL;
   bool capturing_ = false;  // stream_ is being captured: step buffers must not grow
   // Decode graphs: per row count, the whole decode step captured once (after
   // one eager run of the same layout) and replayed while the buffers stay.
@@ -588,7 +590,7 @@ int64_t le_model_graph_replays(const le_model* m) { return m ? m->impl->graph_re
 
 int le_model_set_plan_flags(le_model* m, int32_t flags) {
   if (!m) return LE_EINVAL;
-  if ((flags & ~LE_PLAN_TWO_LAUNCHES) != 0) return LE_EINVAL;
+  if ((flags & ~(LE_PLAN_TWO_LAUNCHES | LE_PLAN_XCD_LOCAL)) != 0) return LE_EINVAL;
   m->impl->set_plan_flags(flags);
   return LE_OK;
 }

@@ -255,7 +255,15 @@ __device__ __forceinline__ void st_coherent16(__amdgpu_buffer_rsrc_t r, uint32_t
 // launches (the last arriver resets it).
 typedef unsigned long long arrival_t;
 
+// Plain stores (write-back into the XCD's L2), for partials that only
+// workgroups on the same XCD read back (LE_PLAN_XCD_LOCAL).
+__device__ __forceinline__ void st_l2_16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, f32x4v v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4raw, v), r, byte_off, 0, 0);
+}
 typedef uint32_t u32x2raw __attribute__((vector_size(8)));
+__device__ __forceinline__ void st_l2_8(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, uint2 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2raw, v), r, byte_off, 0, 0);
+}
 __device__ __forceinline__ void st_coherent8(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, uint2 v) {
   __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2raw, v), r, byte_off, 0, kCachePolicySc1);
 }

@@ -93,7 +93,18 @@ struct DecodeParams {
   int q_heads, kv_heads, head_dim, block_size;
   float scale_log2;         // softmax scale * log2(e)
   int64_t num_cache_blocks;
+  // With items: every partition of a split row runs on one XCD (the plan's
+  // placement, and the dealing confirmed on this device by
+  // xcd_placement_holds), so partials go through that XCD's L2 with plain
+  // stores.
+  int l2_local;
 };
+
+// True when this device deals a launch's workgroups to its XCDs round robin
+// (workgroups whose linear ids are equal modulo 8 share an XCD): checked
+// once per device with a probe launch, then cached. False while the stream
+// is being captured and the device is not checked yet, or on any error.
+bool xcd_placement_holds(hipStream_t stream);
 
 hipError_t attention_decode(const DecodeParams& p, int act_dtype, int kv_dtype, hipStream_t stream);
 
@@ -113,6 +124,7 @@ struct ChunkParams {
   int q_heads, kv_heads, head_dim, block_size;
   float scale_log2;
   int64_t num_cache_blocks;
+  int l2_local;  // split tiles' partitions share an XCD: partials through its L2 (as DecodeParams)
 };
 
 hipError_t attention_chunk(const ChunkParams& p, int act_dtype, int kv_dtype, hipStream_t stream);

@@ -55,13 +55,15 @@ int round_to_blocks(int tokens, int bs) {
   return b < 1 ? 1 : b;
 }
 
-// The dispatcher sends workgroup i of a launch (linear id) to XCD i % 8, and
-// each XCD has its own L2. The partitions of a split chunk tile are kept on
-// one XCD: the groups (one tile's partitions) are dealt longest-first into
-// kXcds bins, each to the bin with the least work so far, and item k of bin b
-// goes to index k * kXcds + b. Bins are padded to one length with empty
-// items, so the item count is a multiple of kXcds and the kv head's offset in
-// the grid (a multiple of the item count) keeps every group on its bin's XCD.
+// The dispatcher deals a launch's workgroups to the XCDs round robin, so
+// workgroups whose linear ids are equal modulo 8 share an XCD, and each XCD
+// has its own L2. The partitions of a split chunk tile (always) and of a
+// split decode row (LE_PLAN_XCD_LOCAL) are kept on one XCD: the groups (one
+// tile's or row's partitions) are dealt longest-first into kXcds bins, each
+// to the bin with the least work so far, and item k of bin b goes to index
+// k * kXcds + b. Bins are padded to one length with empty items, so the item
+// count is a multiple of kXcds and the kv head's offset in the grid (a
+// multiple of the item count) keeps every group on its bin's XCD.
 template <typename Item, typename Same, typename Blocks>
 std::vector<Item> place_on_xcds(const std::vector<Item>& items, Same same_group, Blocks blocks, const Item& pad) {
   struct Group { size_t first, n; int64_t longest, work; };
@@ -101,6 +103,16 @@ std::vector<Item> place_on_xcds(const std::vector<Item>& items, Same same_group,
   return out;
 }
 
+std::vector<le::DecodeItem> place_decode_items(const std::vector<le::DecodeItem>& dec) {
+  le::DecodeItem pad{};
+  pad.token = -1;
+  pad.part = -1;
+  pad.n_parts = 0;  // resolved as no work
+  return place_on_xcds(
+      dec, [](const le::DecodeItem& a, const le::DecodeItem& b) { return a.token == b.token && a.part_begin == b.part_begin; },
+      [](const le::DecodeItem& d) { return static_cast<int64_t>(d.blk_end - d.blk_begin); }, pad);
+}
+
 std::vector<le::ChunkItem> place_chunk_items(const std::vector<le::ChunkItem>& chk) {
   le::ChunkItem pad{};
   pad.n_q = 0;  // no rows: the workgroup returns at once
@@ -121,7 +133,7 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
   if (cfg.block_size <= 0 || cfg.q_heads <= 0 || cfg.kv_heads <= 0 || cfg.head_dim <= 0)
     return LE_EINVAL;
   if (cfg.kv_dtype != LE_F32 && cfg.kv_dtype != LE_BF16 && cfg.kv_dtype != LE_F16) return LE_EINVAL;
-  if ((cfg.flags & ~LE_PLAN_TWO_LAUNCHES) != 0 || cfg.table_capacity < 0)
+  if ((cfg.flags & ~(LE_PLAN_TWO_LAUNCHES | LE_PLAN_XCD_LOCAL)) != 0 || cfg.table_capacity < 0)
     return LE_EINVAL;
   // Fixed layout (table_capacity > 0): decode rows only, a given partition.
   const bool fixed = cfg.table_capacity > 0;
@@ -276,9 +288,18 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
   // launch order, so the items on the critical path (most keys) go first.
   // Merges do not depend on the order (partials are addressed by index).
   if (fixed) parts = static_cast<int32_t>(n_tok) * parts_cap;
-  std::stable_sort(dec.begin(), dec.end(), [](const le::DecodeItem& a, const le::DecodeItem& b) {
-    return a.blk_end - a.blk_begin > b.blk_end - b.blk_begin;
-  });
+  // (With the XCD placement, the bins are dealt longest group first instead:
+  // a row's partitions must stay adjacent until they are placed.)
+  const bool xcd_local = (cfg.flags & LE_PLAN_XCD_LOCAL) && !fixed;
+  bool dec_split = false;
+  for (const auto& d : dec) dec_split |= d.part >= 0;
+  if (xcd_local && dec_split) {
+    dec = place_decode_items(dec);
+  } else {
+    std::stable_sort(dec.begin(), dec.end(), [](const le::DecodeItem& a, const le::DecodeItem& b) {
+      return a.blk_end - a.blk_begin > b.blk_end - b.blk_begin;
+    });
+  }
   bool chunk_split = false;
   for (const auto& c : chk) chunk_split |= c.part0 >= 0;
   if (chunk_split) {
@@ -341,6 +362,7 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
   if (fixed) ids_stride = std::max(dec_pb, (cfg.table_capacity + parts_cap - 1) / parts_cap);
   ids_stride = (ids_stride + 3) / 4 * 4;
   P.decode_ids_stride = ids_stride;
+  P.xcd_local = xcd_local ? 1 : 0;
   P.off_decode_ids = take(static_cast<int64_t>(dec.size() + chk.size()) * ids_stride * 4);
   P.bytes = off;
   P.dev = nullptr;

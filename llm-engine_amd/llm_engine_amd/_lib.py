@@ -23,6 +23,7 @@ LE_F32 = 0
 LE_BF16 = 1
 LE_F16 = 2
 LE_PLAN_TWO_LAUNCHES = 2
+LE_PLAN_XCD_LOCAL = 4
 
 c_i32p = ctypes.POINTER(ctypes.c_int32)
 
@@ -81,7 +82,7 @@ class StepPlan(ctypes.Structure):
         ("off_combine_items", ctypes.c_int64),
         ("off_decode_ids", ctypes.c_int64),
         ("decode_ids_stride", ctypes.c_int32),
-        ("reserved1_", ctypes.c_int32),
+        ("xcd_local", ctypes.c_int32),
         ("bytes", ctypes.c_int64),
         ("dev", ctypes.c_void_p),
     ]

@@ -81,16 +81,23 @@ def check_work_lists(plan, slices, bs=16):
     # decode items: per row, [blk_begin, blk_end) ranges tile [0, pos/bs] exactly once
     rows = {}
     lengths = []
+    row_bins = {}
+    placed = bool(P.xcd_local) and any(int(it[5]) >= 0 for it in dec)
     for k, it in enumerate(dec):
         token, p, to, b0, b1, part, pb, npart = (int(x) for x in it)
-        if npart == 0:  # padding of the fixed (graph-replay) layout
-            assert token == -1 and b0 == b1 and P.cfg.table_capacity > 0
+        if npart == 0:  # padding of the fixed layout, or of the XCD placement
+            assert token == -1 and b0 == b1 and (P.cfg.table_capacity > 0 or placed)
             continue
         assert p == pos[token] and to == toff[tseq[token]]
         rows.setdefault(token, []).append((b0, b1, part, pb, npart))
         lengths.append(b1 - b0)
-    # longest items first (the critical path starts first)
-    assert lengths == sorted(lengths, reverse=True)
+        if part >= 0:
+            row_bins.setdefault(token, set()).add(k % 8)
+    if placed:  # LE_PLAN_XCD_LOCAL: a split row's partitions at indices equal modulo 8
+        assert P.cfg.table_capacity == 0 and len(dec) % 8 == 0
+        assert all(len(b) == 1 for b in row_bins.values())
+    else:  # longest items first (the critical path starts first)
+        assert lengths == sorted(lengths, reverse=True)
     for token, items in rows.items():
         items.sort()
         assert items[0][0] == 0 and items[-1][1] == pos[token] // bs + 1
@@ -185,6 +192,29 @@ def test_packer_matches_reference_on_scheduler_steps(name, kv):
         assert np.array_equal(np.diff(cu), [s.len for s in slices])
         assert np.array_equal(plan.host_array("seq_lens_k"), [s.start + s.len for s in slices])
         check_work_lists(plan, slices)
+
+
+@pytest.mark.parametrize("name", TRACE_NAMES[:6])
+def test_xcd_local_placement_on_scheduler_steps(name):
+    """LE_PLAN_XCD_LOCAL: the same steps with every split row's and tile's
+    partitions placed at item indices equal modulo 8 (one XCD), the work
+    lists otherwise as without the flag; ignored by fixed layouts."""
+    from llm_engine_amd._lib import LE_PLAN_XCD_LOCAL
+    from llm_engine_amd.kernels import Slice
+    steps, toks = parse_trace(TRACES[f"{name}.trace"])
+    seen_split = False
+    for st in steps:
+        slices = [Slice(sid, start, ln, bool(nl), blocks, toks[sid]) for sid, start, ln, nl, pf, blocks in st]
+        for part in (0, 64):  # the planner's partitions, and 64-token ones (many split rows)
+            plan = _plan(slices, flags=LE_PLAN_XCD_LOCAL, partition_tokens=part)
+            assert plan.plan.xcd_local == 1
+            check_work_lists(plan, slices)
+            seen_split |= plan.plan.n_parts > 0
+    assert seen_split
+    dec = [Slice(i, 300 + 50 * i, 1, True, np.arange(40 * i, 40 * i + 40, dtype=np.int32),
+                 np.zeros(640, np.int32)) for i in range(6)]
+    fixed = _plan(dec, flags=LE_PLAN_XCD_LOCAL, partition_tokens=128, table_capacity=64)
+    assert fixed.plan.xcd_local == 0
 
 
 def test_slot_closed_form_and_fragmentation():

@@ -19,7 +19,7 @@ import torch
 
 from cases import loguniform_ctx, make_case, make_shared_prefix_case
 from gpu_util import device_q, emulated_bar, i32, max_abs, oracle_out, poison_unused, slices_of, to_dev_cache
-from llm_engine_amd._lib import LE_PLAN_TWO_LAUNCHES
+from llm_engine_amd._lib import LE_PLAN_TWO_LAUNCHES, LE_PLAN_XCD_LOCAL
 
 pytestmark = pytest.mark.gpu
 
@@ -170,22 +170,25 @@ def test_chunk_rows_small(gpu, kv_bf16):
     assert within(ref_shaped, want, tol_for(case, qh))
 
 
-@pytest.mark.parametrize("act,kv_bf16", [(torch.float32, True), (torch.bfloat16, True), (torch.float32, False)])
-def test_mixed_step_config3(gpu, act, kv_bf16):
+@pytest.mark.parametrize("act,kv_bf16,flags", [(torch.float32, True, 0), (torch.bfloat16, True, 0),
+                                               (torch.float32, False, 0), (torch.float32, True, LE_PLAN_XCD_LOCAL),
+                                               (torch.float32, False, LE_PLAN_XCD_LOCAL)])
+def test_mixed_step_config3(gpu, act, kv_bf16, flags):
     """Config 3: 32 decode rows (ctx U[256, 2048]) + 2 prefill chunks of 512
     at cached offsets 0 and 1024: 32 + 2 * 512 = 1056 ragged rows, with bf16
-    K/V (16-bit MFMA chunk tiles) and fp32 K/V (fp32 MFMA chunk tiles)."""
+    K/V (16-bit MFMA chunk tiles) and fp32 K/V (fp32 MFMA chunk tiles), with
+    write-through partials and with the XCD-local exchange."""
     rng = np.random.default_rng(3)
     dec_ctx = rng.integers(256, 2049, size=32)
     ctx = [512, 1536] + list(dec_ctx)
     q_len = [512, 512] + [1] * 32
     case = make_case(ctx, q_len=q_len, num_blocks=16384, seed=3, kv_bf16=kv_bf16)
-    got, qh, plan = run_ragged(case, act, gpu)
+    got, qh, plan = run_ragged(case, act, gpu, flags=flags)
     assert plan.plan.n_tokens == 1056
-    assert plan.plan.n_chunk_items > 0
+    assert plan.plan.n_chunk_items > 0 and plan.plan.xcd_local == (flags != 0)
     want = oracle_out(case, qh)
     err = max_abs(got, want)
-    print(f"config3 act={act} kv_bf16={kv_bf16}: max|err|={err:.3e}")
+    print(f"config3 act={act} kv_bf16={kv_bf16} flags={flags}: max|err|={err:.3e}")
     assert within(got, want, tol_for(case, qh), act)
 
 
@@ -418,11 +421,12 @@ def test_random_ragged_steps(gpu, seed):
                      block_size=block_size, num_blocks=need + 64, seed=seed, kv_bf16=kv_bf16)
     poison_unused(case)
     part = int(rng.choice([0, 256, 640, 2048]))
-    got, qh, plan = run_ragged(case, act, gpu, partition_tokens=part)
+    flags = int(rng.choice([0, LE_PLAN_XCD_LOCAL]))
+    got, qh, plan = run_ragged(case, act, gpu, partition_tokens=part, flags=flags)
     want = oracle_out(case, qh)
     assert np.isfinite(got).all()
     err = max_abs(got, want)
-    print(f"seed {seed}: {q_heads}/{kv_heads}x{head_dim} bs {block_size} kv_bf16 {kv_bf16} act {act} "
+    print(f"seed {seed}: {q_heads}/{kv_heads}x{head_dim} bs {block_size} kv_bf16 {kv_bf16} act {act} flags {flags} "
           f"rows {plan.plan.n_tokens} dec {plan.plan.n_decode_items} chunk {plan.plan.n_chunk_items} "
           f"parts {plan.plan.n_parts}: max|err| {err:.3e}")
     assert within(got, want, tol_for(case, qh), act)
@@ -430,16 +434,18 @@ def test_random_ragged_steps(gpu, seed):
 
 @pytest.mark.parametrize("kv_bf16", [False, True])
 def test_split_rows_merge_in_launch(gpu, kv_bf16):
-    """Split decode rows (2..7 partitions each) merge inside the launch
-    through write-through partials: against the oracle on a decode-only step
-    and on a mixed step (chunk rows beside them), as one launch and as two
+    """Split decode rows (2..7 partitions each) merge inside the launch,
+    through write-through partials and through one XCD's L2
+    (LE_PLAN_XCD_LOCAL): against the oracle on a decode-only step and on a
+    mixed step (chunk rows beside them), as one launch and as two
     (LE_PLAN_TWO_LAUNCHES)."""
     rng = np.random.default_rng(77)
     ctx = loguniform_ctx(rng, 24, 700, 4096)
     for q_len in (None, [1] * 23 + [64]):
         case = make_case(ctx, q_len=q_len, num_blocks=8192, seed=78, kv_bf16=kv_bf16)
         want = None
-        for flags in ((0,) if q_len is None else (0, LE_PLAN_TWO_LAUNCHES)):
+        shapes = (0,) if q_len is None else (0, LE_PLAN_TWO_LAUNCHES)
+        for flags in shapes + tuple(f | LE_PLAN_XCD_LOCAL for f in shapes):
             got, qh, plan = run_ragged(case, torch.float32, gpu, partition_tokens=640, flags=flags)
             if want is None:
                 want = oracle_out(case, qh)

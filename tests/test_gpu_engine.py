@@ -26,10 +26,12 @@ def prompts_of(seed, lens, vocab):
     return [rng.integers(0, vocab, n).astype(np.int32).tolist() for n in lens]
 
 
-def run_both(w, prompts, max_tokens, num_blocks, cfg=None, prefix=False, frag=0, kv="f32"):
+def run_both(w, prompts, max_tokens, num_blocks, cfg=None, prefix=False, frag=0, kv="f32", plan_flags=None):
     from e2e_util import OracleModel
     from llm_engine_amd.engine import Model, greedy_loop
     m = Model(w, num_blocks, 16, dtype="f32", kv_dtype=kv)
+    if plan_flags is not None:
+        m.set_plan_flags(plan_flags)
     gpu, stats = m.run_greedy(prompts, max_tokens, cfg, prefix, frag)
     m.close()
     o = OracleModel(w, num_blocks, kv_bf16=(kv == "bf16"))
@@ -130,6 +132,16 @@ def test_small_model_matches_oracle(gpu, case):
         gpu_t, cpu_t, _ = run_both(w, prompts, [8] * 4, 256, prefix=True)
         off, _, _ = run_both(w, prompts, [8] * 4, 256, prefix=False)
         assert off == gpu_t
+    assert gpu_t == cpu_t
+
+
+def test_write_through_partials_end_to_end(gpu):
+    """The engine's plans default to the XCD-local exchange of split rows'
+    partials; with the flags cleared (write-through partials) the fragmented
+    multi-sequence case still equals the oracle token for token."""
+    w = qwen_small()
+    prompts = prompts_of(1, (20, 150, 300, 47, 900), w.arch["vocab"])
+    gpu_t, cpu_t, _ = run_both(w, prompts, [8] * 5, 256, frag=40, plan_flags=0)
     assert gpu_t == cpu_t
 
 
