@@ -418,7 +418,9 @@ def phase_summary(n_workgroups):
         raise SystemExit("bench.py --phases: no stamps (decode-only workloads run the stamped kernel)")
     us = (t[:, :5] - t[:, 0].min()) / 100.0  # realtime counter: 100 MHz
     split = (t[:, 6] & 0xffffffff) > 0
-    out = {"workgroups": int(len(t)), "distinct_cus": int(len(set(t[:, 5].tolist())))}
+    # a CU: XCC_ID with HW_ID's cu/sh/se fields (bits 8-15; the low bits name the wave and SIMD)
+    cus = set(zip((t[:, 5] >> 32).tolist(), ((t[:, 5] >> 8) & 0xff).tolist()))
+    out = {"workgroups": int(len(t)), "distinct_cus": int(len(cus))}
     for i, name in enumerate(("start", "staged", "tiles_done", "written", "end")):
         out[name] = {"median": round(float(np.median(us[:, i])), 2), "max": round(float(us[:, i].max()), 2)}
     if split.any():
