@@ -802,7 +802,10 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
   LE_TIM(6, (static_cast<uint64_t>(w.b_end - w.b_begin) << 32) | static_cast<uint32_t>(w.part < 0 ? 0 : w.n_parts));
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
-  const int wave = tid >> 6;
+  // 16-bit tiles: the wave index made provably uniform, so the streaming
+  // loop's branches are scalar (fp32 tiles measured faster without it:
+  // config 2 20.0 against 20.5 us)
+  const int wave = sizeof(KV) == 2 ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
   const int col = lane & 15;   // head of the group (B/C column); key row for A loads
   const int grp = lane >> 4;   // k-group
   const int kvh = by;
@@ -879,14 +882,36 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
       // same loads outstanding and the wait before it covers only the tile
       // being computed.
       typename T::Regs rb;
-      while (true) {
+      if constexpr (sizeof(KV) == 2) {
+        // This wave's tiles: key0, key0 + stride, ... below key_end (at
+        // least one). Pairs run in a loop with one exit and a trip count known
+        // at its entry; the last one or two tiles follow it. (A loop with two
+        // exits, as below, leaves the compiler's structurizer a dead back
+        // edge on which the other buffer's loads are still pending, and the
+        // loop head then waits for every load: the two tiles never overlap.
+        // 64 x 4096: 27.9 -> 27.3 us.)
+        const int n_tiles = (key_end - key0 + stride - 1) / stride;
+        const int pairs = (n_tiles - 1) >> 1;
+        for (int i = 0; i < pairs; i++) {
+          T::load(rb, kc, vc, key0 + stride, key_end, kv_stride, bs_shift, tab, sb0, col);
+          T::compute(st, ra, qb, key0, key_end, p.scale_log2, vt, col, grp);
+          T::load(ra, kc, vc, key0 + 2 * stride, key_end, kv_stride, bs_shift, tab, sb0, col);
+          T::compute(st, rb, qb, key0 + stride, key_end, p.scale_log2, vt, col, grp);
+          key0 += 2 * stride;
+        }
         T::load(rb, kc, vc, key0 + stride, key_end, kv_stride, bs_shift, tab, sb0, col);
         T::compute(st, ra, qb, key0, key_end, p.scale_log2, vt, col, grp);
-        if (key0 + stride >= key_end) break;
-        T::load(ra, kc, vc, key0 + 2 * stride, key_end, kv_stride, bs_shift, tab, sb0, col);
-        T::compute(st, rb, qb, key0 + stride, key_end, p.scale_log2, vt, col, grp);
-        if (key0 + 2 * stride >= key_end) break;
-        key0 += 2 * stride;
+        if (n_tiles - 2 * pairs == 2) T::compute(st, rb, qb, key0 + stride, key_end, p.scale_log2, vt, col, grp);
+      } else {  // fp32 tiles: the two-exit loop measured faster (config 2 20.0 against 20.5 us)
+        while (true) {
+          T::load(rb, kc, vc, key0 + stride, key_end, kv_stride, bs_shift, tab, sb0, col);
+          T::compute(st, ra, qb, key0, key_end, p.scale_log2, vt, col, grp);
+          if (key0 + stride >= key_end) break;
+          T::load(ra, kc, vc, key0 + 2 * stride, key_end, kv_stride, bs_shift, tab, sb0, col);
+          T::compute(st, rb, qb, key0 + stride, key_end, p.scale_log2, vt, col, grp);
+          if (key0 + 2 * stride >= key_end) break;
+          key0 += 2 * stride;
+        }
       }
     } else {
       while (true) {
