@@ -397,38 +397,51 @@ def attention_leg(workload, kv, L, steps, warmup, partition=0, chunk_partition=0
     return res
 
 
-def phase_summary(n_workgroups):
-    """Per-phase stamps of the last decode launch, from a measurement build
+def phase_summary(mixed):
+    """Per-phase stamps of the last attention launch, from a measurement build
     (python llm-engine_amd/build.py -D LE_TIMING --out <dir>/libllm_engine_amd.so,
     loaded with LE_LIB_PATH): microseconds from the first workgroup's start,
-    median and max over workgroups, per phase (attention_decode_wg.h, slots
-    0-4), with the number of distinct CUs the workgroups ran on."""
+    median and max over workgroups, per phase (le_common.h, slots 0-4), per
+    workgroup kind (decode, chunk), with the number of distinct CUs the
+    workgroups ran on. `mixed` reads the fused mixed-step kernel's stamps,
+    which live in its own translation unit."""
     import ctypes
     from llm_engine_amd import _lib
     lib = _lib.load()
-    if not hasattr(lib, "le_timing_read"):
+    fn = "le_timing_read_ragged" if mixed else "le_timing_read"
+    if not hasattr(lib, fn):
         raise SystemExit("bench.py --phases needs a LE_TIMING build (LE_LIB_PATH)")
     buf = np.zeros(65536 * 8, dtype=np.uint64)
-    rc = lib.le_timing_read(ctypes.c_void_p(buf.ctypes.data), ctypes.c_int64(buf.nbytes))
+    rc = getattr(lib, fn)(ctypes.c_void_p(buf.ctypes.data), ctypes.c_int64(buf.nbytes))
     if rc != 0:
-        raise SystemExit(f"le_timing_read: {rc}")
-    t = buf[:n_workgroups * 8].reshape(n_workgroups, 8).astype(np.int64)
-    t = t[t[:, 0] > 0]
-    if not len(t):  # the fused mixed-step kernel keeps its own stamps (another translation unit)
-        raise SystemExit("bench.py --phases: no stamps (decode-only workloads run the stamped kernel)")
-    us = (t[:, :5] - t[:, 0].min()) / 100.0  # realtime counter: 100 MHz
-    split = (t[:, 6] & 0xffffffff) > 0
+        raise SystemExit(f"{fn}: {rc}")
+    t = buf.reshape(65536, 8).astype(np.int64)
+    t = t[(t[:, 0] > 0) & (t[:, 7] > 0)]
+    if not len(t):
+        raise SystemExit("bench.py --phases: no stamps")
+    t = t[t[:, 0] >= t[:, 0].max() - 100000]  # the last launch (stamps of launches 1 ms before stay)
+    t0 = t[:, 0].min()
     # a CU: XCC_ID with HW_ID's cu/sh/se fields (bits 8-15; the low bits name the wave and SIMD)
     cus = set(zip((t[:, 5] >> 32).tolist(), ((t[:, 5] >> 8) & 0xff).tolist()))
     out = {"workgroups": int(len(t)), "distinct_cus": int(len(cus))}
-    for i, name in enumerate(("start", "staged", "tiles_done", "written", "end")):
-        out[name] = {"median": round(float(np.median(us[:, i])), 2), "max": round(float(us[:, i].max()), 2)}
-    if split.any():
-        out["end_split_rows"] = {"median": round(float(np.median(us[split, 4])), 2),
-                                 "max": round(float(us[split, 4].max()), 2)}
-    if (~split).any():
-        out["end_unsplit_rows"] = {"median": round(float(np.median(us[~split, 4])), 2),
-                                   "max": round(float(us[~split, 4].max()), 2)}
+
+    def stat(x):
+        return {"median": round(float(np.median(x)), 2), "max": round(float(x.max()), 2)}
+
+    for kind, kname in ((1, "decode"), (2, "chunk")):
+        k = t[t[:, 7] == kind]
+        if not len(k):
+            continue
+        us = (k[:, :5] - t0) / 100.0  # realtime counter: 100 MHz
+        split = (k[:, 6] & 0xffffffff) > 0
+        o = {"workgroups": int(len(k))}
+        for i, name in enumerate(("start", "staged", "tiles_done", "written", "end")):
+            o[name] = stat(us[:, i])
+        if split.any():
+            o["end_split"] = stat(us[split, 4])
+        if (~split).any():
+            o["end_unsplit"] = stat(us[~split, 4])
+        out[kname] = o
     return out
 
 
@@ -611,7 +624,7 @@ def main():
     res = attention_leg(args.workload, args.kv, args.layers, args.steps, args.warmup, args.partition,
                         args.chunk_partition, args.graph, args.separate_scatter, args.flags)
     if args.phases:
-        res["phases"] = phase_summary(res["plan"]["decode_items"] * KV_HEADS)
+        res["phases"] = phase_summary(res["plan"].get("chunk_items", 0) > 0)
     if extras:
         for key, extra, kv in extras:
             sub = attention_leg(extra, kv, args.layers, max(10, args.steps // 2), args.warmup, flags=args.flags)

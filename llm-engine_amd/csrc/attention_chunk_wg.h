@@ -237,8 +237,13 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
   const int wave = tid >> 6;
   const int col = lane & 15;  // query row of this lane within a 16-row tile
   const int grp = lane >> 4;  // k-group of this lane
+  [[maybe_unused]] const uint64_t t_start = LE_TIM_NOW();
   const ChunkItem it = p.items[item];
   if (it.n_q <= 0) return;  // padding that keeps split tiles on one XCD
+  LE_TIM(0, t_start);
+  LE_TIM(5, LE_TIM_PLACE());
+  LE_TIM(6, (static_cast<uint64_t>(it.blk_end - it.blk_begin) << 32) | static_cast<uint32_t>(it.part0 < 0 ? 0 : it.part_stride));
+  LE_TIM(7, 2);
   const int G = p.q_heads / p.kv_heads;
   const bool computes = wave < G;
   const int head = kvh * G + (computes ? wave : 0);
@@ -366,6 +371,7 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
   for (int rel0 = 0;;) {
     stash();
     __syncthreads();
+    if (rel0 == 0) LE_TIM(1, LE_TIM_NOW());
     const int s0 = key_begin + rel0;
     if (computes) {
       const int key_end = key_begin + it.key_live;  // past the last row's position: dead
@@ -553,6 +559,7 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
     issue(rel0);
   }
 
+  LE_TIM(2, LE_TIM_NOW());
   // acc[rs][d][j] = O[row rs*16 + col][dim d*16 + grp*4 + j]
   float l_tot[2];
 #pragma unroll
@@ -572,6 +579,11 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
         }
       }
     }
+#ifdef LE_TIMING
+    __builtin_amdgcn_s_waitcnt(0);
+    LE_TIM(3, LE_TIM_NOW());
+    LE_TIM(4, LE_TIM_NOW());
+#endif
     return;
   }
 
@@ -621,12 +633,16 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
   }
   __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are performed
   __syncthreads();                // ... and every other thread's
+  LE_TIM(3, LE_TIM_NOW());
   arrival_t* counter = p.parts.counters + static_cast<int64_t>(tok0) * p.kv_heads + kvh;
   if (tid == 0) {
     const arrival_t seen = __hip_atomic_fetch_add(counter, arrival_t{1}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     last = seen == static_cast<arrival_t>(it.part_stride - 1);
   }
   __syncthreads();
+#ifdef LE_TIMING
+  if (!last) LE_TIM(4, LE_TIM_NOW());
+#endif
   if (!last) return;
 
   // Every other partition incremented the counter after its partials were
@@ -642,6 +658,10 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
     merge_tile<ACT, HD, 3, kHalfPartials<KV>>(p, it, acc_rsrc, ml, rec_tile, base, J, G, kvh, nq, tok0);
   }
   if (tid == 0) __hip_atomic_store(counter, arrival_t{0}, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#ifdef LE_TIMING
+  __builtin_amdgcn_s_waitcnt(0);  // the merge's output stores are performed
+  LE_TIM(4, LE_TIM_NOW());
+#endif
 }
 }  // namespace
 }  // namespace chk

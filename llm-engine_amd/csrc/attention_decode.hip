@@ -97,7 +97,7 @@ hipError_t attention_decode(const DecodeParams& p, int act_dtype, int kv_dtype, 
 // Measurement builds only (build.py --timing): the decode workgroups' phase
 // stamps of the last launch, [workgroup][8] uint64 (see g_timing).
 extern "C" int le_timing_read(void* host, int64_t bytes) {
-  return static_cast<int>(hipMemcpyFromSymbol(host, HIP_SYMBOL(le::dec::g_timing), static_cast<size_t>(bytes), 0,
+  return static_cast<int>(hipMemcpyFromSymbol(host, HIP_SYMBOL(le::g_timing), static_cast<size_t>(bytes), 0,
                                               hipMemcpyDeviceToHost));
 }
 #endif

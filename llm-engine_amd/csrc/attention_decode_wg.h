@@ -50,37 +50,6 @@ constexpr int kMergeBatch = 8;       // partial accumulators loaded per batch in
 
 
 
-// Phase stamps (measurement builds, -DLE_TIMING; no code otherwise): thread
-// 0 of each decode workgroup records realtime stamps (100 MHz) of its phases
-// and the CU/XCD it ran on, per linear workgroup id; the last launch's values
-// stay. Slots: 0 start, 1 item and block ids staged, 2 tiles done, 3 output
-// or partial written, 4 end (after the split row's arrival and merge),
-// 5 HW_ID | XCC_ID << 32, 6 partition blocks << 32 | partitions of its row.
-#ifdef LE_TIMING
-constexpr int kTimSlots = 8;
-constexpr int kTimWorkgroups = 65536;
-__device__ uint64_t g_timing[kTimWorkgroups * kTimSlots];
-__device__ __forceinline__ void tim_put(int slot, uint64_t v) {
-  if (threadIdx.x == 0) {
-    const int64_t wg = blockIdx.x + static_cast<int64_t>(blockIdx.y) * gridDim.x;
-    if (wg < kTimWorkgroups) g_timing[wg * kTimSlots + slot] = v;
-  }
-}
-__device__ __forceinline__ uint64_t tim_place() {
-  uint32_t hw, xcc;
-  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
-  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-  return (static_cast<uint64_t>(xcc) << 32) | hw;
-}
-#define LE_TIM(slot, v) tim_put(slot, v)
-#define LE_TIM_NOW() __builtin_amdgcn_s_memrealtime()
-#define LE_TIM_PLACE() tim_place()
-#else
-#define LE_TIM(slot, v) ((void)0)
-#define LE_TIM_NOW() uint64_t{0}
-#define LE_TIM_PLACE() uint64_t{0}
-#endif
-
 struct Work {
   int token, pos, table_off, b_begin, b_end, part, part_begin, n_parts;
   bool valid;
@@ -799,6 +768,7 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
   if (!w.valid) return;
   LE_TIM(0, t_start);
   LE_TIM(5, LE_TIM_PLACE());
+  LE_TIM(7, 1);
   LE_TIM(6, (static_cast<uint64_t>(w.b_end - w.b_begin) << 32) | static_cast<uint32_t>(w.part < 0 ? 0 : w.n_parts));
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);

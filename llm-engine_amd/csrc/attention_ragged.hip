@@ -69,3 +69,12 @@ hipError_t attention_ragged(const DecodeParams& d, const ChunkParams& c, int act
 }
 
 }  // namespace le
+
+#ifdef LE_TIMING
+// Measurement builds only: the mixed-step kernel's phase stamps of its last
+// launch (decode and chunk workgroups; slot 7 tells them apart).
+extern "C" int le_timing_read_ragged(void* host, int64_t bytes) {
+  return static_cast<int>(hipMemcpyFromSymbol(host, HIP_SYMBOL(le::g_timing), static_cast<size_t>(bytes), 0,
+                                              hipMemcpyDeviceToHost));
+}
+#endif

@@ -287,4 +287,39 @@ __host__ __device__ inline auto with_dtype16(int dt, F&& f) {
   return f(bf16_t{});
 }
 
+namespace {
+// Phase stamps (measurement builds, -DLE_TIMING; no code otherwise): thread
+// 0 of each attention workgroup records realtime stamps (100 MHz) of its phases
+// and the CU/XCD it ran on, per linear workgroup id; the last launch's values
+// stay. Slots: 0 start, 1 item and block ids staged, 2 tiles done, 3 output
+// or partial written, 4 end (after the split row's arrival and merge),
+// 5 HW_ID | XCC_ID << 32, 6 partition blocks << 32 | partitions of its row
+// (or tile), 7 kind (1 decode, 2 chunk). Chunk workgroups stamp 1 after
+// their first stage is in LDS and 2 after their last tile.
+#ifdef LE_TIMING
+constexpr int kTimSlots = 8;
+constexpr int kTimWorkgroups = 65536;
+__device__ uint64_t g_timing[kTimWorkgroups * kTimSlots];
+__device__ __forceinline__ void tim_put(int slot, uint64_t v) {
+  if (threadIdx.x == 0) {
+    const int64_t wg = blockIdx.x + static_cast<int64_t>(blockIdx.y) * gridDim.x;
+    if (wg < kTimWorkgroups) g_timing[wg * kTimSlots + slot] = v;
+  }
+}
+__device__ __forceinline__ uint64_t tim_place() {
+  uint32_t hw, xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  return (static_cast<uint64_t>(xcc) << 32) | hw;
+}
+#define LE_TIM(slot, v) tim_put(slot, v)
+#define LE_TIM_NOW() __builtin_amdgcn_s_memrealtime()
+#define LE_TIM_PLACE() tim_place()
+#else
+#define LE_TIM(slot, v) ((void)0)
+#define LE_TIM_NOW() uint64_t{0}
+#define LE_TIM_PLACE() uint64_t{0}
+#endif
+
+}  // namespace
 }  // namespace le
