@@ -411,11 +411,11 @@ def phase_summary(mixed):
     fn = "le_timing_read_ragged" if mixed else "le_timing_read"
     if not hasattr(lib, fn):
         raise SystemExit("bench.py --phases needs a LE_TIMING build (LE_LIB_PATH)")
-    buf = np.zeros(65536 * 8, dtype=np.uint64)
+    buf = np.zeros(65536 * 16, dtype=np.uint64)
     rc = getattr(lib, fn)(ctypes.c_void_p(buf.ctypes.data), ctypes.c_int64(buf.nbytes))
     if rc != 0:
         raise SystemExit(f"{fn}: {rc}")
-    t = buf.reshape(65536, 8).astype(np.int64)
+    t = buf.reshape(65536, 16).astype(np.int64)
     t = t[(t[:, 0] > 0) & (t[:, 7] > 0)]
     if not len(t):
         raise SystemExit("bench.py --phases: no stamps")
@@ -437,6 +437,13 @@ def phase_summary(mixed):
         o = {"workgroups": int(len(k))}
         for i, name in enumerate(("start", "staged", "tiles_done", "written", "end")):
             o[name] = stat(us[:, i])
+        if kind == 1 and (k[:, 8] > 0).any():  # round-trip probe build (LE_TIMING_RT)
+            o["ids_back"] = stat((k[:, 8] - t0) / 100.0)
+            o["first_tile_back"] = stat((k[:, 9] - t0) / 100.0)
+        if kind == 2:  # every wave's tiles done (slots 8-15; 0 for waves that never stamp)
+            w = k[:, 8:16]
+            done = np.where(w > 0, w, 0).max(axis=1)
+            o["tiles_done_all_waves"] = stat((done - t0) / 100.0)
         if split.any():
             o["end_split"] = stat(us[split, 4])
         if (~split).any():

@@ -560,6 +560,7 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
   }
 
   LE_TIM(2, LE_TIM_NOW());
+  LE_TIM_WAVE(8, LE_TIM_NOW());
   // acc[rs][d][j] = O[row rs*16 + col][dim d*16 + grp*4 + j]
   float l_tot[2];
 #pragma unroll

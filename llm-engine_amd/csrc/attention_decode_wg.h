@@ -758,12 +758,21 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
       pre_ids[u] = i < p.ids_stride ? ids_row[i] : -1;
     }
   }
+#ifdef LE_TIMING_RT
+  // round-trip probe (measurement builds only; serialises the first loads)
+  __builtin_amdgcn_s_waitcnt(0);
+  LE_TIM(8, LE_TIM_NOW());
+#endif
   if (early) {
     T::load_direct(ra, T::lane_base(p.k_cache, by, threadIdx.x >> 4 & 3),
                    T::lane_base(p.v_cache, by, threadIdx.x >> 4 & 3), (threadIdx.x >> 6) * T::kKeys,
                    ids_row, p.ids_stride, __builtin_ctz(p.block_size), p.kv_heads * HD, p.num_cache_blocks,
                    threadIdx.x & 15);
   }
+#ifdef LE_TIMING_RT
+  __builtin_amdgcn_s_waitcnt(0);
+  LE_TIM(9, LE_TIM_NOW());
+#endif
   const Work w = resolve(p, bx, bz);
   if (!w.valid) return;
   LE_TIM(0, t_start);

@@ -294,16 +294,23 @@ namespace {
 // stay. Slots: 0 start, 1 item and block ids staged, 2 tiles done, 3 output
 // or partial written, 4 end (after the split row's arrival and merge),
 // 5 HW_ID | XCC_ID << 32, 6 partition blocks << 32 | partitions of its row
-// (or tile), 7 kind (1 decode, 2 chunk). Chunk workgroups stamp 1 after
-// their first stage is in LDS and 2 after their last tile.
+// (or tile), 7 kind (1 decode, 2 chunk), 8 + w wave w's tiles done (chunk
+// workgroups; slot 2 is wave 0's). Chunk workgroups stamp 1 after their first
+// stage is in LDS and 2 after their last tile.
 #ifdef LE_TIMING
-constexpr int kTimSlots = 8;
+constexpr int kTimSlots = 16;
 constexpr int kTimWorkgroups = 65536;
 __device__ uint64_t g_timing[kTimWorkgroups * kTimSlots];
 __device__ __forceinline__ void tim_put(int slot, uint64_t v) {
   if (threadIdx.x == 0) {
     const int64_t wg = blockIdx.x + static_cast<int64_t>(blockIdx.y) * gridDim.x;
     if (wg < kTimWorkgroups) g_timing[wg * kTimSlots + slot] = v;
+  }
+}
+__device__ __forceinline__ void tim_put_wave(int slot, uint64_t v) {
+  if ((threadIdx.x & 63) == 0) {
+    const int64_t wg = blockIdx.x + static_cast<int64_t>(blockIdx.y) * gridDim.x;
+    if (wg < kTimWorkgroups) g_timing[wg * kTimSlots + slot + (threadIdx.x >> 6)] = v;
   }
 }
 __device__ __forceinline__ uint64_t tim_place() {
@@ -313,10 +320,12 @@ __device__ __forceinline__ uint64_t tim_place() {
   return (static_cast<uint64_t>(xcc) << 32) | hw;
 }
 #define LE_TIM(slot, v) tim_put(slot, v)
+#define LE_TIM_WAVE(slot, v) tim_put_wave(slot, v)
 #define LE_TIM_NOW() __builtin_amdgcn_s_memrealtime()
 #define LE_TIM_PLACE() tim_place()
 #else
 #define LE_TIM(slot, v) ((void)0)
+#define LE_TIM_WAVE(slot, v) ((void)0)
 #define LE_TIM_NOW() uint64_t{0}
 #define LE_TIM_PLACE() uint64_t{0}
 #endif
