@@ -42,8 +42,11 @@
 //     per tile and kv head, reset by it) merges them in partition order,
 //     inside the launch.
 // 16-bit caches: 16-bit operands (q and P rounded to the cache type), fp32
-// accumulation. fp32 caches: the same tile on v_mfma_f32_16x16x4_f32 (exact
-// fp32 products), K/V staged 192 keys at a time.
+// accumulation. fp32 caches, head_dim 64: the same tile on the bf16 MFMA with
+// every operand in three bf16 terms (products to within the rounding of an
+// fp32 product, below), K/V staged 128 keys at a time, the next stage's
+// loads in flight during a stage's compute. fp32 caches, head_dim 128: the
+// tile on v_mfma_f32_16x16x4_f32 (exact fp32 products), 64 keys a stage.
 #include <float.h>
 
 #include <type_traits>
@@ -59,13 +62,28 @@ namespace {
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * kWave;
 constexpr int kTileKeys = 64;    // keys per MFMA tile
+// fp32 caches with head_dim 64 run on the bf16 MFMA with every operand held
+// as three bf16 terms, a = hi + mid + lo (hi = bf16(a), mid = bf16(a - hi),
+// lo = bf16(a - hi - mid); both subtractions are exact in fp32), and every
+// product as the six terms of order at least 2^-16: hi*hi + hi*mid + mid*hi
+// + hi*lo + mid*mid + lo*hi (each exact in the fp32 accumulator). The terms
+// left out and lo's rounding are each below 2^-24 |a b|, the size of an fp32
+// product's own rounding. The 16x16x32 bf16 MFMA does a product of 32 keys
+// or dims at 16 times the fp32 MFMA's rate, so six of them cost 2.7 times
+// less than the 16x16x4 fp32 MFMAs they replace. K and V are split once, when
+// a stage is stored to LDS, into three bf16 planes; q once per workgroup and
+// P per tile in registers. fp32 caches with head_dim 128 keep the fp32 MFMA
+// (the three q planes of 128 dims do not fit beside its accumulators).
+template <typename KV, int HD> constexpr bool kSplit3 = std::is_same_v<KV, float> && HD == 64;
+template <typename KV, int HD> constexpr int kPlanes = kSplit3<KV, HD> ? 3 : 1;
 // Keys staged in LDS at once: with a 16-bit cache 384 for head_dim 64 (110 KB
 // of K and V rows, so a default 384-key partition is one memory round trip)
-// and 256 for head_dim 128 (139 KB); with an fp32 cache 192 (104 KB) and 64
-// (68 KB; the registers of 128 keys' staging loads do not fit beside the
-// head_dim 128 accumulators). Always whole 64-key MFMA tiles.
+// and 256 for head_dim 128 (139 KB); with an fp32 cache 128 for head_dim 64
+// (three bf16 planes of K and of V, 110 KB) and 64 for head_dim 128 (68 KB;
+// the registers of 128 keys' staging loads do not fit beside the head_dim
+// 128 accumulators). Always whole 64-key MFMA tiles.
 template <typename KV, int HD>
-constexpr int kStageKeys = sizeof(KV) == 2 ? (HD == 64 ? 384 : 256) : (HD == 64 ? 192 : 64);
+constexpr int kStageKeys = sizeof(KV) == 2 ? (HD == 64 ? 384 : 256) : (HD == 64 ? 128 : 64);
 constexpr int kRowsMax = 32;     // query rows per item
 constexpr int kMaxG = 8;         // query heads per kv head
 constexpr int kMaxSplit = 16;    // partitions of one tile the merge stages in LDS
@@ -78,10 +96,31 @@ __device__ __forceinline__ float vmax3(float a, float b, float c) {
 }
 
 template <typename KV, int HD> struct ChunkLds {
-  static constexpr int ROW = HD * static_cast<int>(sizeof(KV)) + 16;  // bytes per key row of K and of V (padded)
-  static constexpr int K_BYTES = kStageKeys<KV, HD> * ROW;
-  static constexpr int BYTES = 2 * K_BYTES;  // K rows, then V rows
+  // bytes per key row of K and of V (padded); bf16 rows for split fp32
+  static constexpr int ROW = HD * (kSplit3<KV, HD> ? 2 : static_cast<int>(sizeof(KV))) + 16;
+  static constexpr int PLANE = kStageKeys<KV, HD> * ROW;  // one plane of the stage's K or V rows
+  static constexpr int K_BYTES = kPlanes<KV, HD> * PLANE;
+  static constexpr int BYTES = 2 * K_BYTES;  // K rows (planes hi, mid, lo), then V rows
 };
+
+// a = hi + mid + lo in bf16 terms (the split of the fp32 path above)
+struct Bf3 { __bf16 hi, mid, lo; };
+__device__ __forceinline__ Bf3 split3(float a) {
+  Bf3 t;
+  t.hi = static_cast<__bf16>(a);
+  const float r = a - static_cast<float>(t.hi);
+  t.mid = static_cast<__bf16>(r);
+  t.lo = static_cast<__bf16>(r - static_cast<float>(t.mid));
+  return t;
+}
+// element e of three operand vectors from one split
+template <typename V>
+__device__ __forceinline__ void put3(V& h, V& m, V& l, int e, float a) {
+  const Bf3 t = split3(a);
+  h[e] = t.hi;
+  m[e] = t.mid;
+  l[e] = t.lo;
+}
 
 __device__ __forceinline__ void st_dev(float* p, float v) {
   __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
@@ -212,9 +251,11 @@ __device__ __forceinline__ void merge_tile(const ChunkParams& p, const ChunkItem
 template <typename ACT, typename KV, int HD>
 __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>& sm, int item, int kvh) {
   // 16-bit caches: the 16x16x32 MFMA of the cache type (q and P rounded to
-  // it). fp32 caches: v_mfma_f32_16x16x4_f32, exact fp32 products.
-  constexpr bool kF32 = std::is_same_v<KV, float>;
-  using M = mma16<std::conditional_t<kF32, bf16_t, KV>>;
+  // it). fp32 caches: the bf16 MFMA on three-term operands (head_dim 64) or
+  // v_mfma_f32_16x16x4_f32, exact fp32 products (head_dim 128).
+  constexpr bool kSplit = kSplit3<KV, HD>;                    // fp32 operands as three bf16 terms
+  constexpr bool kF32 = std::is_same_v<KV, float> && !kSplit;  // fp32 operands on the fp32 MFMA
+  using M = mma16<std::conditional_t<std::is_same_v<KV, float>, bf16_t, KV>>;
   using V8 = typename M::v8;
   using S16 = typename M::scalar;
   using L = ChunkLds<KV, HD>;
@@ -292,9 +333,26 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
     for (int k = 0; k < PER / 2; k++) {
       const int piece = tid + k * kThreads;  // as in issue(): the LDS place is recomputed, not kept
       const int key_l = piece / CPR, c = piece - key_l * CPR;
-      const int dst = key_l * L::ROW + c * 16;
-      *reinterpret_cast<uint4*>(lds + dst) = okp[k] ? kv[0][k] : make_uint4(0, 0, 0, 0);
-      *reinterpret_cast<uint4*>(lds + L::K_BYTES + dst) = okp[k] ? kv[1][k] : make_uint4(0, 0, 0, 0);
+      if constexpr (kSplit) {
+        // four fp32 dims become 8 bytes in each of the three bf16 planes
+        const int dst = key_l * L::ROW + c * 8;
+#pragma unroll
+        for (int kv_i = 0; kv_i < 2; kv_i++) {
+          const uint4 u = okp[k] ? kv[kv_i][k] : make_uint4(0, 0, 0, 0);
+          const float f[4] = {__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w)};
+          typename M::v4 h, m, l;
+#pragma unroll
+          for (int e = 0; e < 4; e++) put3(h, m, l, e, f[e]);
+          char* base = lds + kv_i * L::K_BYTES + dst;
+          *reinterpret_cast<typename M::v4*>(base) = h;
+          *reinterpret_cast<typename M::v4*>(base + L::PLANE) = m;
+          *reinterpret_cast<typename M::v4*>(base + 2 * L::PLANE) = l;
+        }
+      } else {
+        const int dst = key_l * L::ROW + c * 16;
+        *reinterpret_cast<uint4*>(lds + dst) = okp[k] ? kv[0][k] : make_uint4(0, 0, 0, 0);
+        *reinterpret_cast<uint4*>(lds + L::K_BYTES + dst) = okp[k] ? kv[1][k] : make_uint4(0, 0, 0, 0);
+      }
     }
   };
   // Query rows first (they are needed last, and a wait for them must not
@@ -335,15 +393,20 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
       for (int e = 0; e < 8; e++) qf[rs][u * 8 + e] = ok ? f[e] * p.scale_log2 : 0.f;
     }
   }
-  // 16-bit path: Q^T operands, this lane's 8 dims per k-step of rows col and 16 + col
+  // 16-bit path: Q^T operands, this lane's 8 dims per k-step of rows col and
+  // 16 + col (split fp32: qb, qm, ql the three terms)
   V8 qb[2][KS];
+  [[maybe_unused]] V8 qm[2][KS], ql[2][KS];
   if constexpr (!kF32) {
 #pragma unroll
     for (int rs = 0; rs < 2; rs++)
 #pragma unroll
       for (int ks = 0; ks < KS; ks++)
 #pragma unroll
-        for (int e = 0; e < 8; e++) qb[rs][ks][e] = static_cast<S16>(qf[rs][ks * 8 + e]);
+        for (int e = 0; e < 8; e++) {
+          if constexpr (kSplit) put3(qb[rs][ks], qm[rs][ks], ql[rs][ks], e, qf[rs][ks * 8 + e]);
+          else qb[rs][ks][e] = static_cast<S16>(qf[rs][ks * 8 + e]);
+        }
   }
 
   f32x4 acc[2][DT];
@@ -360,7 +423,7 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
   float sbase[2] = {0.f, 0.f};
   f32x4 nbase[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};  // -sbase, the MFMA's C operand
   // 16-bit path: lsum[rs][0] of the lanes of group 0 = the row's sum of p
-  // (row col), summed on the MFMA; the other entries stay zero. fp32 path:
+  // (row col), summed on the MFMA; the other entries stay zero. fp32 paths:
   // lsum[rs][0] of every lane = its share of the row's sum (the keys of its
   // lane group). Either way the row sum is lsum[rs][0] summed over the four
   // lane groups.
@@ -372,6 +435,9 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
     stash();
     __syncthreads();
     if (rel0 == 0) LE_TIM(1, LE_TIM_NOW());
+    // split fp32: the next stage's loads leave before this stage's compute
+    if constexpr (kSplit)
+      if (rel0 + kStageKeys<KV, HD> < it.key_live) issue(rel0 + kStageKeys<KV, HD>);
     const int s0 = key_begin + rel0;
     if (computes) {
       const int key_end = key_begin + it.key_live;  // past the last row's position: dead
@@ -384,7 +450,28 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
         for (int rs = 0; rs < 2; rs++)
 #pragma unroll
           for (int i = 0; i < 4; i++) s[rs][i] = nbase[rs];
-        if constexpr (!kF32) {
+        if constexpr (kSplit) {
+          // per 16 keys x 32 dims: the three K terms, then both row tiles'
+          // six products, smallest terms first
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int ks = 0; ks < KS; ks++) {
+              const char* kp = kt_lds + (i * 16 + col) * L::ROW + (ks * 32 + grp * 8) * 2;
+              const V8 kh = *reinterpret_cast<const V8*>(kp);
+              const V8 km = *reinterpret_cast<const V8*>(kp + L::PLANE);
+              const V8 kl = *reinterpret_cast<const V8*>(kp + 2 * L::PLANE);
+#pragma unroll
+              for (int rs = 0; rs < 2; rs++) {
+                s[rs][i] = M::mma(kl, qb[rs][ks], s[rs][i]);
+                s[rs][i] = M::mma(km, qm[rs][ks], s[rs][i]);
+                s[rs][i] = M::mma(kh, ql[rs][ks], s[rs][i]);
+                s[rs][i] = M::mma(km, qb[rs][ks], s[rs][i]);
+                s[rs][i] = M::mma(kh, qm[rs][ks], s[rs][i]);
+                s[rs][i] = M::mma(kh, qb[rs][ks], s[rs][i]);
+              }
+            }
+        } else if constexpr (!kF32) {
           // the tile's K fragments, then row tile 0's products before row
           // tile 1's: the softmax of row tile 0 starts while row tile 1's
           // products are still in the MFMA pipe
@@ -477,7 +564,52 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
 #pragma unroll
             for (int j = 0; j < 4; j++) s[rs][i][j] = __builtin_amdgcn_exp2f(s[rs][i][j]);
         };
-        if constexpr (!kF32) {
+        if constexpr (kSplit) {
+          softmax(0);
+          softmax(1);
+          // ---- O^T += V^T . P^T as in the 16-bit path, each operand in three
+          // bf16 terms (P^T split here, V^T read from the three planes) ----
+#pragma unroll
+          for (int kk = 0; kk < 2; kk++) {
+            V8 ph[2], pm[2], pl[2];
+#pragma unroll
+            for (int rs = 0; rs < 2; rs++)
+#pragma unroll
+              for (int j = 0; j < 4; j++) {
+                put3(ph[rs], pm[rs], pl[rs], j, s[rs][2 * kk][j]);
+                put3(ph[rs], pm[rs], pl[rs], 4 + j, s[rs][2 * kk + 1][j]);
+              }
+            const char* r_lo = vt_lds + (kk * 32 + grp * 4 + (col >> 2)) * L::ROW + (col & 3) * 8;
+            const char* r_hi = r_lo + 16 * L::ROW;
+#pragma unroll
+            for (int d = 0; d < DT; d++) {
+              V8 v3[3];
+#pragma unroll
+              for (int pl_i = 0; pl_i < 3; pl_i++) {
+                const typename M::v4 lo = lds_read_tr16<bf16_t>(r_lo + pl_i * L::PLANE + d * 32);
+                const typename M::v4 hi = lds_read_tr16<bf16_t>(r_hi + pl_i * L::PLANE + d * 32);
+                v3[pl_i] = V8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+              }
+#pragma unroll
+              for (int rs = 0; rs < 2; rs++) {
+                acc[rs][d] = M::mma(v3[2], ph[rs], acc[rs][d]);
+                acc[rs][d] = M::mma(v3[1], pm[rs], acc[rs][d]);
+                acc[rs][d] = M::mma(v3[0], pl[rs], acc[rs][d]);
+                acc[rs][d] = M::mma(v3[1], ph[rs], acc[rs][d]);
+                acc[rs][d] = M::mma(v3[0], pm[rs], acc[rs][d]);
+                acc[rs][d] = M::mma(v3[0], ph[rs], acc[rs][d]);
+              }
+            }
+          }
+          // row sums of the fp32 p, per lane group as in the fp32 path
+#pragma unroll
+          for (int rs = 0; rs < 2; rs++) {
+            float ls = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) ls += (s[rs][i][0] + s[rs][i][1]) + (s[rs][i][2] + s[rs][i][3]);
+            lsum[rs][0] += ls;
+          }
+        } else if constexpr (!kF32) {
           // ---- O^T += V^T . P^T over the tile's 64 keys (2 k-steps of 32) ----
           // V^T operands for both row tiles, read once: lane (col, grp)
           // addresses key row kk*32 + 4*grp + col/4 (then +16) at dims
@@ -556,7 +688,7 @@ __device__ __forceinline__ void chunk_wg(const ChunkParams& p, ChunkSmem<KV, HD>
     rel0 += kStageKeys<KV, HD>;
     if (rel0 >= it.key_live) break;
     __syncthreads();  // the stage is no longer read
-    issue(rel0);
+    if constexpr (!kSplit) issue(rel0);
   }
 
   LE_TIM(2, LE_TIM_NOW());

@@ -2,8 +2,10 @@
 against the CPU oracle (oracle.c, restating ops.h:87-111) on identical inputs.
 
 Tolerances (|got - want| against the fp32 oracle, per element):
-  * fp32 K/V: 4e-6 (exact fp32 products, other summation orders; the largest
-    error seen is 1.3e-6; the north star allows 1e-3);
+  * fp32 K/V: 4e-6 (decode rows: exact fp32 products; chunk rows: exact
+    fp32 products at head_dim 128, three-term bf16 products at head_dim 64,
+    each within a few fp32 roundings of the exact product; other summation
+    orders; the largest error seen is 1.3e-6; the north star allows 1e-3);
   * bf16 K/V: twice the error of the host emulation of the kernels'
     roundings on the same case (tests/precision.py: q and the softmax
     weights rounded to bf16 for the MFMA; gpu_util.emulated_bar). The
@@ -176,7 +178,8 @@ def test_chunk_rows_small(gpu, kv_bf16):
 def test_mixed_step_config3(gpu, act, kv_bf16, flags):
     """Config 3: 32 decode rows (ctx U[256, 2048]) + 2 prefill chunks of 512
     at cached offsets 0 and 1024: 32 + 2 * 512 = 1056 ragged rows, with bf16
-    K/V (16-bit MFMA chunk tiles) and fp32 K/V (fp32 MFMA chunk tiles), with
+    K/V (16-bit MFMA chunk tiles) and fp32 K/V (three-term bf16 MFMA chunk
+    tiles), with
     write-through partials and with the XCD-local exchange."""
     rng = np.random.default_rng(3)
     dec_ctx = rng.integers(256, 2049, size=32)
