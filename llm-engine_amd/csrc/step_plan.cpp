@@ -141,7 +141,7 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
   const int bs = cfg.block_size;
   if (!fixed && cfg.partition_tokens <= 0) {
     // Size decode partitions so the step has about kTargetItems workgroups,
-    // about one per CU. Each workgroup pays a fixed chain of dependent memory
+    // two per CU. Each workgroup pays a fixed chain of dependent memory
     // round trips (block ids, then K/V; partial store, arrival counter, merge)
     // of several microseconds, so on MI355X a few long partitions stream
     // faster than many short ones (measured: 64 x 4096 rows, 2048-token
@@ -160,7 +160,24 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
     // (config 3: 22.7 us with the rule above, 22.4 us with 2048 tokens).
     bool chunk_rows = false;
     for (int i = 0; i < n_slices; i++) chunk_rows |= slices[i].len > 1;
-    if (chunk_rows) part = std::max<int64_t>(part, kMixedStepPartition);
+    if (chunk_rows) {
+      part = std::max<int64_t>(part, kMixedStepPartition);
+    } else {
+      // The rows' partitions are whole ceilings, so the rule above can
+      // overshoot: grow the partition until the step's workgroups fit one
+      // round at two per CU (TinyLlama-shaped decode steps, 64 rows, 4 kv
+      // heads: 136-144 items per kv head ran 20.6-21.5 us per launch, 120
+      // items 15-16 us).
+      const int max_parts = std::max(1, kMaxMergeEntries / std::max(1, cfg.q_heads / cfg.kv_heads));
+      auto items_at = [&](int64_t pt) {
+        const int64_t pb = (pt + bs - 1) / bs;
+        int64_t n = 0;
+        for (int i = 0; i < n_slices; i++)
+          if (slices[i].len == 1) n += std::min<int64_t>((slices[i].start / bs + 1 + pb - 1) / pb, max_parts);
+        return n;
+      };
+      while (part < kMaxAutoPartition && items_at(part) * cfg.kv_heads > kTargetItems) part += kPartitionQuantum;
+    }
     cfg.partition_tokens = static_cast<int32_t>(std::min<int64_t>(part, kMaxAutoPartition));
   }
   if (cfg.chunk_q_tile <= 0) cfg.chunk_q_tile = kDefaultChunkTile;
@@ -173,7 +190,7 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
   const int dec_pb = round_to_blocks(cfg.partition_tokens, bs);
   const int chk_pb = round_to_blocks(cfg.chunk_partition_tokens, bs);
   const bool mfma_chunks = true;  // chunk rows on MFMA tiles, every cache type
-  const int max_decode_parts = std::max(1, kMaxMergeEntries / (cfg.q_heads / cfg.kv_heads));
+  const int max_decode_parts = std::max(1, kMaxMergeEntries / std::max(1, cfg.q_heads / cfg.kv_heads));
 
   // ---- sizes, and validation of every slice against its table ----
   int64_t n_tok = 0, n_table = 0;

@@ -433,3 +433,34 @@ def test_plan_fuzz_accepts_exactly_the_valid_steps(bs):
 def kernels_plan(slices, bs):
     from llm_engine_amd import kernels
     return kernels.Plan(slices, 14, 2, 64, bs, torch.bfloat16, device="cpu", pin=False)
+
+
+def test_auto_partition_fits_one_round_at_two_per_cu():
+    """The automatic decode partition (partition_tokens 0): at least 640 keys
+    and a multiple of 128, grown until the step's workgroups (items x kv
+    heads, placement padding aside) fit 512, two per CU, unless it reaches
+    4096; and never grown past the first size that fits."""
+    from llm_engine_amd import kernels
+    from llm_engine_amd.kernels import Slice
+    rng = np.random.default_rng(11)
+    for trial in range(40):
+        qh, kvh = [(14, 2), (32, 4), (32, 8), (16, 16)][trial % 4]
+        n = int(rng.integers(1, 200))
+        lens = rng.integers(1, int(rng.choice([600, 1400, 5000, 20000])), size=n)
+        blocks = [np.arange((l + 15) // 16, dtype=np.int32) for l in lens]
+        sl = [Slice(i, int(l) - 1, 1, True, blocks[i], np.zeros(int(l), np.int32)) for i, l in enumerate(lens)]
+        plan = kernels.Plan(sl, qh, kvh, 64, 16, torch.bfloat16, device="cpu", pin=False)
+        part = plan.plan.cfg.partition_tokens
+        assert part >= 640 and part % 128 == 0 and part <= 4096
+
+        def items(pt):
+            pb = (pt + 15) // 16
+            return sum(min(-(-((int(l) - 1) // 16 + 1) // pb), max(1, 1024 // (qh // kvh))) for l in lens)
+        assert plan.plan.n_decode_items == items(part)
+        if part < 4096:
+            assert items(part) * kvh <= 512
+        if part > 640 and items(part - 128) * kvh <= 512:
+            # grown only past sizes that did not fit: the first rule's size
+            ctx = int(lens.sum())
+            first = max(640, -(-(-(-ctx // max(1, 512 // kvh))) // 128) * 128)
+            assert part == min(first, 4096)
