@@ -12,22 +12,40 @@ namespace {
 constexpr int kMfmaWaves = 4;  // 8 waves measured slower (17.9 against 17.2 us)
 constexpr int kMfmaThreads = kMfmaWaves * 64;
 
-// Two waves per SIMD (two workgroups per CU): without the bound the compiler
-// took 234 VGPRs plus 24 AGPRs as spill slots, one wave per SIMD, and a
-// TinyLlama-shaped decode step (64 rows of 128-1280 keys, 4 kv heads, 416
-// workgroups) ran in two rounds: 19.8 against 15.7 us per launch. The 64 x
-// 4096 point gives back 0.2 us (27.6 against 27.4).
+// Two instantiations of one workgroup body, by the registers they may use:
+// * mfma_kernel: two waves per SIMD (two workgroups per CU, at most 256
+//   registers a lane; 232 VGPRs, no spill). Launches of fewer than 512
+//   workgroups run in one round. A TinyLlama-shaped decode step (64 rows of
+//   128-1280 keys, 4 kv heads, 416 workgroups): 15.7 us per launch, against
+//   19.8 in two rounds at one wave per SIMD.
+// * mfma_kernel_wide: no bound (234 VGPRs plus 24 AGPRs as spill slots, one
+//   wave per SIMD). For launches of two full rounds or more, where the
+//   rounds are even: the 64 x 4096 point (512 workgroups) 27.4 against 27.6
+//   us at two per CU.
 template <typename ACT, typename KV, int HD>
 __global__ __launch_bounds__(kMfmaThreads) __attribute__((amdgpu_waves_per_eu(2))) void mfma_kernel(DecodeParams p) {
   __shared__ dec::DecodeSmem<KV, HD, kMfmaWaves> sm;
   dec::decode_wg<ACT, KV, HD, kMfmaWaves>(p, sm, blockIdx.x, blockIdx.y, blockIdx.z);
 }
+template <typename ACT, typename KV, int HD>
+__global__ __launch_bounds__(kMfmaThreads) void mfma_kernel_wide(DecodeParams p) {
+  __shared__ dec::DecodeSmem<KV, HD, kMfmaWaves> sm;
+  dec::decode_wg<ACT, KV, HD, kMfmaWaves>(p, sm, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
+constexpr int64_t kWideFrom = 512;  // workgroups: two full rounds of one per CU
 
 template <typename ACT, typename KV>
 hipError_t launch(const DecodeParams& p, hipStream_t s) {
   const dim3 grid(p.n_rows, p.kv_heads, p.items ? 1 : p.nsplit);
-  if (p.head_dim == 64) mfma_kernel<ACT, KV, 64><<<grid, kMfmaThreads, 0, s>>>(p);
-  else mfma_kernel<ACT, KV, 128><<<grid, kMfmaThreads, 0, s>>>(p);
+  const bool wide = static_cast<int64_t>(grid.x) * grid.y * grid.z >= kWideFrom;
+  if (p.head_dim == 64) {
+    if (wide) mfma_kernel_wide<ACT, KV, 64><<<grid, kMfmaThreads, 0, s>>>(p);
+    else mfma_kernel<ACT, KV, 64><<<grid, kMfmaThreads, 0, s>>>(p);
+  } else {
+    if (wide) mfma_kernel_wide<ACT, KV, 128><<<grid, kMfmaThreads, 0, s>>>(p);
+    else mfma_kernel<ACT, KV, 128><<<grid, kMfmaThreads, 0, s>>>(p);
+  }
   return hipGetLastError();
 }
 

@@ -67,6 +67,21 @@ def tol_for(case, qh, want=None):
 
 
 @pytest.mark.parametrize("kv_bf16", [False, True])
+def test_decode_target_shape_two_rounds(gpu, kv_bf16):
+    """The 64 x 4096 target point at full size: 256 items x 2 kv heads =
+    512 workgroups, the launch size that takes the unbounded-register decode
+    kernel (two rounds of one workgroup per CU); below it the two-per-CU
+    kernel runs (every other decode test)."""
+    case = make_case([4096] * 64, num_blocks=32768, seed=7, kv_bf16=kv_bf16)
+    got, qh, plan = run_ragged(case, torch.float32, gpu)
+    assert plan.plan.n_decode_items * case.kv_heads >= 512
+    want = oracle_out(case, qh)
+    err = max_abs(got, want)
+    print(f"target kv_bf16={kv_bf16}: items {plan.plan.n_decode_items} max|err|={err:.3e}")
+    assert within(got, want, tol_for(case, qh))
+
+
+@pytest.mark.parametrize("kv_bf16", [False, True])
 @pytest.mark.parametrize("act", [torch.float32, torch.bfloat16])
 def test_decode_config2_shape(gpu, kv_bf16, act):
     """Config 2 at full size: 64 seqs, ctx log-uniform in [64, 4096], tables
