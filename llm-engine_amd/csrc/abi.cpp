@@ -226,6 +226,9 @@ int ragged_attention(const void* q, le_dtype act_dtype, const void* k_new, const
   d.q_heads = cfg.q_heads; d.kv_heads = cfg.kv_heads; d.head_dim = cfg.head_dim;
   d.block_size = cfg.block_size; d.scale_log2 = scale_log2; d.num_cache_blocks = num_cache_blocks;
   d.l2_local = plan->xcd_local && plan->n_parts > 0 && le::xcd_placement_holds(stream);
+  // fixed-layout plans hold empty slots, so their item count says nothing
+  // about the rounds
+  d.wide = cfg.table_capacity == 0 && static_cast<int64_t>(plan->n_decode_items) * cfg.kv_heads >= 512;
   const int64_t num_slots = num_cache_blocks * cfg.block_size;
   hipError_t e = hipSuccess;
   if (k_new) {

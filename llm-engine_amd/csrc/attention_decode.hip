@@ -19,9 +19,9 @@ constexpr int kMfmaThreads = kMfmaWaves * 64;
 //   128-1280 keys, 4 kv heads, 416 workgroups): 15.7 us per launch, against
 //   19.8 in two rounds at one wave per SIMD.
 // * mfma_kernel_wide: no bound (234 VGPRs plus 24 AGPRs as spill slots, one
-//   wave per SIMD). For launches of two full rounds or more, where the
-//   rounds are even: the 64 x 4096 point (512 workgroups) 27.4 against 27.6
-//   us at two per CU.
+//   wave per SIMD). For plans of 512 workgroups or more, two rounds of one
+//   per CU (not fixed-layout plans, whose empty slots inflate the count):
+//   the 64 x 4096 point (512 workgroups) 27.4 against 27.6 us at two per CU.
 template <typename ACT, typename KV, int HD>
 __global__ __launch_bounds__(kMfmaThreads) __attribute__((amdgpu_waves_per_eu(2))) void mfma_kernel(DecodeParams p) {
   __shared__ dec::DecodeSmem<KV, HD, kMfmaWaves> sm;
@@ -33,12 +33,10 @@ __global__ __launch_bounds__(kMfmaThreads) void mfma_kernel_wide(DecodeParams p)
   dec::decode_wg<ACT, KV, HD, kMfmaWaves>(p, sm, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
-constexpr int64_t kWideFrom = 512;  // workgroups: two full rounds of one per CU
-
 template <typename ACT, typename KV>
 hipError_t launch(const DecodeParams& p, hipStream_t s) {
   const dim3 grid(p.n_rows, p.kv_heads, p.items ? 1 : p.nsplit);
-  const bool wide = static_cast<int64_t>(grid.x) * grid.y * grid.z >= kWideFrom;
+  const bool wide = p.wide != 0;
   if (p.head_dim == 64) {
     if (wide) mfma_kernel_wide<ACT, KV, 64><<<grid, kMfmaThreads, 0, s>>>(p);
     else mfma_kernel<ACT, KV, 64><<<grid, kMfmaThreads, 0, s>>>(p);

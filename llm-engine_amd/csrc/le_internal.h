@@ -98,6 +98,10 @@ struct DecodeParams {
   // xcd_placement_holds), so partials go through that XCD's L2 with plain
   // stores.
   int l2_local;
+  // Two even rounds of one workgroup per CU or more (a plan of at least 512
+  // workgroups with no empty fixed-layout slots): the decode kernel
+  // instantiation with no register bound. Otherwise two workgroups per CU.
+  int wide;
 };
 
 // True when this device deals a launch's workgroups to its XCDs round robin
