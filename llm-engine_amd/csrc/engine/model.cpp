@@ -33,8 +33,17 @@
 namespace le::engine {
 namespace {
 
-// Decode partition of graph-replayed steps (fixed, so the layout is too).
-constexpr int kGraphPartition = 1024;
+// Graph-replayed steps use the fixed layout, where every row owns the same
+// number of partition slots whatever its length, and empty slots still cost
+// a workgroup. The partition is chosen per row count so that rows x slots x
+// kv heads is about one workgroup per CU (a TinyLlama-shaped step, 64 rows of
+// 128-1280 keys, 4 kv heads: one slot per row 17.3 us per launch, two 19.8;
+// the Qwen2.5-0.5B shape, 2 kv heads: two slots 13.8 us, one 15.6).
+constexpr int kGraphWorkgroups = 256;
+int graph_partition(int rows, int kv_heads, int cap_blocks, int bs) {
+  const int slots = std::max(1, kGraphWorkgroups / std::max(1, rows * kv_heads));
+  return ((cap_blocks + slots - 1) / slots) * bs;
+}
 
 }  // namespace
 
@@ -366,7 +375,8 @@ bool Model::forward_graph(const le_step_slice* slices, int n_slices, int32_t* to
     if (slices[i].len != 1 || !slices[i].needs_logits) return false;
   const auto t_plan = std::chrono::steady_clock::now();
   const int cap_blocks = (d_.max_pos + bs_ - 1) / bs_;
-  le_plan_config cfg{nh_, nkv_, hd_, bs_, kv_dt_, kGraphPartition, 0, 0, plan_flags_, cap_blocks};
+  le_plan_config cfg{nh_, nkv_, hd_, bs_, kv_dt_, graph_partition(n_slices, nkv_, cap_blocks, bs_), 0, 0,
+                     plan_flags_, cap_blocks};
   le_step_plan plan{};
   int st = le_plan_step(slices, n_slices, &cfg, nullptr, 0, &plan);
   if (st != LE_ENOSPACE) {  // e.g. a table longer than max_pos allows: run eagerly
