@@ -39,9 +39,13 @@ namespace {
 // kv heads is about one workgroup per CU (a TinyLlama-shaped step, 64 rows of
 // 128-1280 keys, 4 kv heads: one slot per row 17.3 us per launch, two 19.8;
 // the Qwen2.5-0.5B shape, 2 kv heads: two slots 13.8 us, one 15.6).
+// A slot never spans more than kGraphMaxPartition keys, so a long row is
+// still split when the model's maximum context is long.
 constexpr int kGraphWorkgroups = 256;
+constexpr int kGraphMaxPartition = 4096;
 int graph_partition(int rows, int kv_heads, int cap_blocks, int bs) {
-  const int slots = std::max(1, kGraphWorkgroups / std::max(1, rows * kv_heads));
+  const int max_pb = std::max(1, kGraphMaxPartition / bs);
+  const int slots = std::max({1, kGraphWorkgroups / std::max(1, rows * kv_heads), (cap_blocks + max_pb - 1) / max_pb});
   return ((cap_blocks + slots - 1) / slots) * bs;
 }
 
