@@ -10,7 +10,10 @@ copy), then per layer the new K/V rows are scattered into that layer's paged
 cache and ragged paged attention runs over the batch -- one launch per layer
 (le_ragged_paged_attention_store; --separate-scatter runs le_kv_cache_write
 then the attention). Each layer has its own KV pool, so a step touches 24
-distinct caches (>> the 256 MB Infinity Cache).
+distinct caches (>> the 256 MB Infinity Cache). The step is captured once as
+a HIP graph and replayed (the engine replays its decode steps the same way);
+--eager-step launches it from Python instead (about 5 % slower on config 2,
+the host's launch cost).
 
 Workloads (Qwen2.5-0.5B GQA: 14 q heads, 2 kv heads, head_dim 64, block 16):
   config2  64 seqs, context log-uniform in [64, 4096], tables from a
@@ -245,9 +248,13 @@ def kv_arena(nbytes: int, dev):
 
 
 def attention_leg(workload, kv, L, steps, warmup, partition=0, chunk_partition=0, graph=False,
-                  separate_scatter=False, flags=0):
+                  separate_scatter=False, flags=0, step_graph=True):
     """The hot path over one workload for L layers per step (see the module
-    docstring); returns the fields of the JSON line for it."""
+    docstring); returns the fields of the JSON line for it. The step is
+    replayed from a captured HIP graph (step_graph, as the engine replays its
+    decode steps; eagerly launched otherwise), and the attention-only loop
+    behind `roofline` is launched eagerly unless `graph`, which replays it
+    from a graph as well."""
     import torch
     from llm_engine_amd import kernels
     from gpu_util import slices_of
@@ -290,7 +297,7 @@ def attention_leg(workload, kv, L, steps, warmup, partition=0, chunk_partition=0
     slots = plan.dev_array("slots")
     ws = kernels.new_workspace(plan.workspace_size(), dev)
     stream = torch.cuda.current_stream()
-    if graph:
+    if graph or step_graph:
         stream = torch.cuda.Stream()  # capture needs a stream other than the legacy default
         stream.wait_stream(torch.cuda.current_stream())
 
@@ -309,7 +316,7 @@ def attention_leg(workload, kv, L, steps, warmup, partition=0, chunk_partition=0
                                                workspace=ws, stream=stream, k_new=knew[l], v_new=vnew[l])
 
     step = eager_step
-    if graph:
+    if graph or step_graph:
         # The whole step (upload + L x (scatter, attention)) as one HIP graph,
         # replayed per step. Nothing in it allocates or clears memory: the
         # workspace counters reset themselves.
@@ -547,7 +554,10 @@ def main():
     ap.add_argument("--workload", choices=["config2", "target", "config3"], default="config2")
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--graph", action="store_true", help="replay the step as one captured HIP graph")
+    ap.add_argument("--graph", action="store_true",
+                    help="replay the attention-only loop behind `roofline` from a captured HIP graph too")
+    ap.add_argument("--eager-step", action="store_true",
+                    help="launch the step's kernels eagerly instead of replaying it from a captured HIP graph")
     ap.add_argument("--separate-scatter", action="store_true",
                     help="scatter with le_kv_cache_write, then attend (instead of the fused entry point)")
     ap.add_argument("--e2e", choices=["decode64", "config4", "config5", "default", "all", "none"], default="default",
@@ -629,12 +639,14 @@ def main():
                for w, k in [(args.workload, args.kv)] + [(e[1], e[2]) for e in extras])
     kv_arena(need, torch.device("cuda:0"))
     res = attention_leg(args.workload, args.kv, args.layers, args.steps, args.warmup, args.partition,
-                        args.chunk_partition, args.graph, args.separate_scatter, args.flags)
+                        args.chunk_partition, args.graph, args.separate_scatter, args.flags,
+                        step_graph=not args.eager_step)
     if args.phases:
         res["phases"] = phase_summary(res["plan"].get("chunk_items", 0) > 0)
     if extras:
         for key, extra, kv in extras:
-            sub = attention_leg(extra, kv, args.layers, max(10, args.steps // 2), args.warmup, flags=args.flags)
+            sub = attention_leg(extra, kv, args.layers, max(10, args.steps // 2), args.warmup, flags=args.flags,
+                                step_graph=not args.eager_step)
             res[key] = {k: sub[k] for k in ("value", "unit", "ms_per_step", "pct_of_peak", "config", "plan",
                                              "roofline")}
     ctx, q_len, _ = workload_shape(args.workload)
