@@ -161,7 +161,9 @@ class Model {
   void* upload(const float* host, size_t n, bool as_bf16) { return upload_parts({{host, n}}, as_bf16); }
   void* upload_parts(const std::vector<std::pair<const float*, size_t>>& parts, bool as_bf16);
   float* upload_f32(const float* host, size_t n) { return static_cast<float*>(upload(host, n, false)); }
-  void gemm(const void* A, const void* B, void* C, int m, int n, int k, bool c_f32 = false);
+  // C = A . B^T (accumulate: C += A . B^T, bf16 models only)
+  void gemm(const void* A, const void* B, void* C, int m, int n, int k, bool c_f32 = false,
+            bool accumulate = false);
   // The device work of a step on stream_, from the plan upload to the token
   // read-back into the pinned tokens buffer (nothing synchronises).
   void enqueue_step(le_step_plan& plan, const void* host_plan, float* logits_out);
@@ -177,6 +179,11 @@ class Model {
 
   le_model_desc d_;
   bool bf16_;
+  // bf16 models: the post-attention RMSNorm folded around the gate|up
+  // projection (its weight in the projection's columns, the residual add in
+  // the O projection's epilogue, the row scale in rms_silu_mul): one launch
+  // fewer per layer. fp32 models keep the reference's order of operations.
+  bool fused_post_norm_ = false;
   int kv_dt_;  // le_dtype of the caches
   double plan_seconds_ = 0.0;
   int H_, QD_, KVD_, I_, V_, hd_, nh_, nkv_, bs_, num_blocks_;
@@ -228,6 +235,7 @@ Model::Model(const le_model_desc& d, int num_blocks, int block_size) : d_(d) {
   bs_ = block_size;
   num_blocks_ = num_blocks;
   act_ = bf16_ ? 2 : 4;
+  fused_post_norm_ = bf16_ && rms_silu_mul_fits(H_, I_);
   if (nh_ % nkv_ != 0 || hd_ % 2 != 0) throw std::invalid_argument("head layout");
   for (DevBuf* b : {&x_, &h_, &qkv_, &q_, &attn_, &o_, &gate_up_, &act_buf_, &logits_, &tokens_, &plan_dev_, &ws_}) {
     b->gen = &gen_;
@@ -254,7 +262,20 @@ Model::Model(const le_model_desc& d, int num_blocks, int block_size) : d_(d) {
           {{d.bq[l], static_cast<size_t>(QD_)}, {d.bk[l], static_cast<size_t>(KVD_)},
            {d.bv[l], static_cast<size_t>(KVD_)}}, false));
     const size_t hi = static_cast<size_t>(I_) * H_;
-    L.wgate_up = upload_parts({{d.wgate[l], hi}, {d.wup[l], hi}}, bf16_);
+    if (fused_post_norm_) {
+      // gate|up columns times the post-attention norm weight, in fp32, then
+      // rounded to bf16 once
+      if (!d.wgate[l] || !d.wup[l] || !d.post_norm[l]) throw std::invalid_argument("missing weight");
+      std::vector<float> g(hi), u(hi);
+      for (size_t j = 0; j < static_cast<size_t>(I_); j++)
+        for (size_t k = 0; k < static_cast<size_t>(H_); k++) {
+          g[j * H_ + k] = d.wgate[l][j * H_ + k] * d.post_norm[l][k];
+          u[j * H_ + k] = d.wup[l][j * H_ + k] * d.post_norm[l][k];
+        }
+      L.wgate_up = upload_parts({{g.data(), hi}, {u.data(), hi}}, true);
+    } else {
+      L.wgate_up = upload_parts({{d.wgate[l], hi}, {d.wup[l], hi}}, bf16_);
+    }
     L.wdown = upload(d.wdown[l], static_cast<size_t>(H_) * I_, bf16_);
   }
   // RoPE tables as the reference builds them: angles in double, stored as
@@ -331,9 +352,10 @@ void* Model::upload_parts(const std::vector<std::pair<const float*, size_t>>& pa
 
 // C[m][n] = A[m][k] * B[n][k]^T in row-major terms. rocBLAS is column-major,
 // so it computes C^T = B * A^T: B with op T first, A with op N second.
-void Model::gemm(const void* A, const void* B, void* C, int m, int n, int k, bool c_f32) {
+void Model::gemm(const void* A, const void* B, void* C, int m, int n, int k, bool c_f32, bool accumulate) {
   const float one = 1.f, zero = 0.f;
   if (!bf16_) {
+    if (accumulate) throw std::logic_error("accumulating GEMM on the fp32 model");
     blas_ok(rocblas_sgemm(blas_, rocblas_operation_transpose, rocblas_operation_none, n, m, k, &one,
                           static_cast<const float*>(B), k, static_cast<const float*>(A), k, &zero,
                           static_cast<float*>(C), n),
@@ -342,7 +364,8 @@ void Model::gemm(const void* A, const void* B, void* C, int m, int n, int k, boo
   }
   const rocblas_datatype ct = c_f32 ? rocblas_datatype_f32_r : rocblas_datatype_bf16_r;
   blas_ok(rocblas_gemm_ex(blas_, rocblas_operation_transpose, rocblas_operation_none, n, m, k, &one,
-                          B, rocblas_datatype_bf16_r, k, A, rocblas_datatype_bf16_r, k, &zero, C, ct, n,
+                          B, rocblas_datatype_bf16_r, k, A, rocblas_datatype_bf16_r, k, accumulate ? &one : &zero,
+                          C, ct, n,
                           C, ct, n, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0),
           "rocblas_gemm_ex");
 }
@@ -528,10 +551,16 @@ void Model::enqueue_step(le_step_plan& plan, const void* host_plan, float* logit
                                 num_blocks_, ws, ws_bytes, stream_),
             "le_attention_decode");
     }
-    gemm(attn, L.wo, o, N, H_, QD_);
-    hip_ok(residual_rmsnorm(x, o, nullptr, L.post_norm, h, N, H_, d_.eps, true, bf16_, stream_), "residual");
-    gemm(h, L.wgate_up, gate_up, N, 2 * I_, H_);
-    hip_ok(silu_mul_split(gate_up, act, N, I_, bf16_, stream_), "silu_mul");
+    if (fused_post_norm_) {
+      gemm(attn, L.wo, x, N, H_, QD_, false, /*accumulate=*/true);  // x += o
+      gemm(x, L.wgate_up, gate_up, N, 2 * I_, H_);
+      hip_ok(rms_silu_mul(x, gate_up, act, N, H_, I_, d_.eps, stream_), "rms_silu_mul");
+    } else {
+      gemm(attn, L.wo, o, N, H_, QD_);
+      hip_ok(residual_rmsnorm(x, o, nullptr, L.post_norm, h, N, H_, d_.eps, true, bf16_, stream_), "residual");
+      gemm(h, L.wgate_up, gate_up, N, 2 * I_, H_);
+      hip_ok(silu_mul_split(gate_up, act, N, I_, bf16_, stream_), "silu_mul");
+    }
     gemm(act, L.wdown, o, N, H_, I_);
     if (l + 1 < L_n)
       hip_ok(residual_rmsnorm(x, o, nullptr, layers_[l + 1].in_norm, h, N, H_, d_.eps, true, bf16_, stream_),

@@ -180,6 +180,63 @@ __global__ void silu_mul_split_vec_kernel(const T* __restrict__ gu, T* __restric
   vec16<T>::store(act + t * inter + j, o);
 }
 
+// The post-attention RMSNorm of the bf16 model folded around its gate|up
+// projection: the norm weight w is folded into the projection's input
+// columns (gate|up = x . (W diag w)^T, rounded to bf16 once at load), so the
+// projection reads the residual stream x itself, and the row's scale
+// r = 1/sqrt(mean(x^2) + eps) is applied here to both halves before the SiLU
+// product: act[t][j] = silu(g r) * (u r). The residual add before it runs in
+// the O projection's epilogue (beta = 1). One workgroup per row; the row of
+// x and the thread's pieces of g and u are requested together, so the row
+// costs one memory round trip. Rows of at most 4 x 256 x 8 elements.
+constexpr int kFusedPieces = 4;
+__global__ __launch_bounds__(256) void rms_silu_mul_kernel(const bf16_t* __restrict__ x,
+                                                          const bf16_t* __restrict__ gu,
+                                                          bf16_t* __restrict__ act, int hidden, int inter,
+                                                          float eps) {
+  constexpr int V = 8;
+  const int64_t t = blockIdx.x;
+  const bf16_t* xr = x + t * hidden;
+  const bf16_t* g_row = gu + t * 2 * inter;
+  bf16_t* out = act + t * inter;
+  const int hp = hidden / V, ip = inter / V;
+  float xv[kFusedPieces][V], g[kFusedPieces][V], u[kFusedPieces][V];
+#pragma unroll
+  for (int i = 0; i < kFusedPieces; i++) {
+    const int pc = threadIdx.x + i * 256;
+    if (pc < hp) vec16<bf16_t>::load(xr + pc * V, xv[i]);
+    if (pc < ip) {
+      vec16<bf16_t>::load(g_row + pc * V, g[i]);
+      vec16<bf16_t>::load(g_row + inter + pc * V, u[i]);
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kFusedPieces; i++)
+    if (threadIdx.x + i * 256 < hp)
+#pragma unroll
+      for (int e = 0; e < V; e++) ss += xv[i][e] * xv[i][e];
+  __shared__ float part[4];
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  const float tot = (part[0] + part[1]) + (part[2] + part[3]);
+  const float r = 1.0f / sqrtf(tot / hidden + eps);
+#pragma unroll
+  for (int i = 0; i < kFusedPieces; i++) {
+    const int pc = threadIdx.x + i * 256;
+    if (pc < ip) {
+      float o[V];
+#pragma unroll
+      for (int e = 0; e < V; e++) {
+        const float gv = g[i][e] * r;
+        o[e] = gv / (1.0f + expf(-gv)) * (u[i][e] * r);
+      }
+      vec16<bf16_t>::store(out + pc * V, o);
+    }
+  }
+}
+
 // act[t][j] = silu(gu[t][j]) * gu[t][inter + j]: the SiLU-gated product over
 // the fused gate|up projection output (ops.h:69-74, elementwise.cu).
 template <typename T>
@@ -280,6 +337,22 @@ hipError_t residual_rmsnorm(void* x, const void* y, const int32_t* rows, const f
   LE_DISPATCH(bf16, residual_rmsnorm_kernel<T><<<n_out, 256, 0, s>>>(
                         static_cast<T*>(x), static_cast<const T*>(y), rows, w, static_cast<T*>(out), cols,
                         eps, write_x ? 1 : 0));
+  return hipGetLastError();
+}
+
+bool rms_silu_mul_fits(int hidden, int inter) {
+  return hidden % 8 == 0 && inter % 8 == 0 && hidden <= kFusedPieces * 256 * 8 && inter <= kFusedPieces * 256 * 8;
+}
+
+hipError_t rms_silu_mul(const void* x, const void* gate_up, void* act, int rows, int hidden, int inter, float eps,
+                        hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  if (!rms_silu_mul_fits(hidden, inter) ||
+      ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gate_up) | reinterpret_cast<uintptr_t>(act)) &
+       15) != 0)
+    return hipErrorInvalidValue;
+  rms_silu_mul_kernel<<<rows, 256, 0, s>>>(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(gate_up),
+                                           static_cast<bf16_t*>(act), hidden, inter, eps);
   return hipGetLastError();
 }
 
