@@ -534,3 +534,28 @@ def test_unused_cache_rows_never_read(gpu, kv):
             a, _ = run_decode(case, torch.float32, gpu)
             assert np.isfinite(a).all()
             assert within(a, want, tol_for(case, qh))
+
+
+def test_fp32_chunk_rows_wide_range(gpu):
+    """fp32 chunk tiles at head_dim 64 hold each operand as three bf16 terms
+    (hi + mid + lo). With keys scaled up (sharp softmax rows, large scores)
+    and values spread over six decades, the error against the fp32 oracle,
+    relative to the largest |V|, stays at the fp32-rounding level, as with
+    the exact fp32 MFMA tile of head_dim 128 on the same data."""
+    errs = {}
+    for hd in (64, 128):
+        case = make_case([1024, 1536] + [700] * 4, q_len=[64, 96] + [1] * 4, num_blocks=512, seed=17,
+                         head_dim=hd)
+        rng = np.random.default_rng(5)
+        case.k_cache *= np.float32(6.0)
+        case.v_cache *= (10.0 ** rng.uniform(-3, 3, size=case.v_cache.shape)).astype(np.float32)
+        got, qh, plan = run_ragged(case, torch.float32, gpu)
+        assert plan.plan.n_chunk_items > 0
+        want = oracle_out(case, qh)
+        vmax = float(np.max(np.abs(case.v_cache)))
+        errs[hd] = max_abs(got, want) / vmax
+        print(f"fp32 chunk rows hd={hd}: max|err|/max|V| = {errs[hd]:.3e} (max|V| {vmax:.3g})")
+    # measured: 1.7e-6 (three-term, head_dim 64) and 2.5e-6 (exact fp32 MFMA,
+    # head_dim 128); the accumulation over up to 1536 keys sets both
+    assert errs[64] < 5e-6
+    assert errs[64] <= 2 * errs[128]
