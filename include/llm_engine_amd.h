@@ -298,6 +298,23 @@ int le_ragged_paged_attention_qkv(const void* qkv, le_dtype act_dtype, int64_t q
                                   void* out, void* q_scratch, void* workspace, size_t workspace_bytes,
                                   hipStream_t stream);
 
+/* le_ragged_paged_attention_qkv with the layer's pre-attention RMSNorm folded
+ * into the QKV projection. No counterpart in the reference, whose norm is a
+ * launch of its own before the projection (cuda_model.cu:353); for engines
+ * that multiply the norm weight into the projection's input columns and
+ * project the un-normalised residual stream x. Each row's q, k and v are
+ * first multiplied by r = 1/sqrt(mean_j x[t][j]^2 + eps) (fp32, the sum of
+ * squares per 16-byte piece and then across a wave), then biased and rounded
+ * to act_dtype once, then rotated: the same for the in-launch decode path and
+ * the separate rope/store path, so the two stay bit for bit equal. x:
+ * [n_tokens][hidden] in act_dtype, 16-byte aligned, hidden a multiple of 8. */
+int le_ragged_paged_attention_qkv_rms(const void* qkv, le_dtype act_dtype, int64_t qkv_row_stride,
+                                      const float* bias, const void* x, int hidden, float eps,
+                                      const float* cos_table, const float* sin_table, int max_positions,
+                                      void* k_cache, void* v_cache, le_dtype kv_dtype, int64_t num_cache_blocks,
+                                      const le_step_plan* plan, float scale, void* out, void* q_scratch,
+                                      void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* ------------------------------------------------------------------------
  * The layer ops between the GEMMs and attention, for any element type.
  * The reference launches them one by one (cuda_kernels.h:17-40, called at

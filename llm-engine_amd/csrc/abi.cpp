@@ -182,6 +182,9 @@ struct RopeRows {
   const float* cos_t;
   const float* sin_t;
   int max_pos;
+  const void* rms_x;  // the folded pre-attention RMSNorm's residual stream, or null
+  int rms_hidden;
+  float rms_eps;
 };
 
 // Ragged attention over a packed step; with k_new, the step's new K/V rows are
@@ -246,6 +249,7 @@ int ragged_attention(const void* q, le_dtype act_dtype, const void* k_new, const
       if (rope) {
         d.rope_row_stride = rope->row_stride; d.rope_bias = rope->bias;
         d.rope_cos = rope->cos_t; d.rope_sin = rope->sin_t; d.rope_max_pos = rope->max_pos;
+        d.rms_x = rope->rms_x; d.rms_hidden = rope->rms_hidden; d.rms_eps = rope->rms_eps;
       }
     }
   }
@@ -301,12 +305,12 @@ int le_ragged_paged_attention_store(const void* q, le_dtype act_dtype, const voi
 }
 
 
-int le_ragged_paged_attention_qkv(const void* qkv, le_dtype act_dtype, int64_t qkv_row_stride,
+static int attention_qkv(const void* qkv, le_dtype act_dtype, int64_t qkv_row_stride,
                                   const float* bias, const float* cos_table, const float* sin_table,
                                   int max_positions, void* k_cache, void* v_cache, le_dtype kv_dtype,
                                   int64_t num_cache_blocks, const le_step_plan* plan, float scale,
                                   void* out, void* q_scratch, void* workspace, size_t workspace_bytes,
-                                  hipStream_t stream) {
+                                  hipStream_t stream, const void* rms_x, int rms_hidden, float rms_eps) {
   if (!plan || !valid_dtype(act_dtype) || !valid_dtype(kv_dtype) || max_positions <= 0)
     return LE_EINVAL;
   if (plan->n_tokens == 0) return LE_OK;
@@ -324,7 +328,7 @@ int le_ragged_paged_attention_qkv(const void* qkv, le_dtype act_dtype, int64_t q
   const void* v_new = row0 + (static_cast<int64_t>(qd) + kvd) * esz;
   if (plan->n_tokens == plan->n_seqs && plan->n_chunk_items == 0 && plan->n_decode_items > 0) {
     // decode rows only: bias, RoPE and the store inside the attention launch
-    RopeRows r{qkv_row_stride, bias, cos_table, sin_table, max_positions};
+    RopeRows r{qkv_row_stride, bias, cos_table, sin_table, max_positions, rms_x, rms_hidden, rms_eps};
     return ragged_attention(qkv, act_dtype, k_new, v_new, act_dtype, k_cache, v_cache, kv_dtype,
                             num_cache_blocks, plan, scale, out, workspace, workspace_bytes, stream, &r);
   }
@@ -335,10 +339,35 @@ int le_ragged_paged_attention_qkv(const void* qkv, le_dtype act_dtype, int64_t q
   const hipError_t e = le::rope_kv_cache_write(
       qkv, act_dtype, qkv_row_stride, bias, positions, slots, cos_table, sin_table, max_positions, plan->n_tokens,
       cfg.q_heads, cfg.kv_heads, cfg.head_dim, q_scratch, k_cache, v_cache, kv_dtype,
-      num_cache_blocks * cfg.block_size, stream);
+      num_cache_blocks * cfg.block_size, stream, rms_x, rms_hidden, rms_eps);
   if (e != hipSuccess) return hip_status(e);
   return ragged_attention(q_scratch, act_dtype, nullptr, nullptr, LE_F32, k_cache, v_cache, kv_dtype,
                           num_cache_blocks, plan, scale, out, workspace, workspace_bytes, stream, nullptr);
+}
+
+
+int le_ragged_paged_attention_qkv(const void* qkv, le_dtype act_dtype, int64_t qkv_row_stride,
+                                  const float* bias, const float* cos_table, const float* sin_table,
+                                  int max_positions, void* k_cache, void* v_cache, le_dtype kv_dtype,
+                                  int64_t num_cache_blocks, const le_step_plan* plan, float scale,
+                                  void* out, void* q_scratch, void* workspace, size_t workspace_bytes,
+                                  hipStream_t stream) {
+  return attention_qkv(qkv, act_dtype, qkv_row_stride, bias, cos_table, sin_table, max_positions, k_cache, v_cache,
+                       kv_dtype, num_cache_blocks, plan, scale, out, q_scratch, workspace, workspace_bytes, stream,
+                       nullptr, 0, 0.f);
+}
+
+int le_ragged_paged_attention_qkv_rms(const void* qkv, le_dtype act_dtype, int64_t qkv_row_stride,
+                                      const float* bias, const void* x, int hidden, float eps,
+                                      const float* cos_table, const float* sin_table, int max_positions,
+                                      void* k_cache, void* v_cache, le_dtype kv_dtype, int64_t num_cache_blocks,
+                                      const le_step_plan* plan, float scale, void* out, void* q_scratch,
+                                      void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (!x || hidden <= 0 || !(eps >= 0.f) || !std::isfinite(eps)) return LE_EINVAL;
+  if (hidden % 8 != 0 || (reinterpret_cast<uintptr_t>(x) & 15) != 0) return LE_EUNSUPPORTED;  // 16-byte pieces
+  return attention_qkv(qkv, act_dtype, qkv_row_stride, bias, cos_table, sin_table, max_positions, k_cache, v_cache,
+                       kv_dtype, num_cache_blocks, plan, scale, out, q_scratch, workspace, workspace_bytes, stream, x,
+                       hidden, eps);
 }
 
 }  // extern "C"

@@ -84,9 +84,12 @@ __device__ __forceinline__ Work resolve(const DecodeParams& p, int bx, int bz) {
 // type; a*c - b*s and b*c + a*s without contraction), so q and k are
 // bit-identical to that kernel's. d0 is a multiple of 8 and half of head_dim
 // a multiple of 8, so the eight dims sit on one side of the rotation.
+// scaled: the row is the projection of the un-normalised residual stream
+// (the RMSNorm folded into the projection), so each element is first
+// multiplied by the row's scale rs, then biased, and rounded once.
 template <typename ACT>
 __device__ __forceinline__ void rope8(const ACT* head, const float* hb, int d0, int half, const float* cs,
-                                      const float* sn, float* o) {
+                                      const float* sn, float* o, bool scaled = false, float rs = 1.f) {
 #pragma clang fp contract(off)
   const bool lo = d0 < half;
   const int dp = lo ? d0 + half : d0 - half;  // the partner dims
@@ -95,7 +98,13 @@ __device__ __forceinline__ void rope8(const ACT* head, const float* hb, int d0, 
   elem<ACT>::load8(head + dp, oth);
   elem<float>::load8(cs + (lo ? d0 : dp), c);
   elem<float>::load8(sn + (lo ? d0 : dp), s);
-  if (hb) {
+  if (scaled) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      own[e] = elem<ACT>::round(hb ? own[e] * rs + hb[d0 + e] : own[e] * rs);
+      oth[e] = elem<ACT>::round(hb ? oth[e] * rs + hb[dp + e] : oth[e] * rs);
+    }
+  } else if (hb) {
 #pragma unroll
     for (int e = 0; e < 8; e++) {
       own[e] = elem<ACT>::round(own[e] + hb[d0 + e]);
@@ -122,9 +131,11 @@ template <typename ACT> struct QRope {
   const float* cs;
   const float* sn;
   int half;
+  bool scaled;
+  float rs;
   // rounded to the activation type, as the separately rotated q is stored
   __device__ __forceinline__ void piece8(int d0, float* o) const {
-    rope8<ACT>(head, hb, d0, half, cs, sn, o);
+    rope8<ACT>(head, hb, d0, half, cs, sn, o, scaled, rs);
 #pragma unroll
     for (int e = 0; e < 8; e++) o[e] = elem<ACT>::round(o[e]);
   }
@@ -143,7 +154,7 @@ __device__ __forceinline__ bool stores_new_row(const DecodeParams& p, const Work
   return p.k_new != nullptr && (w.part < 0 || w.part == w.part_begin + w.n_parts - 1);
 }
 template <typename C>
-__device__ __forceinline__ void store_new_row(const DecodeParams& p, const Work& w, int kvh, int hd) {
+__device__ __forceinline__ void store_new_row(const DecodeParams& p, const Work& w, int kvh, int hd, float rs) {
   if (!stores_new_row(p, w)) return;
   const int pieces = hd / 8;
   const int t = threadIdx.x;
@@ -165,13 +176,18 @@ __device__ __forceinline__ void store_new_row(const DecodeParams& p, const Work&
       const int64_t tab = static_cast<int64_t>(w.pos) * half;
       const S* h = static_cast<const S*>(src_rows) + static_cast<int64_t>(w.token) * p.rope_row_stride + kvh * hd;
       const float* hb = p.rope_bias ? p.rope_bias + (p.q_heads + which * p.kv_heads + kvh) * hd : nullptr;
+      const bool scaled = p.rms_x != nullptr;
       if (!which) {
-        rope8<S>(h, hb, c * 8, half, p.rope_cos + tab, p.rope_sin + tab, v);
+        rope8<S>(h, hb, c * 8, half, p.rope_cos + tab, p.rope_sin + tab, v, scaled, rs);
       } else {
         elem<S>::load8(h + c * 8, v);
-        if (hb)
+        if (scaled) {
+#pragma unroll
+          for (int e = 0; e < 8; e++) v[e] = elem<S>::round(hb ? v[e] * rs + hb[c * 8 + e] : v[e] * rs);
+        } else if (hb) {
 #pragma unroll
           for (int e = 0; e < 8; e++) v[e] = elem<S>::round(v[e] + hb[c * 8 + e]);
+        }
       }
     } else {
       elem<S>::load8(static_cast<const S*>(src_rows) + src, v);
@@ -795,7 +811,12 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
   const KV* kc = T::lane_base(p.k_cache, kvh, grp);
   const KV* vc = T::lane_base(p.v_cache, kvh, grp);
   char* vt = lds + wave * T::VT_BYTES;
-  store_new_row<KV>(p, w, kvh, HD);
+  // the folded pre-attention RMSNorm: the row's scale, per wave
+  const float rs = p.rms_x && p.rope_max_pos > 0
+                       ? row_rms_scale(static_cast<const ACT*>(p.rms_x) + static_cast<int64_t>(w.token) * p.rms_hidden,
+                                       p.rms_hidden, p.rms_eps)
+                       : 1.f;
+  store_new_row<KV>(p, w, kvh, HD, rs);
 
   // Q^T (B operand): column `col` = head kvh*G + col.
   typename T::QOp qb;
@@ -806,7 +827,8 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
       const bool pos_ok = w.pos >= 0 && w.pos < p.rope_max_pos;  // else q = 0, as rope_kv_write_kernel
       const int64_t tab = static_cast<int64_t>(pos_ok ? w.pos : 0) * (HD / 2);
       const QRope<ACT> src{static_cast<const ACT*>(p.q) + static_cast<int64_t>(w.token) * p.rope_row_stride + h * HD,
-                           p.rope_bias ? p.rope_bias + h * HD : nullptr, p.rope_cos + tab, p.rope_sin + tab, HD / 2};
+                           p.rope_bias ? p.rope_bias + h * HD : nullptr, p.rope_cos + tab, p.rope_sin + tab, HD / 2,
+                           p.rms_x != nullptr, rs};
       T::load_q(qb, src, ok && pos_ok, grp);
     } else {
       const QRow<ACT> src{static_cast<const ACT*>(p.q) + (static_cast<int64_t>(w.token) * p.q_heads + h) * HD};

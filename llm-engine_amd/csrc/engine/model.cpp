@@ -184,6 +184,11 @@ class Model {
   // the O projection's epilogue, the row scale in rms_silu_mul): one launch
   // fewer per layer. fp32 models keep the reference's order of operations.
   bool fused_post_norm_ = false;
+  // bf16 models with the ragged attention: the pre-attention RMSNorm folded
+  // into the QKV projection as well (its weight in the projection's columns,
+  // the row scale applied by le_ragged_paged_attention_qkv_rms, the residual
+  // add in the down projection's epilogue): no norm launch inside a layer.
+  bool fused_pre_norm_ = false;
   int kv_dt_;  // le_dtype of the caches
   double plan_seconds_ = 0.0;
   int H_, QD_, KVD_, I_, V_, hd_, nh_, nkv_, bs_, num_blocks_;
@@ -236,6 +241,7 @@ Model::Model(const le_model_desc& d, int num_blocks, int block_size) : d_(d) {
   num_blocks_ = num_blocks;
   act_ = bf16_ ? 2 : 4;
   fused_post_norm_ = bf16_ && rms_silu_mul_fits(H_, I_);
+  fused_pre_norm_ = fused_post_norm_ && d.attention == LE_ATTN_RAGGED && H_ % 8 == 0;
   if (nh_ % nkv_ != 0 || hd_ % 2 != 0) throw std::invalid_argument("head layout");
   for (DevBuf* b : {&x_, &h_, &qkv_, &q_, &attn_, &o_, &gate_up_, &act_buf_, &logits_, &tokens_, &plan_dev_, &ws_}) {
     b->gen = &gen_;
@@ -255,7 +261,21 @@ Model::Model(const le_model_desc& d, int num_blocks, int block_size) : d_(d) {
     L.in_norm = upload_f32(d.in_norm[l], H_);
     L.post_norm = upload_f32(d.post_norm[l], H_);
     const size_t hq = static_cast<size_t>(QD_) * H_, hkv = static_cast<size_t>(KVD_) * H_;
-    L.wqkv = upload_parts({{d.wq[l], hq}, {d.wk[l], hkv}, {d.wv[l], hkv}}, bf16_);
+    if (fused_pre_norm_) {
+      // q, k, v columns times the pre-attention norm weight, in fp32, then
+      // rounded to bf16 once
+      if (!d.wq[l] || !d.wk[l] || !d.wv[l] || !d.in_norm[l]) throw std::invalid_argument("missing weight");
+      auto fold = [&](const float* w, size_t rows) {
+        std::vector<float> f(rows * H_);
+        for (size_t j = 0; j < rows; j++)
+          for (size_t k = 0; k < static_cast<size_t>(H_); k++) f[j * H_ + k] = w[j * H_ + k] * d.in_norm[l][k];
+        return f;
+      };
+      const std::vector<float> fq = fold(d.wq[l], QD_), fk = fold(d.wk[l], KVD_), fv = fold(d.wv[l], KVD_);
+      L.wqkv = upload_parts({{fq.data(), hq}, {fk.data(), hkv}, {fv.data(), hkv}}, true);
+    } else {
+      L.wqkv = upload_parts({{d.wq[l], hq}, {d.wk[l], hkv}, {d.wv[l], hkv}}, bf16_);
+    }
     L.wo = upload(d.wo[l], static_cast<size_t>(H_) * QD_, bf16_);
     if (d.bq && d.bq[l])
       L.bqkv = static_cast<float*>(upload_parts(
@@ -524,16 +544,22 @@ void Model::enqueue_step(le_step_plan& plan, const void* host_plan, float* logit
   // attention with bias+RoPE+cache-write (inside its launch on a decode
   // step), O GEMM, residual+norm, one gate|up GEMM, SiLU product, down GEMM.
   hip_ok(gather_rows(embed_, d_ids, x, N, H_, bf16_, stream_), "embedding");
-  hip_ok(residual_rmsnorm(x, nullptr, nullptr, layers_[0].in_norm, h, N, H_, d_.eps, false, bf16_, stream_),
-         "rmsnorm");
+  if (!fused_pre_norm_)
+    hip_ok(residual_rmsnorm(x, nullptr, nullptr, layers_[0].in_norm, h, N, H_, d_.eps, false, bf16_, stream_),
+           "rmsnorm");
   for (int l = 0; l < L_n; l++) {
     const Layer& L = layers_[l];
-    gemm(h, L.wqkv, qkv, N, QKV, H_);
+    gemm(fused_pre_norm_ ? x : h, L.wqkv, qkv, N, QKV, H_);
     // Bias, RoPE, the K/V store and attention from the QKV rows: one launch
     // on a decode step; otherwise every token's K/V is rotated and written
     // before attention runs, so tokens of one step (a prefill chunk) attend
     // to each other.
-    if (!ref_attn) {
+    if (fused_pre_norm_) {
+      le_ok(le_ragged_paged_attention_qkv_rms(qkv, act_dt, QKV, L.bqkv, x, H_, d_.eps, cos_, sin_, d_.max_pos,
+                                              kc_[l], vc_[l], kv_dt, num_blocks_, &plan, scale, attn, q, ws,
+                                              ws_bytes, stream_),
+            "le_ragged_paged_attention_qkv_rms");
+    } else if (!ref_attn) {
       le_ok(le_ragged_paged_attention_qkv(qkv, act_dt, QKV, L.bqkv, cos_, sin_, d_.max_pos, kc_[l], vc_[l],
                                           kv_dt, num_blocks_, &plan, scale, attn, q, ws, ws_bytes, stream_),
             "le_ragged_paged_attention_qkv");
@@ -561,14 +587,20 @@ void Model::enqueue_step(le_step_plan& plan, const void* host_plan, float* logit
       gemm(h, L.wgate_up, gate_up, N, 2 * I_, H_);
       hip_ok(silu_mul_split(gate_up, act, N, I_, bf16_, stream_), "silu_mul");
     }
-    gemm(act, L.wdown, o, N, H_, I_);
-    if (l + 1 < L_n)
-      hip_ok(residual_rmsnorm(x, o, nullptr, layers_[l + 1].in_norm, h, N, H_, d_.eps, true, bf16_, stream_),
-             "residual");
+    if (fused_pre_norm_) {
+      gemm(act, L.wdown, x, N, H_, I_, false, /*accumulate=*/true);  // x += down; the next norm is folded
+    } else {
+      gemm(act, L.wdown, o, N, H_, I_);
+      if (l + 1 < L_n)
+        hip_ok(residual_rmsnorm(x, o, nullptr, layers_[l + 1].in_norm, h, N, H_, d_.eps, true, bf16_, stream_),
+               "residual");
+    }
   }
   if (R > 0) {
-    // The last residual add and the final norm, on the logit rows only.
-    hip_ok(residual_rmsnorm(x, o, d_rows, final_norm_, h, R, H_, d_.eps, false, bf16_, stream_),
+    // The last residual add (already in x when the norms are folded) and the
+    // final norm, on the logit rows only.
+    hip_ok(residual_rmsnorm(x, fused_pre_norm_ ? nullptr : o, d_rows, final_norm_, h, R, H_, d_.eps, false, bf16_,
+                            stream_),
            "final norm");
     float* logits = static_cast<float*>(logits_.get(static_cast<size_t>(R) * V_ * 4));
     gemm(h, lm_head_, logits, R, V_, H_, /*c_f32=*/true);

@@ -233,6 +233,31 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
+// 1/sqrt(mean(x^2) + eps) of one row of the residual stream (the folded
+// pre-attention RMSNorm), formed by one wave alone: each lane sums the
+// squares of its 16-byte pieces, then the wave reduces (no LDS, no barrier).
+// Every wave that calls it on a row gets the same value (the decode kernel
+// and rope_kv_write_kernel both use it).
+template <typename ACT>
+__device__ __forceinline__ float row_rms_scale(const ACT* x, int hidden, float eps) {
+  constexpr int V = 16 / static_cast<int>(sizeof(ACT));
+  const int lane = threadIdx.x & (kWave - 1);
+  float ss = 0.f;
+  for (int pc = lane; pc * V < hidden; pc += kWave) {
+    float v[8];
+    if constexpr (V == 8) {
+      elem<ACT>::load8(x + pc * V, v);
+    } else {
+      elem<ACT>::load4(x + pc * V, v);
+    }
+#pragma unroll
+    for (int e = 0; e < V; e++) ss += v[e] * v[e];
+  }
+  ss = wave_sum(ss);
+  return 1.0f / sqrtf(ss / hidden + eps);
+}
+
+
 // Device-coherent 16-byte accesses for data exchanged between workgroups
 // (possibly on different XCDs, whose L2s are not coherent with each other):
 // raw buffer loads/stores with the sc1 cache-policy bit, the same policy the

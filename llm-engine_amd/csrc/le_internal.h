@@ -51,7 +51,8 @@ hipError_t rope_kv_cache_write(const void* qkv, int act_dtype, int64_t row_strid
                                const int32_t* positions, const int32_t* slots, const float* cos_t,
                                const float* sin_t, int max_pos, int n_tokens, int q_heads,
                                int kv_heads, int head_dim, void* q_out, void* kc, void* vc,
-                               int cache_dtype, int64_t num_slots, hipStream_t stream);
+                               int cache_dtype, int64_t num_slots, hipStream_t stream,
+                               const void* rms_x = nullptr, int rms_hidden = 0, float rms_eps = 0.f);
 
 struct DecodeParams {
   const void* q;
@@ -85,6 +86,13 @@ struct DecodeParams {
   const float* rope_cos;
   const float* rope_sin;
   int rope_max_pos;
+  // With rope rows: the pre-attention RMSNorm folded into the QKV projection.
+  // rms_x (act dtype, [tokens][rms_hidden]) is the residual stream the rows
+  // were projected from; each row is scaled by 1/sqrt(mean(x^2) + rms_eps)
+  // before its bias. Null: the rows are already normalised.
+  const void* rms_x;
+  int rms_hidden;
+  float rms_eps;
   const DecodeItem* items;  // null: one item per (token, split) with `nsplit` splits
   const int32_t* item_ids;  // with items: block ids of item i at item_ids[i * ids_stride + j]
   int ids_stride;

@@ -28,8 +28,12 @@ __global__ __launch_bounds__(256) void rope_kv_write_kernel(
     const T* __restrict__ qkv, int64_t stride, const float* __restrict__ bias,
     const int32_t* __restrict__ positions, const int32_t* __restrict__ slots,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t, int max_pos, int nh, int nkv,
-    int hd, T* __restrict__ q_out, C* __restrict__ kc, C* __restrict__ vc, int64_t num_slots) {
+    int hd, T* __restrict__ q_out, C* __restrict__ kc, C* __restrict__ vc, int64_t num_slots,
+    const T* __restrict__ rms_x, int rms_hidden, float rms_eps) {
   const int t = blockIdx.x;
+  // the folded pre-attention RMSNorm: every wave forms the row's scale
+  const bool scaled = rms_x != nullptr;
+  const float rs = scaled ? row_rms_scale(rms_x + static_cast<int64_t>(t) * rms_hidden, rms_hidden, rms_eps) : 1.f;
   const int pos = positions[t];
   const bool pos_ok = pos >= 0 && pos < max_pos;
   const int64_t slot = slots[t];
@@ -48,7 +52,13 @@ __global__ __launch_bounds__(256) void rope_kv_write_kernel(
       float a[4], b[4];
       elem<T>::load4(row + off, a);
       elem<T>::load4(row + off + half, b);
-      if (bias) {
+      if (scaled) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          a[e] = elem<T>::round(bias ? a[e] * rs + bias[off + e] : a[e] * rs);
+          b[e] = elem<T>::round(bias ? b[e] * rs + bias[off + half + e] : b[e] * rs);
+        }
+      } else if (bias) {
 #pragma unroll
         for (int e = 0; e < 4; e++) {
           a[e] = elem<T>::round(a[e] + bias[off + e]);
@@ -78,7 +88,10 @@ __global__ __launch_bounds__(256) void rope_kv_write_kernel(
       float x[8];
       elem<T>::load4(row + qd + kvd + j, x);
       elem<T>::load4(row + qd + kvd + j + 4, x + 4);
-      if (bias) {
+      if (scaled) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) x[e] = elem<T>::round(bias ? x[e] * rs + bias[qd + kvd + j + e] : x[e] * rs);
+      } else if (bias) {
 #pragma unroll
         for (int e = 0; e < 8; e++) x[e] = elem<T>::round(x[e] + bias[qd + kvd + j + e]);
       }
@@ -93,10 +106,11 @@ template <typename T, typename C>
 hipError_t launch(const void* qkv, int64_t stride, const float* bias, const int32_t* positions,
                   const int32_t* slots, const float* cos_t, const float* sin_t, int max_pos, int n,
                   int nh, int nkv, int hd, void* q_out, void* kc, void* vc, int64_t num_slots,
-                  hipStream_t stream) {
+                  const void* rms_x, int rms_hidden, float rms_eps, hipStream_t stream) {
   rope_kv_write_kernel<T, C><<<dim3(static_cast<unsigned>(n)), 256, 0, stream>>>(
       static_cast<const T*>(qkv), stride, bias, positions, slots, cos_t, sin_t, max_pos, nh, nkv, hd,
-      static_cast<T*>(q_out), static_cast<C*>(kc), static_cast<C*>(vc), num_slots);
+      static_cast<T*>(q_out), static_cast<C*>(kc), static_cast<C*>(vc), num_slots, static_cast<const T*>(rms_x),
+      rms_hidden, rms_eps);
   return hipGetLastError();
 }
 
@@ -106,12 +120,13 @@ hipError_t rope_kv_cache_write(const void* qkv, int act_dtype, int64_t row_strid
                                const int32_t* positions, const int32_t* slots, const float* cos_t,
                                const float* sin_t, int max_pos, int n_tokens, int q_heads,
                                int kv_heads, int head_dim, void* q_out, void* kc, void* vc,
-                               int cache_dtype, int64_t num_slots, hipStream_t stream) {
+                               int cache_dtype, int64_t num_slots, hipStream_t stream, const void* rms_x,
+                               int rms_hidden, float rms_eps) {
   return with_dtype(act_dtype, [&](auto a) {
     return with_dtype(cache_dtype, [&](auto c) {
       return launch<decltype(a), decltype(c)>(qkv, row_stride, bias, positions, slots, cos_t, sin_t, max_pos,
                                               n_tokens, q_heads, kv_heads, head_dim, q_out, kc, vc, num_slots,
-                                              stream);
+                                              rms_x, rms_hidden, rms_eps, stream);
     });
   });
 }

@@ -258,13 +258,17 @@ def ragged_paged_attention_qkv(qkv: torch.Tensor, bias: torch.Tensor | None, cos
                                sin_t: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                                plan: Plan, scale: float, out: torch.Tensor | None = None,
                                workspace: torch.Tensor | None = None, q_scratch: torch.Tensor | None = None,
-                               stream=None) -> torch.Tensor:
+                               stream=None, rms_x: torch.Tensor | None = None, rms_eps: float = 1e-6) -> torch.Tensor:
     """A layer's attention from its stacked QKV rows (cuda_model.cu:358-377:
     bias, RoPE, the K/V store and attention). Equals rope_kv_cache_write on the
     plan's positions and slots followed by ragged_paged_attention, bit for bit;
     on a decode-only step all of it runs in the attention launch
     (le_ragged_paged_attention_qkv). qkv: [N, >= (q_heads + 2*kv_heads)*head_dim]
-    laid out [q | k | v]; cos_t/sin_t: fp32 [max_pos, head_dim/2]."""
+    laid out [q | k | v]; cos_t/sin_t: fp32 [max_pos, head_dim/2]. With rms_x
+    ([N, hidden] in qkv's dtype, the residual stream the rows were projected
+    from through norm-weighted columns), the pre-attention RMSNorm is folded
+    in: each row is scaled by 1/sqrt(mean(x^2) + rms_eps) before its bias
+    (le_ragged_paged_attention_qkv_rms)."""
     P = plan.plan
     cfg = P.cfg
     n = P.n_tokens
@@ -288,6 +292,15 @@ def ragged_paged_attention_qkv(qkv: torch.Tensor, bias: torch.Tensor | None, cos
     need = plan.workspace_size()
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = torch.zeros(max(need, 1), dtype=torch.uint8, device=qkv.device)
+    if rms_x is not None:
+        _req(rms_x.dtype == qkv.dtype and rms_x.dim() == 2 and rms_x.shape[0] == n and rms_x.is_contiguous(),
+             "rms_x: [N, hidden] contiguous, qkv's dtype")
+        check("le_ragged_paged_attention_qkv_rms", _lib.load().le_ragged_paged_attention_qkv_rms(
+            _p(qkv), _dt(qkv), qkv.stride(0), None if bias is None else _p(bias), _p(rms_x), rms_x.shape[1],
+            float(rms_eps), _p(cos_t), _p(sin_t), cos_t.shape[0], _p(k_cache), _p(v_cache), _dt(k_cache),
+            num_blocks, ctypes.byref(P), float(scale), _p(out), _p(q_scratch), _p(workspace),
+            workspace.numel() * workspace.element_size(), _stream(stream)))
+        return out
     check("le_ragged_paged_attention_qkv", _lib.load().le_ragged_paged_attention_qkv(
         _p(qkv), _dt(qkv), qkv.stride(0), None if bias is None else _p(bias), _p(cos_t), _p(sin_t),
         cos_t.shape[0], _p(k_cache), _p(v_cache), _dt(k_cache), num_blocks, ctypes.byref(P), float(scale),

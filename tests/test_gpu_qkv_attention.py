@@ -90,3 +90,52 @@ def test_qkv_decode_against_oracle(gpu):
     err = max_abs(got.cpu().numpy(), oracle_out(case, q.cpu().numpy()))
     print(f"qkv attention vs oracle: max|err| {err:.3e}")
     assert err < 1e-3
+
+
+@pytest.mark.parametrize("act", ["f32", "bf16"])
+@pytest.mark.parametrize("mixed", [False, True])
+def test_qkv_rms_folded_norm(gpu, act, mixed):
+    """le_ragged_paged_attention_qkv_rms: the rows are the projection of the
+    un-normalised residual stream x, and each row is scaled by
+    r = 1/sqrt(mean(x^2) + eps) before its bias, on the in-launch decode path
+    and on the rope/store path of a mixed step. Against the plain entry point
+    on rows scaled by r on the host: with fp32 rows the two differ only by
+    r's last bit; with bf16 rows by the one rounding the folded path saves
+    (the host's scaled rows are rounded before the bias is added)."""
+    from llm_engine_amd import kernels
+    rng = np.random.default_rng(71 + mixed)
+    q_heads, kv_heads, head_dim, hidden, eps = 14, 2, 64, 896, 1e-6
+    ctx, q_len = ([600, 33, 1200, 5], [70, 1, 1, 5]) if mixed else ([1, 17, 300, 1500, 64, 2049], None)
+    case = make_case(ctx, q_len=q_len, q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim, seed=71,
+                     kv_bf16=True)
+    n = len(case.token_pos)
+    qd, kvd = q_heads * head_dim, kv_heads * head_dim
+    tdt = TORCH_DT[act]
+    x = torch.from_numpy(rng.standard_normal((n, hidden), dtype=np.float32) * 3).to(tdt)
+    xf = x.float().numpy().astype(np.float64)
+    r = (1.0 / np.sqrt((xf * xf).mean(axis=1) + eps)).astype(np.float32)
+    raw = torch.from_numpy(rng.standard_normal((n, qd + 2 * kvd), dtype=np.float32)).to(tdt)
+    b = torch.from_numpy(rng.standard_normal(qd + 2 * kvd, dtype=np.float32)).to(gpu)
+    cos_t, sin_t = (torch.from_numpy(t).to(gpu) for t in oracle.rope_tables(head_dim, 4096, 1e6))
+    kc0 = to_dev_cache(case.k_cache, gpu)
+    plan = kernels.Plan(slices_of(case), q_heads, kv_heads, head_dim, 16, kc0.dtype).upload()
+    kc1, vc1 = kc0.clone(), to_dev_cache(case.v_cache, gpu)
+    got = kernels.ragged_paged_attention_qkv(raw.to(gpu), b, cos_t, sin_t, kc1, vc1, plan, case.scale,
+                                             rms_x=x.to(gpu), rms_eps=eps)
+    kc2, vc2 = kc0.clone(), to_dev_cache(case.v_cache, gpu)
+    scaled = (raw.float() * torch.from_numpy(r)[:, None]).to(tdt).to(gpu)
+    want = kernels.ragged_paged_attention_qkv(scaled, b, cos_t, sin_t, kc2, vc2, plan, case.scale)
+    torch.cuda.synchronize()
+    fused = plan.plan.n_tokens == plan.plan.n_seqs and plan.plan.n_chunk_items == 0
+    assert fused != mixed
+    g, w = got.float().cpu().numpy(), want.float().cpu().numpy()
+    err = max_abs(g, w)
+    kerr = max_abs(kc1.float().cpu(), kc2.float().cpu())
+    verr = max_abs(vc1.float().cpu(), vc2.float().cpu())
+    print(f"qkv rms act={act} mixed={mixed}: max|out diff| {err:.2e}, cache diffs {kerr:.2e} {verr:.2e}")
+    # bf16 cache entries: one bf16 step of the largest written value at most
+    vmax = float(max(kc2.float().abs().max(), vc2.float().abs().max()))
+    assert kerr <= vmax * 2 ** -7 and verr <= vmax * 2 ** -7
+    assert err <= (2e-3 if act == "f32" else 3e-2)
+    # a row scale that is not applied would move outputs by far more
+    assert float(np.abs(r - 1).max()) > 0.3
