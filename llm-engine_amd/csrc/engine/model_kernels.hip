@@ -5,6 +5,8 @@
 // kernels in src/kernels/) for fp32 or bf16 activations; the math is fp32.
 #include <float.h>
 
+#include <algorithm>
+
 #include "../le_common.h"
 #include "model_kernels.h"
 
@@ -186,9 +188,12 @@ __global__ void silu_mul_split_vec_kernel(const T* __restrict__ gu, T* __restric
 // projection reads the residual stream x itself, and the row's scale
 // r = 1/sqrt(mean(x^2) + eps) is applied here to both halves before the SiLU
 // product: act[t][j] = silu(g r) * (u r). The residual add before it runs in
-// the O projection's epilogue (beta = 1). One workgroup per row; the row of
-// x and the thread's pieces of g and u are requested together, so the row
-// costs one memory round trip. Rows of at most 4 x 256 x 8 elements.
+// the O projection's epilogue (beta = 1). Workgroup (t, s) takes the s-th of
+// S contiguous ranges of row t's pieces of g and u (S = gridDim.y: a decode
+// step's few rows spread over more CUs) and forms r itself from the whole
+// row of x; x and its
+// pieces of g and u are requested together, so a workgroup costs one memory
+// round trip. Rows of at most 4 x 256 x 8 elements.
 constexpr int kFusedPieces = 4;
 __global__ __launch_bounds__(256) void rms_silu_mul_kernel(const bf16_t* __restrict__ x,
                                                           const bf16_t* __restrict__ gu,
@@ -200,12 +205,15 @@ __global__ __launch_bounds__(256) void rms_silu_mul_kernel(const bf16_t* __restr
   const bf16_t* g_row = gu + t * 2 * inter;
   bf16_t* out = act + t * inter;
   const int hp = hidden / V, ip = inter / V;
+  const int chunk = (ip + static_cast<int>(gridDim.y) - 1) / static_cast<int>(gridDim.y);
+  const int p0 = static_cast<int>(blockIdx.y) * chunk, p1 = min(ip, p0 + chunk);
   float xv[kFusedPieces][V], g[kFusedPieces][V], u[kFusedPieces][V];
 #pragma unroll
   for (int i = 0; i < kFusedPieces; i++) {
-    const int pc = threadIdx.x + i * 256;
-    if (pc < hp) vec16<bf16_t>::load(xr + pc * V, xv[i]);
-    if (pc < ip) {
+    const int px = threadIdx.x + i * 256;
+    if (px < hp) vec16<bf16_t>::load(xr + px * V, xv[i]);
+    const int pc = p0 + threadIdx.x + i * 256;
+    if (pc < p1) {
       vec16<bf16_t>::load(g_row + pc * V, g[i]);
       vec16<bf16_t>::load(g_row + inter + pc * V, u[i]);
     }
@@ -224,8 +232,8 @@ __global__ __launch_bounds__(256) void rms_silu_mul_kernel(const bf16_t* __restr
   const float r = 1.0f / sqrtf(tot / hidden + eps);
 #pragma unroll
   for (int i = 0; i < kFusedPieces; i++) {
-    const int pc = threadIdx.x + i * 256;
-    if (pc < ip) {
+    const int pc = p0 + threadIdx.x + i * 256;
+    if (pc < p1) {
       float o[V];
 #pragma unroll
       for (int e = 0; e < V; e++) {
@@ -351,8 +359,12 @@ hipError_t rms_silu_mul(const void* x, const void* gate_up, void* act, int rows,
       ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(gate_up) | reinterpret_cast<uintptr_t>(act)) &
        15) != 0)
     return hipErrorInvalidValue;
-  rms_silu_mul_kernel<<<rows, 256, 0, s>>>(static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(gate_up),
-                                           static_cast<bf16_t*>(act), hidden, inter, eps);
+  // pieces of a row per workgroup: a decode step's rows spread over about 256
+  // workgroups (each re-reads its row of x, a few KB)
+  const int S = std::max(1, std::min(8, 256 / rows));
+  rms_silu_mul_kernel<<<dim3(static_cast<unsigned>(rows), static_cast<unsigned>(S)), 256, 0, s>>>(
+      static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(gate_up), static_cast<bf16_t*>(act), hidden, inter,
+      eps);
   return hipGetLastError();
 }
 
