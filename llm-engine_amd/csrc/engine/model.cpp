@@ -395,10 +395,15 @@ void Model::forward(const le_step_slice* slices, int n_slices, int32_t* tokens_o
   const auto t_plan = std::chrono::steady_clock::now();
   le_plan_config cfg{nh_, nkv_, hd_, bs_, kv_dt_, 0, 0, 0, plan_flags_, 0};
   le_step_plan plan{};
-  int st = le_plan_step(slices, n_slices, &cfg, nullptr, 0, &plan);
-  if (st != LE_ENOSPACE) le_ok(st, "le_plan_step");
-  void* host = plan_host_.get(static_cast<size_t>(plan.bytes));
-  le_ok(le_plan_step(slices, n_slices, &cfg, host, plan.bytes, &plan), "le_plan_step");
+  // Packed straight into the pinned buffer when it is large enough (one
+  // call per step); sized first only when it must grow.
+  void* host = plan_host_.p;
+  int st = le_plan_step(slices, n_slices, &cfg, host, static_cast<int64_t>(plan_host_.cap), &plan);
+  if (st == LE_ENOSPACE) {
+    host = plan_host_.get(static_cast<size_t>(plan.bytes));
+    st = le_plan_step(slices, n_slices, &cfg, host, plan.bytes, &plan);
+  }
+  le_ok(st, "le_plan_step");
   plan_seconds_ += std::chrono::duration<double>(std::chrono::steady_clock::now() - t_plan).count();
   if (plan.n_tokens == 0) return;
   enqueue_step(plan, host, logits_out);
@@ -425,14 +430,17 @@ bool Model::forward_graph(const le_step_slice* slices, int n_slices, int32_t* to
   le_plan_config cfg{nh_, nkv_, hd_, bs_, kv_dt_, graph_partition(n_slices, nkv_, cap_blocks, bs_), 0, 0,
                      plan_flags_, cap_blocks};
   le_step_plan plan{};
-  int st = le_plan_step(slices, n_slices, &cfg, nullptr, 0, &plan);
-  if (st != LE_ENOSPACE) {  // e.g. a table longer than max_pos allows: run eagerly
+  void* host = plan_host_.p;
+  int st = le_plan_step(slices, n_slices, &cfg, host, static_cast<int64_t>(plan_host_.cap), &plan);
+  if (st == LE_ENOSPACE) {
+    host = plan_host_.get(static_cast<size_t>(plan.bytes));
+    st = le_plan_step(slices, n_slices, &cfg, host, plan.bytes, &plan);
+  }
+  if (st != LE_OK) {  // e.g. a table longer than max_pos allows: run eagerly
     eager_fallbacks_++;
     return false;
   }
   DecodeGraph& g = graphs_[n_slices];
-  void* host = plan_host_.get(static_cast<size_t>(plan.bytes));
-  le_ok(le_plan_step(slices, n_slices, &cfg, host, plan.bytes, &plan), "le_plan_step");
   plan_seconds_ += std::chrono::duration<double>(std::chrono::steady_clock::now() - t_plan).count();
   if (!g.warm || g.plan_bytes != plan.bytes) {  // first step of this layout: eager
     if (g.exec) (void)hipGraphExecDestroy(g.exec);
