@@ -68,6 +68,7 @@ template <typename Item, typename Same, typename Blocks>
 std::vector<Item> place_on_xcds(const std::vector<Item>& items, Same same_group, Blocks blocks, const Item& pad) {
   struct Group { size_t first, n; int64_t longest, work; };
   std::vector<Group> groups;
+  groups.reserve(items.size());
   for (size_t i = 0; i < items.size();) {
     size_t j = i;
     Group g{i, 0, 0, 0};
@@ -87,6 +88,7 @@ std::vector<Item> place_on_xcds(const std::vector<Item>& items, Same same_group,
     return a.longest != b.longest ? a.longest > b.longest : a.n > b.n;
   });
   std::vector<std::vector<Item>> bins(kXcds);
+  for (auto& b : bins) b.reserve(items.size() / kXcds + 8);
   int64_t load[kXcds] = {};
   for (const Group& g : groups) {
     int b = 0;
@@ -196,8 +198,10 @@ int le_plan_step(const le_step_slice* slices, int n_slices, const le_plan_config
   int64_t n_tok = 0, n_table = 0;
   int n_logits = 0, n_seqs = 0, max_pos = 0;
   std::unordered_map<int64_t, int> seq_index;
+  seq_index.reserve(static_cast<size_t>(n_slices));
   std::vector<int> slice_seq(static_cast<size_t>(n_slices));
   std::vector<int> seq_first_slice;
+  seq_first_slice.reserve(static_cast<size_t>(n_slices));
   for (int i = 0; i < n_slices; i++) {
     const le_step_slice& s = slices[i];
     if (s.len <= 0 || s.start < 0 || s.num_blocks < 0 || !s.tokens) return LE_EINVAL;
