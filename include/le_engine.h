@@ -92,6 +92,12 @@ typedef struct le_model_desc {
   const float* const* wgate;     /* [inter][hidden] */
   const float* const* wup;
   const float* const* wdown;     /* [hidden][inter] */
+  /* bf16 models fold both RMSNorms of a layer into the GEMMs around them
+   * (norm weights in the weight columns, residual adds in the O and down
+   * projections' epilogues, row scales in the SiLU kernel and the attention
+   * launch). Nonzero: keep the norm launches (the fp32 model's order of
+   * operations), e.g. to compare the two. */
+  int32_t unfused_norms;
 } le_model_desc;
 
 #define LE_ATTN_RAGGED 0

@@ -240,7 +240,7 @@ Model::Model(const le_model_desc& d, int num_blocks, int block_size) : d_(d) {
   bs_ = block_size;
   num_blocks_ = num_blocks;
   act_ = bf16_ ? 2 : 4;
-  fused_post_norm_ = bf16_ && rms_silu_mul_fits(H_, I_);
+  fused_post_norm_ = bf16_ && !d.unfused_norms && rms_silu_mul_fits(H_, I_);
   fused_pre_norm_ = fused_post_norm_ && d.attention == LE_ATTN_RAGGED && H_ % 8 == 0;
   if (nh_ % nkv_ != 0 || hd_ % 2 != 0) throw std::invalid_argument("head layout");
   for (DevBuf* b : {&x_, &h_, &qkv_, &q_, &attn_, &o_, &gate_up_, &act_buf_, &logits_, &tokens_, &plan_dev_, &ws_}) {

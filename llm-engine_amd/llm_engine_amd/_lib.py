@@ -113,7 +113,7 @@ class ModelDesc(ctypes.Structure):
         ("kv_dtype", ctypes.c_int32), ("attention", ctypes.c_int32),
         ("embed", ctypes.c_void_p), ("final_norm", ctypes.c_void_p), ("lm_head", ctypes.c_void_p),
     ] + [(n, _fpp) for n in ("in_norm", "post_norm", "wq", "wk", "wv", "wo", "bq", "bk", "bv",
-                              "wgate", "wup", "wdown")]
+                              "wgate", "wup", "wdown")] + [("unfused_norms", ctypes.c_int32)]
 
 
 class RunStats(ctypes.Structure):

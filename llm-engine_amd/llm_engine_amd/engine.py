@@ -78,11 +78,13 @@ class Model:
     DTYPES = {"f32": LE_F32, "bf16": LE_BF16, "f16": LE_F16}
 
     def __init__(self, w: Weights, num_blocks: int, block_size: int = 16, dtype: str = "f32",
-                 kv_dtype: str | None = None, attention: str = "ragged", decode_graph: bool = False):
+                 kv_dtype: str | None = None, attention: str = "ragged", decode_graph: bool = False,
+                 unfused_norms: bool = False):
         """attention: "ragged" (le_ragged_paged_attention_qkv over the packed
         step) or "reference" (the reference-shaped le_attention_decode).
         decode_graph: replay decode steps from captured HIP graphs
-        (le_model_set_decode_graph)."""
+        (le_model_set_decode_graph). unfused_norms: a bf16 model keeps its
+        RMSNorm launches instead of folding them into the GEMMs."""
         a = w.arch
         self.arch = a
         self.num_blocks, self.block_size = num_blocks, block_size
@@ -104,6 +106,7 @@ class Model:
                       None if w.lm_head is None else w.lm_head.ctypes.data)
         for k, v in self._keep.items():
             setattr(d, k, ctypes.cast(v, ctypes.POINTER(ctypes.c_void_p)) if v is not None else None)
+        d.unfused_norms = int(unfused_norms)
         st = ctypes.c_int(0)
         self._h = _lib.load().le_model_create(ctypes.byref(d), num_blocks, block_size, ctypes.byref(st))
         if not self._h:
