@@ -12,7 +12,8 @@ namespace {
 constexpr int kMfmaWaves = 4;  // 8 waves measured slower (17.9 against 17.2 us)
 constexpr int kMfmaThreads = kMfmaWaves * 64;
 
-// Two instantiations of one workgroup body, by the registers they may use:
+// Three instantiations of one workgroup body, by the registers they may use
+// and the rows they take:
 // * mfma_kernel: two waves per SIMD (two workgroups per CU, at most 256
 //   registers a lane; 232 VGPRs, no spill). Launches of fewer than 512
 //   workgroups run in one round. A TinyLlama-shaped decode step (64 rows of
@@ -22,10 +23,19 @@ constexpr int kMfmaThreads = kMfmaWaves * 64;
 //   wave per SIMD). For plans of 512 workgroups or more, two rounds of one
 //   per CU (not fixed-layout plans, whose empty slots inflate the count):
 //   the 64 x 4096 point (512 workgroups) 27.4 against 27.6 us at two per CU.
+// * mfma_kernel_fold: rows straight from the stacked QKV projection with the
+//   folded pre-attention norm (p.rms_x), at two per CU. The row scale's loads
+//   issued ahead of the q and K/V row loads that use it: a TinyLlama-shaped
+//   step 18.4 against 19.7 us with the scale formed before them.
 template <typename ACT, typename KV, int HD>
 __global__ __launch_bounds__(kMfmaThreads) __attribute__((amdgpu_waves_per_eu(2))) void mfma_kernel(DecodeParams p) {
   __shared__ dec::DecodeSmem<KV, HD, kMfmaWaves> sm;
   dec::decode_wg<ACT, KV, HD, kMfmaWaves>(p, sm, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+template <typename ACT, typename KV, int HD>
+__global__ __launch_bounds__(kMfmaThreads) __attribute__((amdgpu_waves_per_eu(2))) void mfma_kernel_fold(DecodeParams p) {
+  __shared__ dec::DecodeSmem<KV, HD, kMfmaWaves> sm;
+  dec::decode_wg<ACT, KV, HD, kMfmaWaves, true>(p, sm, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 template <typename ACT, typename KV, int HD>
 __global__ __launch_bounds__(kMfmaThreads) void mfma_kernel_wide(DecodeParams p) {
@@ -37,7 +47,10 @@ template <typename ACT, typename KV>
 hipError_t launch(const DecodeParams& p, hipStream_t s) {
   const dim3 grid(p.n_rows, p.kv_heads, p.items ? 1 : p.nsplit);
   const bool wide = p.wide != 0;
-  if (p.head_dim == 64) {
+  if (p.rms_x && p.rope_max_pos > 0) {
+    if (p.head_dim == 64) mfma_kernel_fold<ACT, KV, 64><<<grid, kMfmaThreads, 0, s>>>(p);
+    else mfma_kernel_fold<ACT, KV, 128><<<grid, kMfmaThreads, 0, s>>>(p);
+  } else if (p.head_dim == 64) {
     if (wide) mfma_kernel_wide<ACT, KV, 64><<<grid, kMfmaThreads, 0, s>>>(p);
     else mfma_kernel<ACT, KV, 64><<<grid, kMfmaThreads, 0, s>>>(p);
   } else {

@@ -77,6 +77,63 @@ __device__ __forceinline__ Work resolve(const DecodeParams& p, int bx, int bz) {
 }
 
 // ---- Rows straight from the stacked QKV projection ----
+// The folded pre-attention RMSNorm's row scale r = 1/sqrt(mean(x^2) + eps),
+// formed lazily (the decode kernel's folded-norm instantiation): issue() requests the wave's 16-byte pieces of the row of x
+// (up to kHeld per lane, held in registers), and get(), called by every lane
+// of the wave, reduces them the first time. The loads of the q, k and v rows
+// are issued between the two, so the reduction's wait covers only the x
+// loads, which are older (loads complete in order). Same per-lane order and
+// wave reduction as row_rms_scale, which rope_kv_write_kernel uses: the same
+// value. Rows longer than kHeld pieces per lane take row_rms_scale at get().
+template <typename ACT> struct RowScale {
+  static constexpr int V = 16 / static_cast<int>(sizeof(ACT));
+  static constexpr int kHeld = 8;
+  const ACT* x = nullptr;  // null: no folded norm, r = 1
+  int hidden = 0;
+  float eps = 0.f;
+  bool done = false;
+  float r = 1.f;
+  uint4 raw[kHeld];
+  __device__ __forceinline__ bool held() const { return hidden <= kHeld * kWave * V; }
+  __device__ __forceinline__ void issue() {
+    if (!x || !held()) return;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int last = hidden / V - 1;
+#pragma unroll
+    for (int i = 0; i < kHeld; i++)
+      if (i * kWave * V < hidden) raw[i] = ld16(x + min(lane + i * kWave, last) * V);
+  }
+  __device__ __forceinline__ float get() {
+    if (!x) return 1.f;
+    if (!done) {
+      if (held()) {
+        const int lane = threadIdx.x & (kWave - 1);
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < kHeld; i++) {
+          if (i * kWave * V >= hidden) break;
+          if ((lane + i * kWave) * V < hidden) {
+            float v[8];
+            if constexpr (V == 8) {
+              elem<ACT>::widen(raw[i], v);
+            } else {
+              elem<float>::widen(raw[i], v);
+            }
+#pragma unroll
+            for (int e = 0; e < V; e++) ss += v[e] * v[e];
+          }
+        }
+        ss = wave_sum(ss);
+        r = 1.0f / sqrtf(ss / hidden + eps);
+      } else {
+        r = row_rms_scale(x, hidden, eps);
+      }
+      done = true;
+    }
+    return r;
+  }
+};
+
 // Dims [d0, d0 + 8) of one head after bias and rotate_half RoPE (rope.cu:53,
 // ops.h:55-66): head is the head's first element in the row, hb its bias (or
 // null), cs/sn the position's cos/sin rows. The operations and their order
@@ -86,10 +143,12 @@ __device__ __forceinline__ Work resolve(const DecodeParams& p, int bx, int bz) {
 // a multiple of 8, so the eight dims sit on one side of the rotation.
 // scaled: the row is the projection of the un-normalised residual stream
 // (the RMSNorm folded into the projection), so each element is first
-// multiplied by the row's scale rs, then biased, and rounded once.
-template <typename ACT>
+// multiplied by the row's scale rs, then biased, and rounded once; kLazy:
+// the scale is sc->get(), read after this piece's loads are issued.
+template <typename ACT, bool kLazy = false, typename XS = ACT>
 __device__ __forceinline__ void rope8(const ACT* head, const float* hb, int d0, int half, const float* cs,
-                                      const float* sn, float* o, bool scaled = false, float rs = 1.f) {
+                                      const float* sn, float* o, bool scaled = false, float rs = 1.f,
+                                      RowScale<XS>* sc = nullptr) {
 #pragma clang fp contract(off)
   const bool lo = d0 < half;
   const int dp = lo ? d0 + half : d0 - half;  // the partner dims
@@ -98,6 +157,10 @@ __device__ __forceinline__ void rope8(const ACT* head, const float* hb, int d0, 
   elem<ACT>::load8(head + dp, oth);
   elem<float>::load8(cs + (lo ? d0 : dp), c);
   elem<float>::load8(sn + (lo ? d0 : dp), s);
+  if constexpr (kLazy) {
+    scaled = true;
+    rs = sc->get();
+  }
   if (scaled) {
 #pragma unroll
     for (int e = 0; e < 8; e++) {
@@ -125,7 +188,7 @@ template <typename ACT> struct QRow {
   const ACT* row;
   __device__ __forceinline__ void piece8(int d0, float* o) const { elem<ACT>::load8(row + d0, o); }
 };
-template <typename ACT> struct QRope {
+template <typename ACT, bool kLazy = false> struct QRope {
   const ACT* head;
   const float* hb;
   const float* cs;
@@ -133,9 +196,10 @@ template <typename ACT> struct QRope {
   int half;
   bool scaled;
   float rs;
+  RowScale<ACT>* sc;  // kLazy: the lazily formed row scale (rs and scaled unused)
   // rounded to the activation type, as the separately rotated q is stored
   __device__ __forceinline__ void piece8(int d0, float* o) const {
-    rope8<ACT>(head, hb, d0, half, cs, sn, o, scaled, rs);
+    rope8<ACT, kLazy>(head, hb, d0, half, cs, sn, o, scaled, rs, sc);
 #pragma unroll
     for (int e = 0; e < 8; e++) o[e] = elem<ACT>::round(o[e]);
   }
@@ -153,11 +217,57 @@ template <typename ACT> struct QRope {
 __device__ __forceinline__ bool stores_new_row(const DecodeParams& p, const Work& w) {
   return p.k_new != nullptr && (w.part < 0 || w.part == w.part_begin + w.n_parts - 1);
 }
-template <typename C>
-__device__ __forceinline__ void store_new_row(const DecodeParams& p, const Work& w, int kvh, int hd, float rs) {
+// kFold: the folded-norm instantiation (rows from the stacked QKV projection
+// with the row scale sc), the only one that reads sc.
+template <typename C, bool kFold = false, typename ACT = float>
+__device__ __forceinline__ void store_new_row(const DecodeParams& p, const Work& w, int kvh, int hd, float rs,
+                                              RowScale<ACT>* sc = nullptr) {
   if (!stores_new_row(p, w)) return;
   const int pieces = hd / 8;
   const int t = threadIdx.x;
+  if constexpr (kFold) {
+    // Folded pre-attention norm (rows from the stacked QKV projection, in the
+    // activation type): the whole of wave 0 loads (lanes past the 2 * pieces
+    // that store read piece 0 again), so the row scale's wave reduction runs
+    // with every lane after the row's loads are issued. Same operations as
+    // rope8 and the V branch below with the scale.
+    if (t >= kWave) return;
+    if (w.pos < 0 || w.pos >= p.rope_max_pos) return;  // as rope_kv_write_kernel
+    const int64_t slot = p.slots[w.token];
+    const bool on = t < 2 * pieces && slot >= 0 && slot < p.num_slots;
+    const int tt = t < 2 * pieces ? t : 0;
+    const int which = tt >= pieces;  // 0 = K, 1 = V
+    const int c = tt - which * pieces;
+    const int half = hd / 2, d0 = c * 8;
+    const bool lo = d0 < half;
+    const int dp = lo ? d0 + half : d0 - half;
+    const ACT* h = static_cast<const ACT*>(which ? p.v_new : p.k_new) +
+                   static_cast<int64_t>(w.token) * p.rope_row_stride + kvh * hd;
+    const float* hb = p.rope_bias ? p.rope_bias + (p.q_heads + which * p.kv_heads + kvh) * hd : nullptr;
+    const int64_t tab = static_cast<int64_t>(w.pos) * half;
+    float own[8], oth[8], cs[8], sn[8], v[8];
+    elem<ACT>::load8(h + d0, own);
+    elem<ACT>::load8(h + dp, oth);
+    elem<float>::load8(p.rope_cos + tab + (lo ? d0 : dp), cs);
+    elem<float>::load8(p.rope_sin + tab + (lo ? d0 : dp), sn);
+    const float rs = sc->get();
+    {
+#pragma clang fp contract(off)
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const float a = elem<ACT>::round(hb ? own[e] * rs + hb[d0 + e] : own[e] * rs);
+        const float b = elem<ACT>::round(hb ? oth[e] * rs + hb[dp + e] : oth[e] * rs);
+        const float x = a * cs[e];
+        const float y = b * sn[e];
+        v[e] = which ? a : (lo ? x - y : x + y);
+      }
+    }
+    if (on) {
+      const int64_t dst = (slot * p.kv_heads + kvh) * hd + c * 8;
+      elem<C>::store8(static_cast<C*>(const_cast<void*>(which ? p.v_cache : p.k_cache)) + dst, v);
+    }
+    return;
+  }
   if (t >= 2 * pieces) return;
   const int64_t slot = p.slots[w.token];
   if (slot < 0 || slot >= p.num_slots) return;
@@ -746,7 +856,11 @@ template <typename KV, int HD, int NW> struct DecodeSmem {
 // One decode workgroup of NW waves: item (or row) bx, kv head by, split bz
 // (the reference-shaped launch without a plan). Shared by the decode kernel
 // and the fused ragged kernel.
-template <typename ACT, typename KV, int HD, int NW>
+// kFold: rows straight from the stacked QKV projection with the folded
+// pre-attention norm (p.rms_x set, p.rope_max_pos > 0), the row scale formed
+// lazily behind the row loads; an instantiation of its own, so the code of
+// every other path is not shaped by it.
+template <typename ACT, typename KV, int HD, int NW, bool kFold = false>
 __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, HD, NW>& sm, int bx, int by, int bz) {
   using T = DecodeTile<KV, HD>;
   using L = MfmaLds<HD, T::VT_BYTES, NW>;
@@ -812,23 +926,31 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
   const KV* vc = T::lane_base(p.v_cache, kvh, grp);
   char* vt = lds + wave * T::VT_BYTES;
   // the folded pre-attention RMSNorm: the row's scale, per wave
-  const float rs = p.rms_x && p.rope_max_pos > 0
-                       ? row_rms_scale(static_cast<const ACT*>(p.rms_x) + static_cast<int64_t>(w.token) * p.rms_hidden,
-                                       p.rms_hidden, p.rms_eps)
-                       : 1.f;
-  store_new_row<KV>(p, w, kvh, HD, rs);
+  float rs = 1.f;
+  RowScale<ACT> xs;
+  if constexpr (kFold) {
+    xs.x = static_cast<const ACT*>(p.rms_x) + static_cast<int64_t>(w.token) * p.rms_hidden;
+    xs.hidden = p.rms_hidden;
+    xs.eps = p.rms_eps;
+    xs.issue();
+  } else if (p.rms_x && p.rope_max_pos > 0) {
+    rs = row_rms_scale(static_cast<const ACT*>(p.rms_x) + static_cast<int64_t>(w.token) * p.rms_hidden,
+                       p.rms_hidden, p.rms_eps);
+  }
+  store_new_row<KV, kFold>(p, w, kvh, HD, rs, &xs);
 
   // Q^T (B operand): column `col` = head kvh*G + col.
   typename T::QOp qb;
   {
     const bool ok = col < G;
     const int h = kvh * G + (ok ? col : 0);
-    if (p.rope_max_pos > 0) {
+    if (kFold || p.rope_max_pos > 0) {
       const bool pos_ok = w.pos >= 0 && w.pos < p.rope_max_pos;  // else q = 0, as rope_kv_write_kernel
       const int64_t tab = static_cast<int64_t>(pos_ok ? w.pos : 0) * (HD / 2);
-      const QRope<ACT> src{static_cast<const ACT*>(p.q) + static_cast<int64_t>(w.token) * p.rope_row_stride + h * HD,
-                           p.rope_bias ? p.rope_bias + h * HD : nullptr, p.rope_cos + tab, p.rope_sin + tab, HD / 2,
-                           p.rms_x != nullptr, rs};
+      const QRope<ACT, kFold> src{
+          static_cast<const ACT*>(p.q) + static_cast<int64_t>(w.token) * p.rope_row_stride + h * HD,
+          p.rope_bias ? p.rope_bias + h * HD : nullptr, p.rope_cos + tab, p.rope_sin + tab, HD / 2,
+          p.rms_x != nullptr, rs, &xs};
       T::load_q(qb, src, ok && pos_ok, grp);
     } else {
       const QRow<ACT> src{static_cast<const ACT*>(p.q) + (static_cast<int64_t>(w.token) * p.q_heads + h) * HD};
