@@ -545,6 +545,37 @@ def e2e_leg(which, layers=None):
                    layers=layers)
 
 
+def copy_floor():
+    """A plain copy of the same traffic as each attention workload's launch
+    (algorithmic bytes, half read and half written), 24 rotating buffer pairs
+    as the 24 layers' pools rotate, HIP events over 20 rounds."""
+    import torch
+    sizes = {"config2": 30345840, "config3": 26332552, "target": 134742784}
+    out = {"calibration": "device copy (torch copy_, bf16) with the traffic of one attention launch, "
+                          "24 rotating buffer pairs, HIP events over 20 x 24 launches", "sizes": {}}
+    for name, nbytes in sizes.items():
+        n = nbytes // 4  # bf16 elements read (and written): nbytes of traffic in all
+        xs = [torch.empty(n, dtype=torch.bfloat16, device="cuda").normal_() for _ in range(24)]
+        ys = [torch.empty_like(x) for x in xs]
+        for _ in range(3):
+            for x, y in zip(xs, ys):
+                y.copy_(x)
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record()
+        for _ in range(20):
+            for x, y in zip(xs, ys):
+                y.copy_(x)
+        t1.record()
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) * 1e3 / (20 * 24)
+        out["sizes"][name] = {"traffic_bytes": 4 * n, "us_per_launch": round(us, 3),
+                              "gbs": round(4 * n / us / 1e3, 1),
+                              "frac_of_8tbs": round(4 * n / us / 1e3 / HBM_PEAK_GBS, 4)}
+        del xs, ys
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -578,6 +609,11 @@ def main():
     ap.add_argument("--calibrate-stream", action="store_true",
                     help="only measure the read rate of a library reduction (torch sum) over 134 MB "
                          "buffers that no recent launch touched: the practical HBM read ceiling")
+    ap.add_argument("--calibrate-floor", action="store_true",
+                    help="only time a plain device copy (torch copy_) whose traffic equals each "
+                         "workload's algorithmic bytes per launch (half read, half written), over 24 "
+                         "rotating buffer pairs: what a launch of that size reaches with no gather, "
+                         "no compute and no merge")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
@@ -604,6 +640,9 @@ def main():
                                          "134217728-byte buffers, HIP events over 80 launches",
                           "bytes_per_launch": nbytes, "us_per_launch": round(us, 3),
                           "gbs": round(nbytes / us / 1e3, 1), "frac_of_8tbs": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}))
+        return
+    if args.calibrate_floor:
+        print(json.dumps(copy_floor()))
         return
     if args.calibrate_copy:
         import torch
