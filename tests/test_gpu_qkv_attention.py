@@ -94,20 +94,25 @@ def test_qkv_decode_against_oracle(gpu):
 
 @pytest.mark.parametrize("act", ["f32", "bf16"])
 @pytest.mark.parametrize("mixed", [False, True])
-def test_qkv_rms_folded_norm(gpu, act, mixed):
+@pytest.mark.parametrize("shape", [(896, 64, True), (5120, 128, False)],
+                         ids=["h896-hd64-kvbf16", "h5120-hd128-kvf32"])
+def test_qkv_rms_folded_norm(gpu, act, mixed, shape):
     """le_ragged_paged_attention_qkv_rms: the rows are the projection of the
     un-normalised residual stream x, and each row is scaled by
     r = 1/sqrt(mean(x^2) + eps) before its bias, on the in-launch decode path
     and on the rope/store path of a mixed step. Against the plain entry point
     on rows scaled by r on the host: with fp32 rows the two differ only by
     r's last bit; with bf16 rows by the one rounding the folded path saves
-    (the host's scaled rows are rounded before the bias is added)."""
+    (the host's scaled rows are rounded before the bias is added). Hidden
+    5120 is longer than the decode kernel holds in registers while its row
+    loads are in flight (4096 bf16 or 2048 fp32 elements): its other path."""
     from llm_engine_amd import kernels
     rng = np.random.default_rng(71 + mixed)
-    q_heads, kv_heads, head_dim, hidden, eps = 14, 2, 64, 896, 1e-6
+    hidden, head_dim, kv_bf16 = shape
+    q_heads, kv_heads, eps = 14, 2, 1e-6
     ctx, q_len = ([600, 33, 1200, 5], [70, 1, 1, 5]) if mixed else ([1, 17, 300, 1500, 64, 2049], None)
     case = make_case(ctx, q_len=q_len, q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim, seed=71,
-                     kv_bf16=True)
+                     kv_bf16=kv_bf16)
     n = len(case.token_pos)
     qd, kvd = q_heads * head_dim, kv_heads * head_dim
     tdt = TORCH_DT[act]
@@ -132,8 +137,8 @@ def test_qkv_rms_folded_norm(gpu, act, mixed):
     err = max_abs(g, w)
     kerr = max_abs(kc1.float().cpu(), kc2.float().cpu())
     verr = max_abs(vc1.float().cpu(), vc2.float().cpu())
-    print(f"qkv rms act={act} mixed={mixed}: max|out diff| {err:.2e}, cache diffs {kerr:.2e} {verr:.2e}")
-    # bf16 cache entries: one bf16 step of the largest written value at most
+    print(f"qkv rms act={act} mixed={mixed} shape={shape}: max|out diff| {err:.2e}, cache diffs {kerr:.2e} {verr:.2e}")
+    # cache entries: one bf16 step of the largest written value at most
     vmax = float(max(kc2.float().abs().max(), vc2.float().abs().max()))
     assert kerr <= vmax * 2 ** -7 and verr <= vmax * 2 ** -7
     assert err <= (2e-3 if act == "f32" else 3e-2)
