@@ -435,19 +435,20 @@ def phase_summary(mixed):
     def stat(x):
         return {"median": round(float(np.median(x)), 2), "max": round(float(x.max()), 2)}
 
-    for kind, kname in ((1, "decode"), (2, "chunk")):
-        k = t[t[:, 7] == kind]
+    for kinds, kname in (((1, 3), "decode"), ((2,), "chunk")):
+        k = t[np.isin(t[:, 7], kinds)]
         if not len(k):
             continue
+        rt = (k[:, 7] == 3).any()  # round-trip probe build (LE_TIMING_RT): slots 8 and 9 are its stamps
         us = (k[:, :5] - t0) / 100.0  # realtime counter: 100 MHz
         split = (k[:, 6] & 0xffffffff) > 0
         o = {"workgroups": int(len(k))}
         for i, name in enumerate(("start", "staged", "tiles_done", "written", "end")):
             o[name] = stat(us[:, i])
-        if kind == 1 and (k[:, 8] > 0).any():  # round-trip probe build (LE_TIMING_RT)
+        if rt:
             o["ids_back"] = stat((k[:, 8] - t0) / 100.0)
             o["first_tile_back"] = stat((k[:, 9] - t0) / 100.0)
-        if kind == 2:  # every wave's tiles done (slots 8-15; 0 for waves that never stamp)
+        else:  # every wave's tiles done (slots 8-15; 0 for waves that never stamp)
             w = k[:, 8:16]
             done = np.where(w > 0, w, 0).max(axis=1)
             o["tiles_done_all_waves"] = stat((done - t0) / 100.0)

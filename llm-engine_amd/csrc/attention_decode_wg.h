@@ -907,7 +907,11 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
   if (!w.valid) return;
   LE_TIM(0, t_start);
   LE_TIM(5, LE_TIM_PLACE());
+#ifdef LE_TIMING_RT
+  LE_TIM(7, 3);  // decode, slots 8 and 9 the round-trip probe's
+#else
   LE_TIM(7, 1);
+#endif
   LE_TIM(6, (static_cast<uint64_t>(w.b_end - w.b_begin) << 32) | static_cast<uint32_t>(w.part < 0 ? 0 : w.n_parts));
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -1048,6 +1052,9 @@ __device__ __forceinline__ void decode_wg(const DecodeParams& p, DecodeSmem<KV, 
 
   // ---- merge the four waves ----
   LE_TIM(2, LE_TIM_NOW());
+#ifndef LE_TIMING_RT
+  LE_TIM_WAVE(8, LE_TIM_NOW());  // every wave's tiles done (slots 8 + wave)
+#endif
   float l_tot = st.l + __shfl_xor(st.l, 16, kWave);
   l_tot += __shfl_xor(l_tot, 32, kWave);
   __syncthreads();  // V^T tiles are dead; reuse the LDS for the merge
