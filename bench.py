@@ -448,7 +448,7 @@ def phase_summary(mixed):
         if rt:
             o["ids_back"] = stat((k[:, 8] - t0) / 100.0)
             o["first_tile_back"] = stat((k[:, 9] - t0) / 100.0)
-        else:  # every wave's tiles done (slots 8-15; 0 for waves that never stamp)
+        elif (k[:, 8] > 0).any():  # every wave's tiles done (slots 8-15; 0 for waves that never stamp)
             w = k[:, 8:16]
             done = np.where(w > 0, w, 0).max(axis=1)
             o["tiles_done_all_waves"] = stat((done - t0) / 100.0)

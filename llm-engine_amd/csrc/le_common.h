@@ -321,7 +321,8 @@ namespace {
 // 5 HW_ID | XCC_ID << 32, 6 partition blocks << 32 | partitions of its row
 // (or tile), 7 kind (1 decode, 2 chunk, 3 decode in a round-trip probe
 // build, whose slots 8 and 9 hold the probe's stamps), 8 + w wave w's tiles
-// done (slot 2 is wave 0's). Chunk workgroups stamp 1 after their first
+// done (chunk workgroups and the mixed-step kernel's decode workgroups; slot
+// 2 is wave 0's). Chunk workgroups stamp 1 after their first
 // stage is in LDS and 2 after their last tile.
 #ifdef LE_TIMING
 constexpr int kTimSlots = 16;
