@@ -339,6 +339,47 @@ def test_bf16_folded_norms_match_unfused(gpu, arch):
     assert checked > 0
 
 
+@pytest.mark.parametrize("arch", ["qwen2.5-0.5b", "tinyllama-1.1b"])
+def test_bf16_decode_graph_matches_eager(gpu, arch):
+    """The bf16 model's decode steps replayed from captured HIP graphs (the
+    folded-norm decode attention, the SiLU kernel and the GEMMs in one graph,
+    fixed-layout plans) against the same model run eagerly, step for step on
+    one scheduler trace: the graph's partitions differ from the eager plan's,
+    which moves only roundings, so the greedy tokens agree wherever the eager
+    logits' top-2 margin exceeds 2 % of the logit scale (the bf16 model's own
+    error bar against the fp32 oracle is 5 %)."""
+    from e2e_util import top2_margin
+    from llm_engine_amd.engine import Model, Scheduler, sched_config, synthetic_weights
+    w = synthetic_weights(arch, 29, layers=3)
+    prompts = prompts_of(13, (70, 21, 300, 9, 150, 44), w.arch["vocab"])
+    graph = Model(w, 160, 16, dtype="bf16", kv_dtype="bf16", decode_graph=True)
+    eager = Model(w, 160, 16, dtype="bf16", kv_dtype="bf16")
+    sch = Scheduler(160, 16, sched_config(max_num_batched_tokens=256), fragment_blocks=10)
+    for i, p in enumerate(prompts):
+        sch.add(i, p, 12)
+    checked = decode_steps = 0
+    while sch.has_work():
+        sl = sch.step()
+        n = sum(int(s.needs_logits) for s in sl)
+        t_g, _ = graph.forward(sl, n)
+        t_e, lg = eager.forward(sl, n, want_logits=True)
+        if n and all(int(s.len) == 1 for s in sl):
+            decode_steps += 1
+        scale = float(np.abs(lg).max()) if n else 0.0
+        for r in range(n):
+            if top2_margin(lg[r]) > 0.02 * scale:
+                assert t_g[r] == t_e[r]
+                checked += 1
+        sch.done(t_e)  # both models continue from the eager tokens
+    replays, fallbacks = graph.graph_replays, graph.eager_fallbacks
+    graph.close()
+    eager.close()
+    print(f"{arch}: {decode_steps} decode steps, {replays} graph replays, {fallbacks} eager fallbacks, "
+          f"{checked} greedy tokens compared")
+    assert replays > 0 and fallbacks == 0
+    assert checked > 0
+
+
 @pytest.mark.parametrize("kv", ["f32", "bf16"])
 def test_config5_shared_prefix_preemption(gpu, kv):
     """Config 5 at a size the oracle finishes in seconds: 128 sequences share a
